@@ -1,0 +1,682 @@
+// Per-frame CFG decode engine: device state, weight binding, prefill,
+// whole-frame hipGraph capture and replay (GraphFrameEngine counterpart,
+// soraku_inference/acceleration/graph_frame.py:23-328).
+//
+// HBM layout (all FP32 unless the matrices are BF16):
+//   x, hidden, prefix, abuf, ybuf  [rows][d]       residual stream / depth state
+//   qkv                            [rows][(Hq+2Hkv) hd]
+//   attn                           [rows][Hq hd]
+//   act                            [rows][max(I, depth_inner)]
+//   logits                         [rows][V]
+//   K cache, V cache               [L][rows][Hkv][max_ctx][hd]
+//   rope cos/sin                   [max_ctx][hd/2]
+//   per-frame ring                 uniforms [F][n_utts][Q] f64, flags [F][2],
+//                                  forced/codes [F][n_utts][Q] i64
+// Row r = 2u is utterance u's cond row, 2u+1 its uncond row (cfg_rows = 2).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "sk_error.h"
+#include "sk_kernels.h"
+#include "sk_launch.h"
+#include "soraku_mi355x.h"
+
+using namespace sk;
+
+namespace {
+
+struct LayerW {
+  const void *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+  const void *gate = nullptr, *up = nullptr, *down = nullptr;
+  const float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+template <typename T>
+hipError_t dalloc(T** p, size_t n) {
+  return hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T) + 256);
+}
+
+}  // namespace
+
+struct sk_engine {
+  sk_config c{};
+  int rows = 0, G = 0, nqkv = 0, inner_max = 0, max_chunks = 0;
+  int device = 0;
+  hipStream_t stream = nullptr;
+
+  // weights (borrowed)
+  std::vector<LayerW> L;
+  const float* final_norm = nullptr;
+  const void* embed_tokens = nullptr;
+  const void* table = nullptr;
+  const float *d_norm_in = nullptr, *d_norm_out = nullptr, *d_bias = nullptr, *lang = nullptr;
+  const void *d_gate = nullptr, *d_up = nullptr, *d_down = nullptr;
+
+  // device buffers (owned)
+  float *x = nullptr, *hidden = nullptr, *prefix = nullptr, *abuf = nullptr, *ybuf = nullptr;
+  float *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+  float *kc = nullptr, *vc = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
+  float *part = nullptr, *dbg = nullptr, *embeds = nullptr;
+  int *counters = nullptr, *kv_len = nullptr, *pos = nullptr, *active = nullptr, *plen = nullptr;
+  int *fc = nullptr, *pf_t = nullptr, *flag_ring = nullptr;
+  double* u_ring = nullptr;
+  int64_t *forced_ring = nullptr, *codes_ring = nullptr, *stage_ids = nullptr, *stage_codes = nullptr;
+  SkParams* params = nullptr;
+
+  // host mirrors
+  int fc_host = 0;
+  bool prefilled = false;
+  std::vector<int> kv_host, len_host;
+  std::vector<char> staged;
+  SkParams p_host{};
+
+  hipGraph_t graph = nullptr, pf_graph = nullptr;
+  hipGraphExec_t exec = nullptr, pf_exec = nullptr;
+};
+
+namespace {
+
+size_t kv_layer_elems(const sk_engine* e) {
+  return (size_t)e->rows * e->c.n_kv_heads * e->c.max_ctx * e->c.head_dim;
+}
+
+void drop_graphs(sk_engine* e) {
+  if (e->exec) hipGraphExecDestroy(e->exec);
+  if (e->graph) hipGraphDestroy(e->graph);
+  if (e->pf_exec) hipGraphExecDestroy(e->pf_exec);
+  if (e->pf_graph) hipGraphDestroy(e->pf_graph);
+  e->exec = nullptr; e->graph = nullptr; e->pf_exec = nullptr; e->pf_graph = nullptr;
+}
+
+int validate_config(const sk_config* c) {
+  SK_CHECK(c != nullptr, SK_EINVAL, "config is NULL");
+  SK_CHECK(c->d_model > 0 && c->d_model % 8 == 0, SK_EINVAL, "d_model must be a positive multiple of 8");
+  SK_CHECK(c->n_layers > 0, SK_EINVAL, "n_layers must be positive");
+  SK_CHECK(c->n_q_heads > 0 && c->n_kv_heads > 0 && c->n_q_heads % c->n_kv_heads == 0, SK_EINVAL,
+           "n_q_heads must be a positive multiple of n_kv_heads");
+  const int hd = c->head_dim;
+  SK_CHECK(hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256 || hd == 512,
+           SK_EINVAL, "head_dim must be a power of two in [8, 512]");
+  SK_CHECK(c->trunk_inter > 0 && c->trunk_inter % 8 == 0, SK_EINVAL, "trunk_inter must be a positive multiple of 8");
+  SK_CHECK(c->depth_inner > 0 && c->depth_inner % 8 == 0, SK_EINVAL, "depth_inner must be a positive multiple of 8");
+  SK_CHECK(c->n_codebooks > 0 && c->n_codebooks <= 64, SK_EINVAL, "n_codebooks must be in [1, 64]");
+  SK_CHECK(c->audio_vocab > 3 && c->audio_vocab <= MAX_V, SK_EINVAL, "audio_vocab must be in [4, %d]", MAX_V);
+  SK_CHECK(c->text_vocab > 0, SK_EINVAL, "text_vocab must be positive");
+  SK_CHECK(c->bos_id >= 0 && c->bos_id < c->audio_vocab && c->eos_id >= 0 && c->eos_id < c->audio_vocab &&
+               c->pad_id >= 0 && c->pad_id < c->audio_vocab,
+           SK_EINVAL, "special ids must lie inside the audio vocabulary");
+  SK_CHECK(c->trunk_eps > 0.f && c->depth_eps > 0.f && c->rope_theta > 0.f, SK_EINVAL,
+           "eps and rope_theta must be positive");
+  SK_CHECK(c->weight_dtype == SK_F32 || c->weight_dtype == SK_BF16, SK_EINVAL, "weight_dtype must be SK_F32 or SK_BF16");
+  SK_CHECK(c->cfg_rows == 1 || c->cfg_rows == 2, SK_EINVAL, "cfg_rows must be 1 or 2");
+  SK_CHECK(c->n_utts >= 1 && c->n_utts * c->cfg_rows <= 4, SK_EINVAL,
+           "n_utts * cfg_rows must be in [1, 4] (decode rows)");
+  SK_CHECK(c->max_ctx >= 2 && c->max_ctx <= 65536, SK_EINVAL, "max_ctx must be in [2, 65536]");
+  SK_CHECK(c->max_frames >= 1, SK_EINVAL, "max_frames must be positive");
+  SK_CHECK(c->n_language == 0 || c->n_language == 4, SK_EINVAL, "n_language must be 0 or 4");
+  SK_CHECK((c->n_q_heads / c->n_kv_heads) * hd <= 4096, SK_EINVAL, "GQA group too large");
+  return SK_OK;
+}
+
+// FP32 RoPE angle inv_freq * pos, cos/sin evaluated in double and rounded once
+// (inv_freq as modeling_qwen3.py:116-122; cos/sin modeling_qwen3.py:126-137).
+void rope_tables(const sk_config& c, std::vector<float>& cs, std::vector<float>& sn) {
+  const int half = c.head_dim / 2;
+  std::vector<float> inv(half);
+  for (int i = 0; i < half; ++i) {
+    const float ex = (float)(2 * i) / (float)c.head_dim;
+    inv[i] = 1.0f / powf(c.rope_theta, ex);
+  }
+  cs.resize((size_t)c.max_ctx * half);
+  sn.resize((size_t)c.max_ctx * half);
+  for (int p = 0; p < c.max_ctx; ++p)
+    for (int i = 0; i < half; ++i) {
+      const float ang = (float)p * inv[i];
+      cs[(size_t)p * half + i] = (float)cos((double)ang);
+      sn[(size_t)p * half + i] = (float)sin((double)ang);
+    }
+}
+
+int check_decode_weights(const sk_engine* e) {
+  for (int i = 0; i < e->c.n_layers; ++i) {
+    const LayerW& w = e->L[i];
+    SK_CHECK(w.q && w.k && w.v && w.o && w.gate && w.up && w.down && w.in_norm && w.post_norm &&
+                 w.q_norm && w.k_norm,
+             SK_ENOWEIGHT, "trunk.layers.%d is not fully bound", i);
+  }
+  SK_CHECK(e->final_norm, SK_ENOWEIGHT, "trunk.norm.weight is not bound");
+  SK_CHECK(e->table, SK_ENOWEIGHT, "audio_codebooks.table is not bound");
+  SK_CHECK(e->d_norm_in && e->d_norm_out && e->d_bias && e->d_gate && e->d_up && e->d_down,
+           SK_ENOWEIGHT, "depth_head is not fully bound");
+  return SK_OK;
+}
+
+// ---- graph bodies -------------------------------------------------------
+
+hipError_t enqueue_trunk(sk_engine* e) {
+  const sk_config& c = e->c;
+  const int d = c.d_model, hd = c.head_dim, M = e->rows;
+  const int wt = c.weight_dtype;
+  hipError_t err;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerW& w = e->L[l];
+    GemvArgs a = gemv_args(w.q, e->nqkv, d, e->x, d, e->qkv, e->nqkv);
+    a.w[1] = w.k; a.w[2] = w.v;
+    a.seg_rows[0] = c.n_q_heads * hd; a.seg_rows[1] = c.n_kv_heads * hd; a.seg_rows[2] = c.n_kv_heads * hd;
+    a.norm_w = w.in_norm; a.eps = c.trunk_eps;
+    if ((err = launch_gemv<PRO_NORM, EPI_STORE>(wt, M, a, e->stream)) != hipSuccess) return err;
+
+    AttnArgs at{};
+    at.qkv = e->qkv; at.ldqkv = e->nqkv;
+    at.kc = e->kc + (size_t)l * kv_layer_elems(e);
+    at.vc = e->vc + (size_t)l * kv_layer_elems(e);
+    at.qn_w = w.q_norm; at.kn_w = w.k_norm; at.eps = c.trunk_eps;
+    at.rope_cos = e->rope_cos; at.rope_sin = e->rope_sin;
+    at.kv_len = e->kv_len; at.pos = e->pos; at.active = e->active;
+    at.part = e->part; at.counters = e->counters;
+    at.out = e->attn; at.ldo = c.n_q_heads * hd;
+    at.Hq = c.n_q_heads; at.Hkv = c.n_kv_heads; at.hd = hd; at.max_ctx = c.max_ctx;
+    at.max_chunks = e->max_chunks;
+    at.scale = 1.0f / sqrtf((float)hd);
+    const size_t asmem = ((size_t)e->G * hd + 2 * hd + (size_t)e->G * ATT_CHUNK + 2 * e->G) * sizeof(float);
+    hipLaunchKernelGGL(attention_kernel, dim3(e->max_chunks, c.n_kv_heads, M), dim3(NT), asmem,
+                       e->stream, at);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+
+    a = gemv_args(w.o, d, c.n_q_heads * hd, e->attn, c.n_q_heads * hd, e->x, d);
+    a.res = e->x; a.ldr = d;
+    if ((err = launch_gemv<PRO_NONE, EPI_RESID>(wt, M, a, e->stream)) != hipSuccess) return err;
+
+    a = gemv_args(w.gate, c.trunk_inter, d, e->x, d, e->act, e->inner_max);
+    a.w[1] = w.up; a.norm_w = w.post_norm; a.eps = c.trunk_eps;
+    if ((err = launch_gemv<PRO_NORM, EPI_SWIGLU>(wt, M, a, e->stream)) != hipSuccess) return err;
+
+    a = gemv_args(w.down, d, c.trunk_inter, e->act, e->inner_max, e->x, d);
+    a.res = e->x; a.ldr = d;
+    if ((err = launch_gemv<PRO_NONE, EPI_RESID>(wt, M, a, e->stream)) != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+hipError_t enqueue_frame(sk_engine* e) {
+  const sk_config& c = e->c;
+  const int d = c.d_model, M = e->rows, V = c.audio_vocab;
+  const int wt = c.weight_dtype;
+  const size_t tsz = (wt == SK_BF16) ? 2 : 4;
+  hipError_t err;
+  SampleArgs s{};
+  s.logits = e->logits; s.ldl = V; s.rows_per_utt = c.cfg_rows; s.V = V;
+  s.params = e->params; s.fc = e->fc;
+  s.u_ring = e->u_ring; s.flag_ring = e->flag_ring; s.forced_ring = e->forced_ring;
+  s.codes_ring = e->codes_ring; s.dbg = e->dbg; s.table = e->table;
+  s.prefix = e->prefix; s.xnext = e->x; s.d = d; s.Q = c.n_codebooks; s.scale = c.frame_scale;
+  s.bos = c.bos_id; s.eos = c.eos_id; s.pad = c.pad_id; s.n_utts = c.n_utts;
+  for (int q = 0; q < c.n_codebooks; ++q) {
+    GemvArgs a = gemv_args(e->d_gate, c.depth_inner, d, e->hidden, d, e->act, e->inner_max);
+    a.w[1] = e->d_up; a.x2 = e->prefix; a.ldx2 = d;
+    a.norm_w = e->d_norm_in; a.eps = c.depth_eps; a.norm_out = e->abuf; a.ldno = d;
+    if ((err = launch_gemv<PRO_ADDNORM, EPI_SWIGLU>(wt, M, a, e->stream)) != hipSuccess) return err;
+
+    a = gemv_args(e->d_down, d, c.depth_inner, e->act, e->inner_max, e->ybuf, d);
+    a.res = e->abuf; a.ldr = d;
+    if ((err = launch_gemv<PRO_NONE, EPI_RESID>(wt, M, a, e->stream)) != hipSuccess) return err;
+
+    const void* tq = static_cast<const char*>(e->table) + (size_t)q * V * d * tsz;
+    a = gemv_args(tq, V, d, e->ybuf, d, e->logits, V);
+    a.norm_w = e->d_norm_out; a.eps = c.depth_eps; a.bias = e->d_bias + (size_t)q * V;
+    if ((err = launch_gemv<PRO_NORM, EPI_BIAS>(wt, M, a, e->stream)) != hipSuccess) return err;
+
+    if (wt == SK_BF16)
+      hipLaunchKernelGGL(sample_step_kernel<WBF16>, dim3(c.n_utts), dim3(NT), SAMPLE_SMEM, e->stream, s, q);
+    else
+      hipLaunchKernelGGL(sample_step_kernel<WF32>, dim3(c.n_utts), dim3(NT), SAMPLE_SMEM, e->stream, s, q);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  if ((err = enqueue_trunk(e)) != hipSuccess) return err;
+  hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x, e->final_norm,
+                     c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->fc);
+  return hipGetLastError();
+}
+
+hipError_t enqueue_prefill_step(sk_engine* e) {
+  const sk_config& c = e->c;
+  hipLaunchKernelGGL(prefill_load_kernel, dim3(e->rows), dim3(NT), 0, e->stream, e->embeds,
+                     c.max_ctx, e->plen, e->pf_t, c.d_model, e->x, e->active);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  if ((err = enqueue_trunk(e)) != hipSuccess) return err;
+  hipLaunchKernelGGL(final_norm_kernel, dim3(e->rows), dim3(NT), 0, e->stream, e->x, e->final_norm,
+                     c.trunk_eps, c.d_model, e->hidden, e->kv_len, e->pos, e->active, e->pf_t);
+  return hipGetLastError();
+}
+
+int capture(sk_engine* e, hipError_t (*body)(sk_engine*), hipGraph_t* g, hipGraphExec_t* x) {
+  SK_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+  const hipError_t err = body(e);
+  hipGraph_t graph = nullptr;
+  const hipError_t end = hipStreamEndCapture(e->stream, &graph);
+  if (err != hipSuccess) {
+    if (graph) hipGraphDestroy(graph);
+    return fail(SK_EHIP, "kernel launch during capture failed: %s", hipGetErrorString(err));
+  }
+  SK_CHECK(end == hipSuccess, SK_EHIP, "hipStreamEndCapture failed: %s", hipGetErrorString(end));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t ins = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (ins != hipSuccess) {
+    hipGraphDestroy(graph);
+    return fail(SK_EHIP, "hipGraphInstantiate failed: %s", hipGetErrorString(ins));
+  }
+  *g = graph;
+  *x = exec;
+  return SK_OK;
+}
+
+bool parse_layer(const char* key, int* layer, const char** rest) {
+  const char* pre = "trunk.layers.";
+  const size_t n = strlen(pre);
+  if (strncmp(key, pre, n) != 0) return false;
+  const char* p = key + n;
+  if (*p < '0' || *p > '9') return false;
+  int v = 0;
+  while (*p >= '0' && *p <= '9') { v = v * 10 + (*p - '0'); ++p; if (v > 100000) return false; }
+  if (*p != '.') return false;
+  *layer = v;
+  *rest = p + 1;
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sk_last_error(void) { return last_error().c_str(); }
+
+int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
+  SK_CHECK(out != nullptr, SK_EINVAL, "out is NULL");
+  *out = nullptr;
+  int rc = validate_config(cfg);
+  if (rc != SK_OK) return rc;
+  sk_engine* e = new sk_engine();
+  e->c = *cfg;
+  const sk_config& c = e->c;
+  e->rows = c.n_utts * c.cfg_rows;
+  e->G = c.n_q_heads / c.n_kv_heads;
+  e->nqkv = (c.n_q_heads + 2 * c.n_kv_heads) * c.head_dim;
+  e->inner_max = c.trunk_inter > c.depth_inner ? c.trunk_inter : c.depth_inner;
+  e->max_chunks = (c.max_ctx + ATT_CHUNK - 1) / ATT_CHUNK;
+  e->L.resize(c.n_layers);
+  e->kv_host.assign(e->rows, 0);
+  e->len_host.assign(e->rows, 0);
+  e->staged.assign(e->rows, 0);
+  auto bail = [&](int code) { sk_destroy(e); return code; };
+#define ALLOC(ptr, n)                                                                   \
+  do {                                                                                  \
+    const hipError_t _a = dalloc(&(ptr), (n));                                          \
+    if (_a != hipSuccess) {                                                             \
+      fail(SK_EHIP, "hipMalloc(%s) failed: %s", #ptr, hipGetErrorString(_a));           \
+      return bail(SK_EHIP);                                                             \
+    }                                                                                   \
+  } while (0)
+  if (hipGetDevice(&e->device) != hipSuccess) { fail(SK_EHIP, "no HIP device"); return bail(SK_EHIP); }
+  if (hip_stream) {
+    const hipError_t se = hipStreamSynchronize(static_cast<hipStream_t>(hip_stream));
+    if (se != hipSuccess) { fail(SK_EHIP, "caller stream: %s", hipGetErrorString(se)); return bail(SK_EHIP); }
+  }
+  if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess) {
+    fail(SK_EHIP, "hipStreamCreateWithFlags failed");
+    return bail(SK_EHIP);
+  }
+  const size_t R = e->rows, d = c.d_model, Q = c.n_codebooks, V = c.audio_vocab;
+  ALLOC(e->x, R * d); ALLOC(e->hidden, R * d); ALLOC(e->prefix, R * d);
+  ALLOC(e->abuf, R * d); ALLOC(e->ybuf, R * d);
+  ALLOC(e->qkv, R * e->nqkv); ALLOC(e->attn, R * c.n_q_heads * c.head_dim);
+  ALLOC(e->act, R * e->inner_max); ALLOC(e->logits, R * V);
+  ALLOC(e->kc, (size_t)c.n_layers * kv_layer_elems(e));
+  ALLOC(e->vc, (size_t)c.n_layers * kv_layer_elems(e));
+  ALLOC(e->rope_cos, (size_t)c.max_ctx * c.head_dim / 2);
+  ALLOC(e->rope_sin, (size_t)c.max_ctx * c.head_dim / 2);
+  ALLOC(e->part, R * c.n_q_heads * e->max_chunks * (c.head_dim + 2));
+  ALLOC(e->counters, R * c.n_kv_heads);
+  ALLOC(e->kv_len, R); ALLOC(e->pos, R); ALLOC(e->active, R); ALLOC(e->plen, R);
+  ALLOC(e->fc, 1); ALLOC(e->pf_t, 1);
+  ALLOC(e->u_ring, (size_t)c.max_frames * c.n_utts * Q);
+  ALLOC(e->flag_ring, (size_t)c.max_frames * 2);
+  ALLOC(e->forced_ring, (size_t)c.max_frames * c.n_utts * Q);
+  ALLOC(e->codes_ring, (size_t)c.max_frames * c.n_utts * Q);
+  ALLOC(e->dbg, (size_t)c.n_utts * Q * V);
+  ALLOC(e->embeds, R * c.max_ctx * d);
+  ALLOC(e->stage_ids, (size_t)c.max_ctx);
+  ALLOC(e->stage_codes, (size_t)c.max_ctx * Q);
+  ALLOC(e->params, 1);
+#undef ALLOC
+  std::vector<float> cs, sn;
+  rope_tables(c, cs, sn);
+  hipError_t he = hipMemcpy(e->rope_cos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice);
+  if (he == hipSuccess) he = hipMemcpy(e->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice);
+  if (he == hipSuccess) he = hipMemset(e->counters, 0, R * c.n_kv_heads * sizeof(int));
+  if (he == hipSuccess) he = hipMemset(e->x, 0, R * d * sizeof(float));
+  if (he == hipSuccess) he = hipMemset(e->prefix, 0, R * d * sizeof(float));
+  if (he == hipSuccess) he = hipMemset(e->kv_len, 0, R * sizeof(int));
+  if (he == hipSuccess) he = hipMemset(e->pos, 0, R * sizeof(int));
+  if (he == hipSuccess) he = hipMemset(e->fc, 0, sizeof(int));
+  if (he == hipSuccess) he = hipMemset(e->flag_ring, 0, (size_t)c.max_frames * 2 * sizeof(int));
+  if (he == hipSuccess) he = hipMemset(e->u_ring, 0, (size_t)c.max_frames * c.n_utts * Q * sizeof(double));
+  e->p_host.cfg_scale = 1.0f;
+  e->p_host.temperature = 0.0f;
+  if (he == hipSuccess) he = hipMemcpy(e->params, &e->p_host, sizeof(SkParams), hipMemcpyHostToDevice);
+  if (he == hipSuccess) he = prepare_sampler();
+  if (he != hipSuccess) { fail(SK_EHIP, "engine init: %s", hipGetErrorString(he)); return bail(SK_EHIP); }
+  *out = e;
+  return SK_OK;
+}
+
+int sk_destroy(sk_engine* e) {
+  if (!e) return SK_OK;
+  if (e->stream) hipStreamSynchronize(e->stream);
+  drop_graphs(e);
+  void* bufs[] = {e->x, e->hidden, e->prefix, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
+                  e->kc, e->vc, e->rope_cos, e->rope_sin, e->part, e->dbg, e->embeds, e->counters,
+                  e->kv_len, e->pos, e->active, e->plen, e->fc, e->pf_t, e->flag_ring, e->u_ring,
+                  e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
+  for (void* p : bufs)
+    if (p) hipFree(p);
+  if (e->stream) hipStreamDestroy(e->stream);
+  delete e;
+  return SK_OK;
+}
+
+int sk_bind_weight(sk_engine* e, const char* key, const void* dev_ptr, int32_t dtype,
+                   const int64_t* shape, int32_t ndim) {
+  SK_CHECK(e && key && shape, SK_EINVAL, "engine, key and shape must be non-NULL");
+  SK_CHECK(dev_ptr != nullptr, SK_EINVAL, "%s: device pointer is NULL", key);
+  SK_CHECK(((uintptr_t)dev_ptr & 15) == 0, SK_EINVAL, "%s: device pointer must be 16-byte aligned", key);
+  const sk_config& c = e->c;
+  const int64_t d = c.d_model, hd = c.head_dim, wt = c.weight_dtype;
+  auto want = [&](std::initializer_list<int64_t> dims, int32_t dt) -> int {
+    SK_CHECK(dtype == dt, SK_EINVAL, "%s: dtype %d, expected %d", key, dtype, dt);
+    SK_CHECK(ndim == (int32_t)dims.size(), SK_EINVAL, "%s: ndim %d, expected %d", key, ndim, (int)dims.size());
+    int i = 0;
+    for (int64_t v : dims) {
+      SK_CHECK(shape[i] == v, SK_EINVAL, "%s: dim %d is %lld, expected %lld", key, i,
+               (long long)shape[i], (long long)v);
+      ++i;
+    }
+    return SK_OK;
+  };
+  int rc = SK_OK;
+  int layer = -1;
+  const char* rest = nullptr;
+  if (parse_layer(key, &layer, &rest)) {
+    SK_CHECK(layer < c.n_layers, SK_EINVAL, "%s: layer index out of range", key);
+    LayerW& w = e->L[layer];
+    const std::string r(rest);
+    if (r == "input_layernorm.weight") { if (!(rc = want({d}, SK_F32))) w.in_norm = (const float*)dev_ptr; }
+    else if (r == "post_attention_layernorm.weight") { if (!(rc = want({d}, SK_F32))) w.post_norm = (const float*)dev_ptr; }
+    else if (r == "self_attn.q_norm.weight") { if (!(rc = want({hd}, SK_F32))) w.q_norm = (const float*)dev_ptr; }
+    else if (r == "self_attn.k_norm.weight") { if (!(rc = want({hd}, SK_F32))) w.k_norm = (const float*)dev_ptr; }
+    else if (r == "self_attn.q_proj.weight") { if (!(rc = want({c.n_q_heads * hd, d}, wt))) w.q = dev_ptr; }
+    else if (r == "self_attn.k_proj.weight") { if (!(rc = want({c.n_kv_heads * hd, d}, wt))) w.k = dev_ptr; }
+    else if (r == "self_attn.v_proj.weight") { if (!(rc = want({c.n_kv_heads * hd, d}, wt))) w.v = dev_ptr; }
+    else if (r == "self_attn.o_proj.weight") { if (!(rc = want({d, c.n_q_heads * hd}, wt))) w.o = dev_ptr; }
+    else if (r == "mlp.gate_proj.weight") { if (!(rc = want({c.trunk_inter, d}, wt))) w.gate = dev_ptr; }
+    else if (r == "mlp.up_proj.weight") { if (!(rc = want({c.trunk_inter, d}, wt))) w.up = dev_ptr; }
+    else if (r == "mlp.down_proj.weight") { if (!(rc = want({d, c.trunk_inter}, wt))) w.down = dev_ptr; }
+    else return fail(SK_EINVAL, "unknown weight key %s", key);
+  } else {
+    const std::string k(key);
+    if (k == "trunk.norm.weight") { if (!(rc = want({d}, SK_F32))) e->final_norm = (const float*)dev_ptr; }
+    else if (k == "trunk.embed_tokens.weight") { if (!(rc = want({c.text_vocab, d}, wt))) e->embed_tokens = dev_ptr; }
+    else if (k == "audio_codebooks.table") { if (!(rc = want({c.n_codebooks, c.audio_vocab, d}, wt))) e->table = dev_ptr; }
+    else if (k == "depth_head.norm_in.weight") { if (!(rc = want({d}, SK_F32))) e->d_norm_in = (const float*)dev_ptr; }
+    else if (k == "depth_head.norm_out.weight") { if (!(rc = want({d}, SK_F32))) e->d_norm_out = (const float*)dev_ptr; }
+    else if (k == "depth_head.mlp.gate_proj.weight") { if (!(rc = want({c.depth_inner, d}, wt))) e->d_gate = dev_ptr; }
+    else if (k == "depth_head.mlp.up_proj.weight") { if (!(rc = want({c.depth_inner, d}, wt))) e->d_up = dev_ptr; }
+    else if (k == "depth_head.mlp.down_proj.weight") { if (!(rc = want({d, c.depth_inner}, wt))) e->d_down = dev_ptr; }
+    else if (k == "depth_head.bias") { if (!(rc = want({c.n_codebooks, c.audio_vocab}, SK_F32))) e->d_bias = (const float*)dev_ptr; }
+    else if (k == "language_embeddings.weight") {
+      SK_CHECK(c.n_language == 4, SK_EINVAL, "language_embeddings.weight bound but n_language is 0");
+      if (!(rc = want({4, d}, SK_F32))) e->lang = (const float*)dev_ptr;
+    } else return fail(SK_EINVAL, "unknown weight key %s", key);
+  }
+  if (rc == SK_OK) drop_graphs(e);  // captured graphs hold the old addresses
+  return rc;
+}
+
+int sk_prefill_row(sk_engine* e, int32_t row, const int64_t* text_ids, int32_t n_text,
+                   const int64_t* frame_codes, int32_t n_frames) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  const sk_config& c = e->c;
+  SK_CHECK(row >= 0 && row < e->rows, SK_EINVAL, "row %d out of range [0, %d)", row, e->rows);
+  SK_CHECK(n_text >= 0 && n_frames >= 0 && n_text + n_frames >= 1, SK_EINVAL, "empty prefix");
+  SK_CHECK(n_text == 0 || text_ids, SK_EINVAL, "text_ids is NULL");
+  SK_CHECK(n_frames == 0 || frame_codes, SK_EINVAL, "frame_codes is NULL");
+  SK_CHECK(n_text + n_frames < c.max_ctx, SK_EKVFULL, "prefix of %d tokens does not fit max_ctx=%d",
+           n_text + n_frames, c.max_ctx);
+  for (int i = 0; i < n_text; ++i)
+    SK_CHECK(text_ids[i] >= 0 && text_ids[i] < c.text_vocab, SK_EINVAL, "text id %lld out of range",
+             (long long)text_ids[i]);
+  for (int i = 0; i < n_frames * c.n_codebooks; ++i)
+    SK_CHECK(frame_codes[i] >= 0 && frame_codes[i] < c.audio_vocab, SK_EINVAL, "frame code %lld out of range",
+             (long long)frame_codes[i]);
+  SK_CHECK(n_text == 0 || e->embed_tokens, SK_ENOWEIGHT, "trunk.embed_tokens.weight is not bound");
+  SK_CHECK(n_frames == 0 || e->table, SK_ENOWEIGHT, "audio_codebooks.table is not bound");
+  SK_CHECK(c.n_language == 0 || n_text == 0 || e->lang, SK_ENOWEIGHT, "language_embeddings.weight is not bound");
+  if (n_text) SK_HIP(hipMemcpyAsync(e->stage_ids, text_ids, n_text * sizeof(int64_t), hipMemcpyHostToDevice, e->stream));
+  if (n_frames)
+    SK_HIP(hipMemcpyAsync(e->stage_codes, frame_codes, (size_t)n_frames * c.n_codebooks * sizeof(int64_t),
+                          hipMemcpyHostToDevice, e->stream));
+  float* dst = e->embeds + (size_t)row * c.max_ctx * c.d_model;
+  const int n = n_text + n_frames;
+  if (c.weight_dtype == SK_BF16)
+    hipLaunchKernelGGL(embed_prefix_kernel<WBF16>, dim3(n), dim3(NT), 0, e->stream, e->stage_ids, n_text,
+                       e->stage_codes, e->embed_tokens, e->lang, c.n_language, c.language_ids[0],
+                       c.language_ids[1], c.language_ids[2], c.language_ids[3], e->table, c.n_codebooks,
+                       c.audio_vocab, c.d_model, c.frame_scale, dst);
+  else
+    hipLaunchKernelGGL(embed_prefix_kernel<WF32>, dim3(n), dim3(NT), 0, e->stream, e->stage_ids, n_text,
+                       e->stage_codes, e->embed_tokens, e->lang, c.n_language, c.language_ids[0],
+                       c.language_ids[1], c.language_ids[2], c.language_ids[3], e->table, c.n_codebooks,
+                       c.audio_vocab, c.d_model, c.frame_scale, dst);
+  SK_HIP(hipGetLastError());
+  SK_HIP(hipStreamSynchronize(e->stream));
+  e->len_host[row] = n;
+  e->staged[row] = 1;
+  e->prefilled = false;
+  return SK_OK;
+}
+
+int sk_prefill_run(sk_engine* e) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  for (int r = 0; r < e->rows; ++r) SK_CHECK(e->staged[r], SK_ESTATE, "row %d has no staged prefix", r);
+  int rc = check_decode_weights(e);
+  if (rc != SK_OK) return rc;
+  const int R = e->rows;
+  std::vector<int> zeros(R, 0);
+  SK_HIP(hipMemcpyAsync(e->plen, e->len_host.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->kv_len, zeros.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->pos, zeros.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemsetAsync(e->pf_t, 0, sizeof(int), e->stream));
+  SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
+  SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
+  SK_HIP(hipStreamSynchronize(e->stream));
+  if (!e->pf_exec) {
+    rc = capture(e, enqueue_prefill_step, &e->pf_graph, &e->pf_exec);
+    if (rc != SK_OK) return rc;
+  }
+  int longest = 0;
+  for (int r = 0; r < R; ++r) longest = e->len_host[r] > longest ? e->len_host[r] : longest;
+  for (int t = 0; t < longest; ++t) SK_HIP(hipGraphLaunch(e->pf_exec, e->stream));
+  std::vector<int> ones(R, 1);
+  SK_HIP(hipMemcpyAsync(e->active, ones.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipStreamSynchronize(e->stream));
+  for (int r = 0; r < R; ++r) { e->kv_host[r] = e->len_host[r]; e->staged[r] = 0; }
+  e->fc_host = 0;
+  e->prefilled = true;
+  return SK_OK;
+}
+
+int sk_set_row_state(sk_engine* e, int32_t row, int32_t kv_len, int32_t position) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  SK_CHECK(row >= 0 && row < e->rows, SK_EINVAL, "row %d out of range", row);
+  SK_CHECK(kv_len >= 0 && kv_len < e->c.max_ctx, SK_EKVFULL, "kv_len %d outside [0, max_ctx)", kv_len);
+  SK_CHECK(position >= 0 && position < e->c.max_ctx, SK_EINVAL, "position %d outside [0, max_ctx)", position);
+  SK_HIP(hipMemcpy(e->kv_len + row, &kv_len, sizeof(int), hipMemcpyHostToDevice));
+  SK_HIP(hipMemcpy(e->pos + row, &position, sizeof(int), hipMemcpyHostToDevice));
+  const int one = 1;
+  SK_HIP(hipMemcpy(e->active + row, &one, sizeof(int), hipMemcpyHostToDevice));
+  e->kv_host[row] = kv_len;
+  return SK_OK;
+}
+
+int sk_kv_ptr(sk_engine* e, int32_t layer, int32_t kv, void** out) {
+  SK_CHECK(e && out, SK_EINVAL, "engine and out must be non-NULL");
+  SK_CHECK(layer >= 0 && layer < e->c.n_layers, SK_EINVAL, "layer out of range");
+  SK_CHECK(kv == 0 || kv == 1, SK_EINVAL, "kv must be 0 (K) or 1 (V)");
+  *out = (kv ? e->vc : e->kc) + (size_t)layer * kv_layer_elems(e);
+  return SK_OK;
+}
+
+int sk_get_hidden(sk_engine* e, float* host_out) {
+  SK_CHECK(e && host_out, SK_EINVAL, "engine and host_out must be non-NULL");
+  SK_HIP(hipStreamSynchronize(e->stream));
+  SK_HIP(hipMemcpy(host_out, e->hidden, (size_t)e->rows * e->c.d_model * sizeof(float), hipMemcpyDeviceToHost));
+  return SK_OK;
+}
+
+int sk_set_sampling(sk_engine* e, float cfg_scale, float temperature, int32_t top_k, float top_p,
+                    int32_t has_q0, float temperature_q0, int32_t top_k_q0, float top_p_q0) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  SK_CHECK(isfinite(cfg_scale) && isfinite(temperature) && isfinite(top_p), SK_EINVAL, "non-finite sampling parameter");
+  SK_CHECK(!has_q0 || (isfinite(temperature_q0) && isfinite(top_p_q0)), SK_EINVAL, "non-finite q0 parameter");
+  SK_CHECK(e->c.cfg_rows == 2 || cfg_scale == 1.0f, SK_EINVAL, "cfg_scale != 1 needs cfg_rows == 2");
+  SkParams p = e->p_host;
+  p.cfg_scale = cfg_scale;
+  p.temperature = temperature; p.top_k = top_k; p.top_p = top_p;
+  p.has_q0 = has_q0 ? 1 : 0;
+  p.temperature_q0 = has_q0 ? temperature_q0 : temperature;
+  p.top_k_q0 = has_q0 ? top_k_q0 : top_k;
+  p.top_p_q0 = has_q0 ? top_p_q0 : top_p;
+  SK_HIP(hipStreamSynchronize(e->stream));
+  SK_HIP(hipMemcpy(e->params, &p, sizeof(SkParams), hipMemcpyHostToDevice));
+  e->p_host = p;
+  return SK_OK;
+}
+
+int sk_set_debug(sk_engine* e, int32_t record_logits) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  SkParams p = e->p_host;
+  p.record_logits = record_logits ? 1 : 0;
+  SK_HIP(hipStreamSynchronize(e->stream));
+  SK_HIP(hipMemcpy(e->params, &p, sizeof(SkParams), hipMemcpyHostToDevice));
+  e->p_host = p;
+  return SK_OK;
+}
+
+int sk_capture(sk_engine* e) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  int rc = check_decode_weights(e);
+  if (rc != SK_OK) return rc;
+  if (e->exec) return SK_OK;
+  SK_HIP(hipStreamSynchronize(e->stream));
+  return capture(e, enqueue_frame, &e->graph, &e->exec);
+}
+
+static int check_step(sk_engine* e, int n) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  SK_CHECK(e->exec != nullptr, SK_ENOCAPTURE, "step before capture");
+  SK_CHECK(e->prefilled, SK_ESTATE, "step before prefill");
+  SK_CHECK(n >= 1, SK_EINVAL, "frame count must be positive");
+  SK_CHECK(e->fc_host + n <= e->c.max_frames, SK_EKVFULL, "frame ring full (max_frames=%d)", e->c.max_frames);
+  for (int r = 0; r < e->rows; ++r)
+    SK_CHECK(e->kv_host[r] + n <= e->c.max_ctx, SK_EKVFULL, "KV cache full on row %d (max_ctx=%d)", r, e->c.max_ctx);
+  return SK_OK;
+}
+
+int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
+                  const int64_t* forced_codes, int64_t* codes_out, float* logits_dbg) {
+  int rc = check_step(e, 1);
+  if (rc != SK_OK) return rc;
+  SK_CHECK(codes_out != nullptr, SK_EINVAL, "codes_out is NULL");
+  SK_CHECK(!logits_dbg || e->p_host.record_logits, SK_ESTATE, "logits_dbg needs sk_set_debug(e, 1)");
+  const sk_config& c = e->c;
+  const size_t nq = (size_t)c.n_utts * c.n_codebooks;
+  if (uniforms)
+    for (size_t i = 0; i < nq; ++i)
+      SK_CHECK(uniforms[i] >= 0.0 && uniforms[i] < 1.0, SK_EINVAL, "uniform %zu outside [0,1)", i);
+  if (forced_codes)
+    for (size_t i = 0; i < nq; ++i)
+      SK_CHECK(forced_codes[i] >= 0 && forced_codes[i] < c.audio_vocab, SK_EINVAL, "forced code out of range");
+  const int slot = e->fc_host;
+  std::vector<double> u(nq, 0.0);
+  if (uniforms) memcpy(u.data(), uniforms, nq * sizeof(double));
+  const int flags[2] = {mask_eos_q0 ? 1 : 0, forced_codes ? 1 : 0};
+  SK_HIP(hipMemcpyAsync(e->u_ring + slot * nq, u.data(), nq * sizeof(double), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->flag_ring + 2 * slot, flags, sizeof(flags), hipMemcpyHostToDevice, e->stream));
+  if (forced_codes)
+    SK_HIP(hipMemcpyAsync(e->forced_ring + slot * nq, forced_codes, nq * sizeof(int64_t), hipMemcpyHostToDevice,
+                          e->stream));
+  SK_HIP(hipGraphLaunch(e->exec, e->stream));
+  SK_HIP(hipMemcpyAsync(codes_out, e->codes_ring + slot * nq, nq * sizeof(int64_t), hipMemcpyDeviceToHost, e->stream));
+  if (logits_dbg)
+    SK_HIP(hipMemcpyAsync(logits_dbg, e->dbg, nq * c.audio_vocab * sizeof(float), hipMemcpyDeviceToHost, e->stream));
+  SK_HIP(hipStreamSynchronize(e->stream));
+  e->fc_host += 1;
+  for (int r = 0; r < e->rows; ++r) e->kv_host[r] += 1;
+  return SK_OK;
+}
+
+int sk_queue_frames(sk_engine* e, int32_t n, const double* uniforms, const int32_t* mask_eos_q0) {
+  int rc = check_step(e, n);
+  if (rc != SK_OK) return rc;
+  const sk_config& c = e->c;
+  const size_t nq = (size_t)c.n_utts * c.n_codebooks;
+  std::vector<double> u((size_t)n * nq, 0.0);
+  if (uniforms) {
+    for (size_t i = 0; i < u.size(); ++i)
+      SK_CHECK(uniforms[i] >= 0.0 && uniforms[i] < 1.0, SK_EINVAL, "uniform %zu outside [0,1)", i);
+    memcpy(u.data(), uniforms, u.size() * sizeof(double));
+  }
+  std::vector<int> flags((size_t)2 * n, 0);
+  for (int i = 0; i < n; ++i) flags[2 * i] = mask_eos_q0 ? (mask_eos_q0[i] ? 1 : 0) : 0;
+  SK_HIP(hipStreamSynchronize(e->stream));
+  SK_HIP(hipMemcpy(e->u_ring + (size_t)e->fc_host * nq, u.data(), u.size() * sizeof(double), hipMemcpyHostToDevice));
+  SK_HIP(hipMemcpy(e->flag_ring + 2 * (size_t)e->fc_host, flags.data(), flags.size() * sizeof(int),
+                   hipMemcpyHostToDevice));
+  return SK_OK;
+}
+
+int sk_replay(sk_engine* e, int32_t n) {
+  int rc = check_step(e, n);
+  if (rc != SK_OK) return rc;
+  for (int i = 0; i < n; ++i) SK_HIP(hipGraphLaunch(e->exec, e->stream));
+  e->fc_host += n;
+  for (int r = 0; r < e->rows; ++r) e->kv_host[r] += n;
+  return SK_OK;
+}
+
+int sk_read_codes(sk_engine* e, int32_t n, int64_t* codes_out) {
+  SK_CHECK(e && codes_out, SK_EINVAL, "engine and codes_out must be non-NULL");
+  SK_CHECK(n >= 1 && n <= e->fc_host, SK_EINVAL, "only %d frames were decoded", e->fc_host);
+  const size_t nq = (size_t)e->c.n_utts * e->c.n_codebooks;
+  SK_HIP(hipStreamSynchronize(e->stream));
+  SK_HIP(hipMemcpy(codes_out, e->codes_ring + (size_t)(e->fc_host - n) * nq, (size_t)n * nq * sizeof(int64_t),
+                   hipMemcpyDeviceToHost));
+  return SK_OK;
+}
+
+int sk_synchronize(sk_engine* e) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  SK_HIP(hipStreamSynchronize(e->stream));
+  return SK_OK;
+}
+
+void* sk_stream(sk_engine* e) { return e ? (void*)e->stream : nullptr; }
+
+int32_t sk_frames_done(sk_engine* e) { return e ? e->fc_host : -1; }
+
+}  // extern "C"

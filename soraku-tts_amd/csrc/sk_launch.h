@@ -1,0 +1,72 @@
+// Host-side launch helpers shared by the engine and the operator API.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "sk_kernels.h"
+#include "soraku_mi355x.h"
+
+namespace sk {
+
+template <int M, int RPW, int PRO, int EPI, typename WL>
+static hipError_t launch_gemv_t(const GemvArgs& a, hipStream_t st) {
+  constexpr int rows_per_block = WAVES * RPW;
+  const int grid = (a.N + rows_per_block - 1) / rows_per_block;
+  const size_t smem = (size_t)M * a.K * sizeof(float);
+  auto fn = gemv_kernel<M, RPW, PRO, EPI, WL>;
+  if (smem > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(NT), smem, st, a);
+  return hipGetLastError();
+}
+
+// Rows per wave: 2 when that still yields >= 512 workgroups, else 1, so every
+// GEMV of the decode step spreads over all 256 CUs.
+template <int PRO, int EPI, typename WL>
+static hipError_t launch_gemv_m(int M, const GemvArgs& a, hipStream_t st) {
+  const bool wide = (a.N / (WAVES * 2)) >= 512;
+  switch (M) {
+    case 1: return wide ? launch_gemv_t<1, 2, PRO, EPI, WL>(a, st) : launch_gemv_t<1, 1, PRO, EPI, WL>(a, st);
+    case 2: return wide ? launch_gemv_t<2, 2, PRO, EPI, WL>(a, st) : launch_gemv_t<2, 1, PRO, EPI, WL>(a, st);
+    case 3: return wide ? launch_gemv_t<3, 2, PRO, EPI, WL>(a, st) : launch_gemv_t<3, 1, PRO, EPI, WL>(a, st);
+    case 4: return wide ? launch_gemv_t<4, 2, PRO, EPI, WL>(a, st) : launch_gemv_t<4, 1, PRO, EPI, WL>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int PRO, int EPI>
+static hipError_t launch_gemv(int wdtype, int M, const GemvArgs& a, hipStream_t st) {
+  return wdtype == SK_BF16 ? launch_gemv_m<PRO, EPI, WBF16>(M, a, st)
+                           : launch_gemv_m<PRO, EPI, WF32>(M, a, st);
+}
+
+static inline GemvArgs gemv_args(const void* w, int N, int K, const float* x, int ldx, float* out,
+                                 int ldo) {
+  GemvArgs a{};
+  a.w[0] = w; a.w[1] = nullptr; a.w[2] = nullptr;
+  a.seg_rows[0] = N; a.seg_rows[1] = 0; a.seg_rows[2] = 0;
+  a.N = N; a.K = K;
+  a.x = x; a.ldx = ldx;
+  a.out = out; a.ldo = ldo;
+  return a;
+}
+
+static inline hipError_t prepare_sampler() {
+  static bool done = false;
+  if (done) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sample_step_kernel<WF32>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)SAMPLE_SMEM);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(sample_step_kernel<WBF16>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)SAMPLE_SMEM);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(sample_op_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)SAMPLE_SMEM);
+  if (e == hipSuccess) done = true;
+  return e;
+}
+
+}  // namespace sk

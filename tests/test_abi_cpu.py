@@ -1,0 +1,119 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+include/soraku_mi355x.h declares, and rejects bad arguments before any HIP
+call (the host-side failure list of the reference: graph_frame.py:128-129,
+155-156, 301-302; fast_generate.py:250-251; model.py:541-544)."""
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "soraku_mi355x.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\*|void\*|int32_t|int)\s+(sk_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from soraku_amd import _lib
+
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported(L):
+    names = declared_symbols()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_binding_covers_header():
+    from soraku_amd._lib import PROTOTYPES
+
+    assert sorted(PROTOTYPES) == declared_symbols()
+
+
+def test_config_struct_layout_matches_header():
+    """sk_config: 23 int32/float fields then int32[4] = 108 bytes."""
+    from soraku_amd._lib import SkConfig
+
+    assert C.sizeof(SkConfig) == 23 * 4 + 16
+
+
+def _good_config():
+    from soraku_amd.config import TINY, to_sk_config
+
+    return to_sk_config(TINY, n_utts=1, cfg_rows=2, max_ctx=64, max_frames=16)
+
+
+@pytest.mark.parametrize("field,value", [
+    ("d_model", 12), ("head_dim", 24), ("n_kv_heads", 3), ("cfg_rows", 3), ("n_utts", 0),
+    ("audio_vocab", 5000), ("max_ctx", 1), ("bos_id", 35), ("weight_dtype", 7), ("n_language", 2),
+    ("trunk_eps", 0.0),
+])
+def test_create_rejects_bad_config(L, field, value):
+    from soraku_amd._lib import SK_EINVAL
+
+    c = _good_config()
+    setattr(c, field, value)
+    h = C.c_void_p()
+    assert L.sk_create(C.byref(c), None, C.byref(h)) == SK_EINVAL
+    assert h.value is None
+    assert L.sk_last_error().decode()
+
+
+def test_null_handles_are_rejected(L):
+    from soraku_amd._lib import SK_EINVAL
+
+    assert L.sk_create(None, None, None) == SK_EINVAL
+    assert L.sk_destroy(None) == 0
+    assert L.sk_prefill_run(None) == SK_EINVAL
+    assert L.sk_capture(None) == SK_EINVAL
+    assert L.sk_step_frame(None, 0, None, None, None, None) == SK_EINVAL
+    assert L.sk_bind_weight(None, b"trunk.norm.weight", None, 0, None, 0) == SK_EINVAL
+    assert L.sk_frames_done(None) == -1
+
+
+def test_ops_reject_bad_arguments(L):
+    from soraku_amd._lib import SK_EINVAL
+
+    p = C.c_void_p(4096)
+    assert L.sk_op_swiglu_gemv(None, 2, 16, 12, 0, p, p, p, p) == SK_EINVAL   # D % 8
+    assert L.sk_op_swiglu_gemv(None, 2, 16, 16, 9, p, p, p, p) == SK_EINVAL   # dtype
+    assert L.sk_op_classifier_gemv(None, 2, 16, 16, 0, p, None, p, p) == SK_EINVAL
+    assert L.sk_op_down_residual_gemv(None, 0, 16, 16, 0, p, p, p, p) == SK_EINVAL
+    assert L.sk_op_sample(None, 3, 64, p, 1.5, 0, 0, 61, 62, 63, 0.9, 50, 0.9, 0.5, p) == SK_EINVAL
+    assert L.sk_op_sample(None, 2, 64, p, 1.5, 0, 0, 61, 62, 63, 0.9, 50, 0.9, 1.0, p) == SK_EINVAL
+    assert L.sk_op_sample(None, 2, 9000, p, 1.5, 0, 0, 61, 62, 63, 0.9, 50, 0.9, 0.5, p) == SK_EINVAL
+    assert L.sk_op_rmsnorm(None, 0, 16, 1e-6, p, p, p) == SK_EINVAL
+
+
+def test_generate_argument_errors_before_gpu():
+    """FastGenerator.generate validates like fast_generate.py:351-354."""
+    from soraku_amd import FastGenerator
+
+    g = FastGenerator.__new__(FastGenerator)
+    with pytest.raises(ValueError):
+        FastGenerator.generate(g, input_ids=np.zeros((2, 3), np.int64))
+    with pytest.raises(ValueError):
+        FastGenerator.generate(g, input_ids=np.zeros((1, 3), np.int64), cfg_scale=1.5)
+
+
+def test_synthetic_weights_match_oracle():
+    """The package's seeded weights are the oracle's, value for value."""
+    from oracle.model import TINY as OT, synthetic_weights as ow
+    from soraku_amd.config import TINY
+    from soraku_amd.synthetic import synthetic_weights as pw
+
+    a = ow(OT, 3, norm_gain_std=0.1, bias_std=0.02)
+    b = pw(TINY, 3, norm_gain_std=0.1, bias_std=0.02)
+    assert sorted(a) == sorted(b)
+    for k in a:
+        np.testing.assert_array_equal(a[k], b[k])

@@ -1,0 +1,166 @@
+"""The oracle against golden vectors written by the reference's native path
+(tests/golden/make_golden.py: SorakuTTSv2.generate over the transformers
+Qwen3 trunk, CPU, seeded weights)."""
+
+import numpy as np
+import pytest
+
+from conftest import load_golden
+from oracle.generate import Record, generate
+from oracle.model import OracleModel, synthetic_weights
+from oracle.sampler import apply_masks, filtered_probs
+
+TINY_FIXTURES = ["tiny_greedy", "tiny_sampled", "tiny_nocfg_topp"]
+
+
+def _model(f, s, dtype):
+    w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                          bias_std=float(f["bias_std"]))
+    return OracleModel(s, w, dtype, language_token_ids=tuple(int(v) for v in f["language_ids"]))
+
+
+def _masked_calls(rec, s, gen, n):
+    out = []
+    for fi, fr in enumerate(rec.merged):
+        for q, m in enumerate(fr):
+            out.append(apply_masks(m, q=q, frame_index=fi, min_new_frames=gen["min_new_frames"],
+                                   bos_id=s.bos_id, eos_id=s.eos_id, pad_id=s.pad_id))
+    return np.stack(out[:n])
+
+
+def _forced(f, s):
+    codes = f["codes"]
+    if int(f["stop_eos"]):
+        codes = np.concatenate([codes, np.full((1, s.n_codebooks), s.eos_id)])
+    return codes
+
+
+def _run(f, s, gen, dtype, batched=False):
+    m = _model(f, s, dtype)
+    g = {k: v for k, v in gen.items() if k != "seed"}
+    rec = Record()
+    codes, info = generate(m, input_ids=f["text_ids"], prompt_codes=f["prompt_codes"],
+                           uncond_input_ids=f["uncond_ids"], forced_codes=_forced(f, s),
+                           record=rec, batched=batched, **g)
+    return rec, codes, info
+
+
+@pytest.mark.parametrize("name", TINY_FIXTURES)
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_sample_logits_match_reference(name, dtype):
+    f, s, gen = load_golden(name)
+    rec, codes, _ = _run(f, s, gen, dtype)
+    ref = f["sample_logits"]
+    got = _masked_calls(rec, s, gen, ref.shape[0])
+    fin = np.isfinite(ref)
+    assert (np.isfinite(got) == fin).all()
+    rel = np.abs(got[fin] - ref[fin]).max() / np.abs(ref[fin]).max()
+    assert rel < 2e-6, rel
+    np.testing.assert_array_equal(codes, f["codes"])
+
+
+@pytest.mark.parametrize("name", TINY_FIXTURES)
+def test_hidden_states_match_reference(name):
+    f, s, gen = load_golden(name)
+    rec, _, _ = _run(f, s, gen, np.float64)
+    ref = f["hidden"]
+    got = np.stack(rec.hidden)
+    n = min(len(got), len(ref))
+    assert n >= ref.shape[0] - 1
+    rel = np.abs(got[:n] - ref[:n]).max() / np.abs(ref).max()
+    assert rel < 2e-6, rel
+
+
+def test_greedy_free_running_codes_match_reference():
+    f, s, gen = load_golden("tiny_greedy")
+    m = _model(f, s, np.float64)
+    g = {k: v for k, v in gen.items() if k != "seed"}
+    codes, info = generate(m, input_ids=f["text_ids"], prompt_codes=f["prompt_codes"],
+                           uncond_input_ids=f["uncond_ids"], **g)
+    np.testing.assert_array_equal(codes, f["codes"])
+    assert info["stop_reason"] == ("eos" if int(f["stop_eos"]) else "max_frames")
+
+
+@pytest.mark.parametrize("name", ["tiny_sampled", "tiny_nocfg_topp"])
+def test_filtered_distribution_matches_reference(name):
+    """Top-k / top-p filter = what _sample_logits hands to torch.multinomial."""
+    f, s, gen = load_golden(name)
+    rec, _, _ = _run(f, s, gen, np.float32)
+    ref = f["probs"]
+    got = _masked_calls(rec, s, gen, ref.shape[0])
+    i = 0
+    for fi in range(len(rec.merged)):
+        for q in range(s.n_codebooks):
+            if i >= ref.shape[0]:
+                break
+            t = gen.get("temperature_q0") if q == 0 and gen.get("temperature_q0") is not None else gen["temperature"]
+            k = gen.get("top_k_q0") if q == 0 and gen.get("top_k_q0") is not None else gen.get("top_k")
+            p = gen.get("top_p_q0") if q == 0 and gen.get("top_p_q0") is not None else gen.get("top_p")
+            x = (got[i] / np.float32(t)).astype(np.float32)
+            pr = filtered_probs(x, k, p)
+            np.testing.assert_array_equal(pr > 0, ref[i] > 0)
+            assert np.abs(pr - ref[i]).max() < 1e-6
+            i += 1
+    assert i == ref.shape[0]
+
+
+def test_batched_rows_equal_native_rows_to_rounding():
+    f, s, gen = load_golden("tiny_sampled")
+    rec_a, _, _ = _run(f, s, gen, np.float64, batched=False)
+    rec_b, _, _ = _run(f, s, gen, np.float64, batched=True)
+    a = np.stack([np.stack(x) for x in rec_a.merged])
+    b = np.stack([np.stack(x) for x in rec_b.merged])
+    assert np.abs(a - b).max() < 1e-12
+
+
+def test_q06b_fixture_prefix_and_first_frames():
+    """Qwen3-0.6B shape (28 layers, d=1024, V=2051): the reference's first
+    frames, teacher-forced, in float32."""
+    f, s, gen = load_golden("q06b_greedy")
+    rec, codes, _ = _run(f, s, gen, np.float32, batched=True)
+    ref = f["sample_logits"]
+    got = _masked_calls(rec, s, gen, ref.shape[0])
+    fin = np.isfinite(ref)
+    rel = np.abs(got[fin] - ref[fin]).max() / np.abs(ref[fin]).max()
+    assert rel < 1e-4, rel
+    np.testing.assert_array_equal(codes, f["codes"])
+
+
+def test_planted_mistakes_are_caught():
+    """A dropped residual in the depth head or a swapped CFG order in the
+    oracle must break agreement with the reference vectors."""
+    import oracle.model as om
+    import oracle.sampler as osm
+
+    f, s, gen = load_golden("tiny_greedy")
+    ref = f["sample_logits"]
+    fin = np.isfinite(ref)
+
+    def err():
+        rec, _, _ = _run(f, s, gen, np.float64)
+        got = _masked_calls(rec, s, gen, ref.shape[0])
+        return np.abs(got[fin] - ref[fin]).max() / np.abs(ref[fin]).max()
+
+    assert err() < 2e-6
+    orig = om.OracleModel.depth_logits
+
+    def no_residual(self, hidden, prefix, q):
+        w = self.w
+        a = om.rms_norm(hidden + prefix, w["depth_head.norm_in.weight"], om.FLT_EPS)
+        y = (om.silu(a @ w["depth_head.mlp.gate_proj.weight"].T) * (a @ w["depth_head.mlp.up_proj.weight"].T)) \
+            @ w["depth_head.mlp.down_proj.weight"].T
+        body = om.rms_norm(y, w["depth_head.norm_out.weight"], om.FLT_EPS)
+        return body @ w["audio_codebooks.table"][q].T + w["depth_head.bias"][q]
+
+    om.OracleModel.depth_logits = no_residual
+    try:
+        assert err() > 1e-3
+    finally:
+        om.OracleModel.depth_logits = orig
+    orig_merge = osm.cfg_merge
+    import oracle.generate as og
+    og.cfg_merge = lambda c, u, sc: orig_merge(u, c, sc)
+    try:
+        assert err() > 1e-3
+    finally:
+        og.cfg_merge = orig_merge

@@ -1,0 +1,195 @@
+"""Benchmark: per-frame CFG decode on one MI355X.
+
+Workload (full synthetic utterance, Qwen3-0.6B shape, FP32): random-init
+weights N(0, 0.02); cond prefix = 96 text ids + BOS frame + 144 prompt frames
+(241 positions), uncond prefix = [bos] + BOS frame + prompt frames (146);
+240 decoded frames with CFG 1.5, temperature 0.9, top-k 50, top-p 0.95 and
+seeded uniform draws; one hipGraph replay per frame.  A step is one frame.
+
+Timed region: W warm-up replays, then K replays back to back on the engine's
+stream bracketed by HIP events (inputs already resident in HBM; per-frame
+uniforms uploaded before the timed region).  EOS is masked on every frame
+so all K frames run (the work per frame does not depend on it).
+
+Prints one JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one
+GPU (utterances shard across GPUs with no per-frame exchange).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "soraku-tts_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "codec frames/sec and µs/frame (CFG batch 2) + % HBM roofline, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+N_TEXT, N_PROMPT, N_FRAMES = 96, 144, 240
+CFG, TEMP, TOP_K, TOP_P = 1.5, 0.9, 50, 0.95
+TEXT_BOS = 151643
+
+
+def workload_inputs(shape, seed=0):
+    from soraku_amd.synthetic import utterance
+
+    text, prompt = utterance(shape, seed + 100, n_text=N_TEXT, n_prompt=N_PROMPT)
+    text[0] = TEXT_BOS
+    uncond = np.array([TEXT_BOS], np.int64)
+    u = np.random.default_rng(seed + 1).random((N_FRAMES, shape.n_codebooks))
+    return text, prompt, uncond, u
+
+
+def algorithmic_bytes(shape, kv_lens, w_bytes=4, kv_bytes=4):
+    """Bytes one frame must move at minimum: every weight tensor read once
+    (depth MLP counted once although applied Q times), K/V of every cached
+    token of every row read once, the new token's K/V written, Q table rows
+    gathered.  ``kv_lens``: cached tokens per row at the frame's start."""
+    s = shape
+    per_layer = (2 * s.n_q_heads * s.head_dim * s.d_model + 2 * s.n_kv_heads * s.head_dim * s.d_model
+                 + 3 * s.trunk_inter * s.d_model + 2 * s.d_model + 2 * s.head_dim)
+    trunk = s.n_layers * per_layer + s.d_model
+    depth = 3 * s.depth_inner * s.d_model + 2 * s.d_model
+    table = s.n_codebooks * s.audio_vocab * s.d_model
+    bias = s.n_codebooks * s.audio_vocab
+    weights = (trunk + depth + table) * w_bytes + bias * 4
+    kv_token = s.n_layers * 2 * s.n_kv_heads * s.head_dim * kv_bytes
+    kv = sum(kv_lens) * kv_token + len(kv_lens) * kv_token
+    gather = s.n_codebooks * s.d_model * 4
+    return weights + kv + gather
+
+
+def cpu_info():
+    model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model
+
+
+def cpu_baseline(shape, weights, text, prompt, uncond, u, n_frames=6, n_warm=1):
+    """The oracle (NumPy FP32, the reference's native two-branch order) on the
+    host cores, over a bounded sample of the same workload."""
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    from oracle.generate import generate, start_states
+    from oracle.model import OracleModel, Shape
+
+    cores = os.cpu_count() or 1
+    with threadpool_limits(limits=cores):
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        os_shape = Shape(**{k: getattr(shape, k) for k in Shape.__dataclass_fields__})
+        m = OracleModel(os_shape, weights, np.float32)
+        max_ctx = text.size + 1 + prompt.shape[0] + n_frames + n_warm + 2
+        states = start_states(m, text, prompt, uncond, CFG, max_ctx)
+        kw = dict(min_new_frames=10**6, temperature=TEMP, top_k=TOP_K, top_p=TOP_P, cfg_scale=CFG)
+        generate(m, max_new_frames=n_warm, uniforms=u, states=states, input_ids=text, **kw)
+        t0 = time.perf_counter()
+        generate(m, max_new_frames=n_frames, uniforms=u[n_warm:], states=states, input_ids=text, **kw)
+        dt = time.perf_counter() - t0
+    return {"value": n_frames / dt, "unit": "frames/s", "cores": int(threads), "kind": "port",
+            "sample": (f"oracle/ (NumPy FP32, cond and uncond as separate B=1 branches), "
+                       f"{n_frames} frames timed after {n_warm} warm-up at prefixes "
+                       f"{text.size + 1 + prompt.shape[0]}/{uncond.size + 1 + prompt.shape[0]}; "
+                       f"{dt / n_frames * 1e3:.1f} ms/frame; host {cpu_info()}")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}): utterances shard across GPUs "
+              "with no per-frame exchange, so the per-GPU figure is the N=1 line.", file=sys.stderr)
+        sys.exit(2)
+    if args.steps + args.warmup > N_FRAMES:
+        sys.exit(f"steps + warmup must be <= {N_FRAMES} (the workload's decoded frames)")
+
+    import torch
+
+    from soraku_amd import GraphFrameEngine
+    from soraku_amd.config import QWEN3_06B
+    from soraku_amd.synthetic import synthetic_weights
+
+    shape = QWEN3_06B
+    t_setup = time.perf_counter()
+    weights = synthetic_weights(shape, args.seed)
+    text, prompt, uncond, u = workload_inputs(shape, args.seed)
+    dev = torch.device("cuda:0")
+    max_ctx = text.size + 1 + prompt.shape[0] + N_FRAMES + 8
+    e = GraphFrameEngine(device=dev, max_cache_len=max_ctx, cfg_scale=CFG, batch=2,
+                         state_dict=weights, shape=shape, max_frames=N_FRAMES)
+    e.set_temperature(TEMP)
+    e.set_sampling(sampled=True, top_k=TOP_K, top_p=TOP_P)
+    t0 = time.perf_counter()
+    e.prefill(text, uncond, prompt)
+    t_prefill = time.perf_counter() - t0
+    e.capture()
+    total = args.warmup + args.steps
+    e.queue_frames(u[:total], np.ones(total, np.int32))
+    kv0 = [text.size + 1 + prompt.shape[0], uncond.size + 1 + prompt.shape[0]]
+    print(f"# setup {time.perf_counter() - t_setup:.1f}s, prefill {t_prefill * 1e3:.1f} ms", file=sys.stderr,
+          flush=True)
+
+    stream = torch.cuda.ExternalStream(e.stream_handle, device=dev)
+    e.replay(args.warmup)
+    e.synchronize()
+    torch.cuda.synchronize(dev)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    evs[0].record(stream)
+    for i in range(args.steps):
+        e.replay(1)
+        evs[i + 1].record(stream)
+    e.synchronize()
+    torch.cuda.synchronize(dev)
+    per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]) * 1e3  # us
+    total_ms = evs[0].elapsed_time(evs[-1])
+    codes = e.read_codes(args.steps)
+    assert codes.min() >= 0 and codes.max() < shape.codebook_size, "decoded a special id"
+
+    us = total_ms * 1e3 / args.steps
+    kv_mid = [k + args.warmup + (args.steps - 1) / 2 for k in kv0]
+    alg = algorithmic_bytes(shape, kv_mid)
+    achieved = alg / (us * 1e-6) / 1e9
+    out = {
+        "metric": METRIC, "value": 1e6 / us, "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": us / 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": ("full synthetic utterance, Qwen3-0.6B shape FP32: 96 text ids + "
+                                "144 prompt frames, CFG 1.5, T 0.9, top-k 50, top-p 0.95, seeded "
+                                "uniforms, one hipGraph per frame"),
+                   "global_batch": 2, "seq_len": int(kv0[0] + N_FRAMES), "parallelism": "none",
+                   "us_per_frame_median": float(np.median(per)),
+                   "us_per_frame_p90": float(np.percentile(per, 90)),
+                   "prefill_ms": t_prefill * 1e3},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "unit_of_work": "one frame = one hipGraph launch",
+                     "algorithmic_bytes_per_launch": alg},
+    }
+    e.close()
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(shape, weights, text, prompt, uncond, u)
+        out["cpu_baseline"]["speedup"] = out["value"] / out["cpu_baseline"]["value"]
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

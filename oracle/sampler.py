@@ -19,8 +19,9 @@ pick the same code:
 1. candidates = finite values that survive top-k, ordered by value
    descending, ties by lower index first;
 2. ``w_i = exp(x_i - x_0)`` in float64, ``W_i`` = sequential prefix sums;
-3. top-p keeps ``n_keep = 1 + #{i >= 1 : W_{i-1} / W_{n-1} <= p}`` leading
-   candidates (p taken as an FP32 value promoted to float64);
+3. top-p keeps the leading candidates up to and including the first i with
+   ``W_i > p * W_{n-1}`` (all n if none; p taken as an FP32 value promoted to
+   float64, the product rounded once), i.e. ``cum > p`` shifted right by one;
 4. the code is the first kept candidate with ``W_j > u * W_{n_keep-1}``
    (the last kept one if rounding leaves none).
 
@@ -80,7 +81,7 @@ def topp_weights(vals, top_p):
     n_keep = n
     if top_p is not None and 0 < top_p < 1:
         p = float(np.float32(top_p))
-        over = np.nonzero(W[:-1] / W[-1] > p)[0]
+        over = np.nonzero(W[:-1] > p * W[-1])[0]
         if over.size:
             n_keep = int(over[0]) + 1
     return w, W, n_keep

@@ -60,12 +60,13 @@ struct sk_engine {
   // device buffers (owned)
   float *x = nullptr, *hidden = nullptr, *prefix = nullptr, *abuf = nullptr, *ybuf = nullptr;
   float *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
-  float *kc = nullptr, *vc = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
+  float *kc = nullptr, *vc = nullptr, *inv_freq = nullptr;
   float *part = nullptr, *dbg = nullptr, *embeds = nullptr;
-  int *counters = nullptr, *kv_len = nullptr, *pos = nullptr, *active = nullptr, *plen = nullptr;
-  int *fc = nullptr, *pf_t = nullptr, *flag_ring = nullptr;
-  double* u_ring = nullptr;
+  int *kv_len = nullptr, *pos = nullptr, *active = nullptr, *plen = nullptr;
+  int *fc = nullptr, *pf_t = nullptr, *flag_ring = nullptr, *flag_cur = nullptr;
+  double *u_ring = nullptr, *u_cur = nullptr;
   int64_t *forced_ring = nullptr, *codes_ring = nullptr, *stage_ids = nullptr, *stage_codes = nullptr;
+  int* codes_cur = nullptr;
   SkParams* params = nullptr;
 
   // host mirrors
@@ -100,8 +101,8 @@ int validate_config(const sk_config* c) {
   SK_CHECK(c->n_q_heads > 0 && c->n_kv_heads > 0 && c->n_q_heads % c->n_kv_heads == 0, SK_EINVAL,
            "n_q_heads must be a positive multiple of n_kv_heads");
   const int hd = c->head_dim;
-  SK_CHECK(hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256 || hd == 512,
-           SK_EINVAL, "head_dim must be a power of two in [8, 512]");
+  SK_CHECK(hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256 || hd == 512,
+           SK_EINVAL, "head_dim must be a power of two in [16, 512]");
   SK_CHECK(c->trunk_inter > 0 && c->trunk_inter % 8 == 0, SK_EINVAL, "trunk_inter must be a positive multiple of 8");
   SK_CHECK(c->depth_inner > 0 && c->depth_inner % 8 == 0, SK_EINVAL, "depth_inner must be a positive multiple of 8");
   SK_CHECK(c->n_codebooks > 0 && c->n_codebooks <= 64, SK_EINVAL, "n_codebooks must be in [1, 64]");
@@ -123,23 +124,17 @@ int validate_config(const sk_config* c) {
   return SK_OK;
 }
 
-// FP32 RoPE angle inv_freq * pos, cos/sin evaluated in double and rounded once
-// (inv_freq as modeling_qwen3.py:116-122; cos/sin modeling_qwen3.py:126-137).
-void rope_tables(const sk_config& c, std::vector<float>& cs, std::vector<float>& sn) {
+// FP32 RoPE inverse frequencies 1 / theta^(2i/hd) (modeling_qwen3.py:116-122);
+// the kernels form the FP32 angle pos * inv_freq and its cos/sin
+// (modeling_qwen3.py:126-137).
+std::vector<float> rope_inv_freq(const sk_config& c) {
   const int half = c.head_dim / 2;
   std::vector<float> inv(half);
   for (int i = 0; i < half; ++i) {
     const float ex = (float)(2 * i) / (float)c.head_dim;
     inv[i] = 1.0f / powf(c.rope_theta, ex);
   }
-  cs.resize((size_t)c.max_ctx * half);
-  sn.resize((size_t)c.max_ctx * half);
-  for (int p = 0; p < c.max_ctx; ++p)
-    for (int i = 0; i < half; ++i) {
-      const float ang = (float)p * inv[i];
-      cs[(size_t)p * half + i] = (float)cos((double)ang);
-      sn[(size_t)p * half + i] = (float)sin((double)ang);
-    }
+  return inv;
 }
 
 int check_decode_weights(const sk_engine* e) {
@@ -176,16 +171,18 @@ hipError_t enqueue_trunk(sk_engine* e) {
     at.kc = e->kc + (size_t)l * kv_layer_elems(e);
     at.vc = e->vc + (size_t)l * kv_layer_elems(e);
     at.qn_w = w.q_norm; at.kn_w = w.k_norm; at.eps = c.trunk_eps;
-    at.rope_cos = e->rope_cos; at.rope_sin = e->rope_sin;
+    at.inv_freq = e->inv_freq;
     at.kv_len = e->kv_len; at.pos = e->pos; at.active = e->active;
-    at.part = e->part; at.counters = e->counters;
+    at.part = e->part;
     at.out = e->attn; at.ldo = c.n_q_heads * hd;
     at.Hq = c.n_q_heads; at.Hkv = c.n_kv_heads; at.hd = hd; at.max_ctx = c.max_ctx;
     at.max_chunks = e->max_chunks;
     at.scale = 1.0f / sqrtf((float)hd);
-    const size_t asmem = ((size_t)e->G * hd + 2 * hd + (size_t)e->G * ATT_CHUNK + 2 * e->G) * sizeof(float);
+    const size_t asmem = attn_smem_floats(e->G, hd) * sizeof(float);
     hipLaunchKernelGGL(attention_kernel, dim3(e->max_chunks, c.n_kv_heads, M), dim3(NT), asmem,
                        e->stream, at);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(c.n_q_heads, M), dim3(hd), 0, e->stream, at);
     if ((err = hipGetLastError()) != hipSuccess) return err;
 
     a = gemv_args(w.o, d, c.n_q_heads * hd, e->attn, c.n_q_heads * hd, e->x, d);
@@ -212,8 +209,8 @@ hipError_t enqueue_frame(sk_engine* e) {
   SampleArgs s{};
   s.logits = e->logits; s.ldl = V; s.rows_per_utt = c.cfg_rows; s.V = V;
   s.params = e->params; s.fc = e->fc;
-  s.u_ring = e->u_ring; s.flag_ring = e->flag_ring; s.forced_ring = e->forced_ring;
-  s.codes_ring = e->codes_ring; s.dbg = e->dbg; s.table = e->table;
+  s.u_cur = e->u_cur; s.flag_cur = e->flag_cur; s.forced_ring = e->forced_ring;
+  s.codes_ring = e->codes_ring; s.codes_cur = e->codes_cur; s.dbg = e->dbg; s.table = e->table;
   s.prefix = e->prefix; s.xnext = e->x; s.d = d; s.Q = c.n_codebooks; s.scale = c.frame_scale;
   s.bos = c.bos_id; s.eos = c.eos_id; s.pad = c.pad_id; s.n_utts = c.n_utts;
   for (int q = 0; q < c.n_codebooks; ++q) {
@@ -239,7 +236,8 @@ hipError_t enqueue_frame(sk_engine* e) {
   }
   if ((err = enqueue_trunk(e)) != hipSuccess) return err;
   hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x, e->final_norm,
-                     c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->fc);
+                     c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->fc, e->u_ring,
+                     e->flag_ring, e->u_cur, e->flag_cur, c.n_utts * c.n_codebooks, c.max_frames);
   return hipGetLastError();
 }
 
@@ -251,7 +249,8 @@ hipError_t enqueue_prefill_step(sk_engine* e) {
   if (err != hipSuccess) return err;
   if ((err = enqueue_trunk(e)) != hipSuccess) return err;
   hipLaunchKernelGGL(final_norm_kernel, dim3(e->rows), dim3(NT), 0, e->stream, e->x, e->final_norm,
-                     c.trunk_eps, c.d_model, e->hidden, e->kv_len, e->pos, e->active, e->pf_t);
+                     c.trunk_eps, c.d_model, e->hidden, e->kv_len, e->pos, e->active, e->pf_t,
+                     (const double*)nullptr, (const int*)nullptr, (double*)nullptr, (int*)nullptr, 0, 0);
   return hipGetLastError();
 }
 
@@ -338,14 +337,15 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   ALLOC(e->act, R * e->inner_max); ALLOC(e->logits, R * V);
   ALLOC(e->kc, (size_t)c.n_layers * kv_layer_elems(e));
   ALLOC(e->vc, (size_t)c.n_layers * kv_layer_elems(e));
-  ALLOC(e->rope_cos, (size_t)c.max_ctx * c.head_dim / 2);
-  ALLOC(e->rope_sin, (size_t)c.max_ctx * c.head_dim / 2);
+  ALLOC(e->inv_freq, (size_t)c.head_dim / 2);
   ALLOC(e->part, R * c.n_q_heads * e->max_chunks * (c.head_dim + 2));
-  ALLOC(e->counters, R * c.n_kv_heads);
   ALLOC(e->kv_len, R); ALLOC(e->pos, R); ALLOC(e->active, R); ALLOC(e->plen, R);
   ALLOC(e->fc, 1); ALLOC(e->pf_t, 1);
   ALLOC(e->u_ring, (size_t)c.max_frames * c.n_utts * Q);
   ALLOC(e->flag_ring, (size_t)c.max_frames * 2);
+  ALLOC(e->u_cur, (size_t)c.n_utts * Q);
+  ALLOC(e->flag_cur, 2);
+  ALLOC(e->codes_cur, (size_t)c.n_utts * Q);
   ALLOC(e->forced_ring, (size_t)c.max_frames * c.n_utts * Q);
   ALLOC(e->codes_ring, (size_t)c.max_frames * c.n_utts * Q);
   ALLOC(e->dbg, (size_t)c.n_utts * Q * V);
@@ -354,11 +354,10 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   ALLOC(e->stage_codes, (size_t)c.max_ctx * Q);
   ALLOC(e->params, 1);
 #undef ALLOC
-  std::vector<float> cs, sn;
-  rope_tables(c, cs, sn);
-  hipError_t he = hipMemcpy(e->rope_cos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice);
-  if (he == hipSuccess) he = hipMemcpy(e->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice);
-  if (he == hipSuccess) he = hipMemset(e->counters, 0, R * c.n_kv_heads * sizeof(int));
+  const std::vector<float> inv = rope_inv_freq(c);
+  hipError_t he = hipMemcpy(e->inv_freq, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice);
+  if (he == hipSuccess) he = hipMemset(e->u_cur, 0, (size_t)c.n_utts * Q * sizeof(double));
+  if (he == hipSuccess) he = hipMemset(e->flag_cur, 0, 2 * sizeof(int));
   if (he == hipSuccess) he = hipMemset(e->x, 0, R * d * sizeof(float));
   if (he == hipSuccess) he = hipMemset(e->prefix, 0, R * d * sizeof(float));
   if (he == hipSuccess) he = hipMemset(e->kv_len, 0, R * sizeof(int));
@@ -380,7 +379,7 @@ int sk_destroy(sk_engine* e) {
   if (e->stream) hipStreamSynchronize(e->stream);
   drop_graphs(e);
   void* bufs[] = {e->x, e->hidden, e->prefix, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
-                  e->kc, e->vc, e->rope_cos, e->rope_sin, e->part, e->dbg, e->embeds, e->counters,
+                  e->kc, e->vc, e->inv_freq, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->pf_t, e->flag_ring, e->u_ring,
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
   for (void* p : bufs)
@@ -617,6 +616,8 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
   const int flags[2] = {mask_eos_q0 ? 1 : 0, forced_codes ? 1 : 0};
   SK_HIP(hipMemcpyAsync(e->u_ring + slot * nq, u.data(), nq * sizeof(double), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemcpyAsync(e->flag_ring + 2 * slot, flags, sizeof(flags), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->u_cur, u.data(), nq * sizeof(double), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->flag_cur, flags, sizeof(flags), hipMemcpyHostToDevice, e->stream));
   if (forced_codes)
     SK_HIP(hipMemcpyAsync(e->forced_ring + slot * nq, forced_codes, nq * sizeof(int64_t), hipMemcpyHostToDevice,
                           e->stream));
@@ -647,6 +648,8 @@ int sk_queue_frames(sk_engine* e, int32_t n, const double* uniforms, const int32
   SK_HIP(hipMemcpy(e->u_ring + (size_t)e->fc_host * nq, u.data(), u.size() * sizeof(double), hipMemcpyHostToDevice));
   SK_HIP(hipMemcpy(e->flag_ring + 2 * (size_t)e->fc_host, flags.data(), flags.size() * sizeof(int),
                    hipMemcpyHostToDevice));
+  SK_HIP(hipMemcpy(e->u_cur, u.data(), nq * sizeof(double), hipMemcpyHostToDevice));
+  SK_HIP(hipMemcpy(e->flag_cur, flags.data(), 2 * sizeof(int), hipMemcpyHostToDevice));
   return SK_OK;
 }
 

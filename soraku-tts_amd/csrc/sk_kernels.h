@@ -17,7 +17,7 @@ namespace {
 
 constexpr int NT = 256;      // threads per workgroup
 constexpr int WAVES = NT / 64;
-constexpr int ATT_CHUNK = 64; // KV tokens per attention workgroup
+constexpr int ATT_CHUNK = 32; // KV tokens per attention workgroup
 constexpr int MAX_V = 4096;   // sampler LDS capacity (audio vocab)
 
 // ------------------------------------------------------------ reductions
@@ -96,23 +96,18 @@ struct GemvArgs {
   const float* bias;           // EPI_BIAS
 };
 
-// Workgroup: 4 waves, each wave owns RPW output rows and streams those rows'
-// full K with 16-byte loads; x comes from LDS.  With RMSNorm prologues each
-// workgroup normalises the (tiny) input itself, which saves a launch.
-// Norm form: w * (x * (1 / sqrt(mean(x^2) + eps))) (Qwen3RMSNorm, nn.RMSNorm).
-template <int M, int RPW, int PRO, int EPI, typename WL>
-__global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
-  extern __shared__ float smem[];
-  float* xs = smem;                 // [M][K]
-  __shared__ float red[M][WAVES];
+// Stage x (+ x2) into LDS xs[M][K], applying the RMSNorm prologue if asked.
+template <int M, int PRO>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, int K, float* xs, float (*red)[WAVES]) {
   const int tid = threadIdx.x;
-  const int K = a.K;
-
   for (int m = 0; m < M; ++m)
-    for (int k = tid; k < K; k += NT) {
-      float v = a.x[(size_t)m * a.ldx + k];
-      if (PRO == PRO_ADDNORM) v += a.x2[(size_t)m * a.ldx2 + k];
-      xs[m * K + k] = v;
+    for (int k = tid * 4; k < K; k += NT * 4) {
+      float4 v = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + k);
+      if (PRO == PRO_ADDNORM) {
+        const float4 w = *reinterpret_cast<const float4*>(a.x2 + (size_t)m * a.ldx2 + k);
+        v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+      }
+      *reinterpret_cast<float4*>(&xs[m * K + k]) = v;
     }
   if (PRO != PRO_NONE) {
     __syncthreads();
@@ -144,6 +139,20 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
       }
   }
   __syncthreads();
+}
+
+// Workgroup: 4 waves, each wave owns RPW output rows and streams those rows'
+// full K with 16-byte loads; x comes from LDS.  With RMSNorm prologues each
+// workgroup normalises the (tiny) input itself, which saves a launch.
+// Norm form: w * (x * (1 / sqrt(mean(x^2) + eps))) (Qwen3RMSNorm, nn.RMSNorm).
+template <int M, int RPW, int PRO, int EPI, typename WL>
+__global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
+  extern __shared__ float smem[];
+  float* xs = smem;                 // [M][K]
+  __shared__ float red[M][WAVES];
+  const int tid = threadIdx.x;
+  const int K = a.K;
+  stage_x<M, PRO>(a, K, xs, red);
 
   constexpr int VEC = WL::VEC;
   constexpr int NS = (EPI == EPI_SWIGLU) ? 2 : 1;
@@ -233,6 +242,158 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// Full-wave sum via DPP (row_shr / row_bcast); the total lands in lane 63
+// and is broadcast with readlane.  Fixed order, so replays are bitwise equal.
+template <int CTRL, int ROW_MASK, bool BOUND0>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, BOUND0));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp<0xb1, 0xf, true>(v);    // quad_perm [1,0,3,2]
+  v += dpp<0x4e, 0xf, true>(v);    // quad_perm [2,3,0,1]
+  v += dpp<0x114, 0xf, true>(v);   // row_shr:4
+  v += dpp<0x118, 0xf, true>(v);   // row_shr:8
+  v += dpp<0x142, 0xa, false>(v);  // row_bcast:15
+  v += dpp<0x143, 0xc, false>(v);  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// GEMV for a compile-time K with no LDS and no barriers.  Each wave owns RW
+// output rows (x NS sources for SwiGLU).  It first loads the activations it
+// needs straight into registers in its own lane layout (lane l holds
+// x[m][(j*64 + l)*VEC ..+VEC) for every j: the whole K across the wave), then
+// issues every 16-byte weight load of its rows, so the HBM stream starts
+// before any arithmetic and waits only on the (L2-resident) activations.  The
+// RMSNorm prologue is computed per wave from those registers with a DPP
+// reduction.  Rows past N re-read row N-1 (in bounds) and are discarded.
+template <int M, int KT, int RW, int PRO, int EPI, typename WL>
+__global__ __launch_bounds__(NT) void gemv_fast_kernel(GemvArgs a) {
+  constexpr int VEC = WL::VEC;
+  constexpr int NV = KT / (64 * VEC);
+  constexpr int NS = (EPI == EPI_SWIGLU) ? 2 : 1;
+  static_assert(KT % (64 * VEC) == 0, "K must be a multiple of 64 * VEC");
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row0 = (blockIdx.x * WAVES + wave) * RW;
+
+  float xv[M][NV][VEC];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int i = 0; i < VEC; i += 4) {
+        const size_t k = (size_t)(j * 64 + lane) * VEC + i;
+        float4 t = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + k);
+        if (PRO == PRO_ADDNORM) {
+          const float4 w = *reinterpret_cast<const float4*>(a.x2 + (size_t)m * a.ldx2 + k);
+          t.x += w.x; t.y += w.y; t.z += w.z; t.w += w.w;
+        }
+        xv[m][j][i] = t.x; xv[m][j][i + 1] = t.y; xv[m][j][i + 2] = t.z; xv[m][j][i + 3] = t.w;
+      }
+
+  // Small operands next (norm gains, residual / bias for this lane's
+  // outputs), so waiting on them never waits on the weight stream.
+  float gw[(PRO != PRO_NONE) ? NV : 1][VEC];
+  if (PRO != PRO_NONE) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int i = 0; i < VEC; i += 4) {
+        const float4 g = *reinterpret_cast<const float4*>(a.norm_w + (j * 64 + lane) * VEC + i);
+        gw[j][i] = g.x; gw[j][i + 1] = g.y; gw[j][i + 2] = g.z; gw[j][i + 3] = g.w;
+      }
+  }
+  float epi[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = min(row0 + r, a.N - 1);
+    const int m = lane < M ? lane : 0;
+    epi[r] = (EPI == EPI_BIAS) ? a.bias[n] : (EPI == EPI_RESID) ? a.res[(size_t)m * a.ldr + n] : 0.f;
+  }
+
+  float wv[RW][NS][NV][VEC];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = min(row0 + r, a.N - 1);
+    const void* base[NS];
+    size_t off;
+    if (EPI == EPI_SWIGLU) {
+      base[0] = a.w[0];
+      if (NS > 1) base[NS - 1] = a.w[1];
+      off = (size_t)n * KT;
+    } else {
+      int seg = 0, local = n;
+      while (seg < 2 && local >= a.seg_rows[seg]) { local -= a.seg_rows[seg]; ++seg; }
+      base[0] = a.w[seg];
+      off = (size_t)local * KT;
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) WL::load(base[s], off + (size_t)(j * 64 + lane) * VEC, wv[r][s][j]);
+  }
+
+  if (PRO != PRO_NONE) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) ss = fmaf(xv[m][j][i], xv[m][j][i], ss);
+      const float inv = 1.0f / sqrtf(wave_sum_dpp(ss) / (float)KT + a.eps);
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; i += 4) {
+          const int k = (j * 64 + lane) * VEC + i;
+          xv[m][j][i] = gw[j][i] * (xv[m][j][i] * inv);
+          xv[m][j][i + 1] = gw[j][i + 1] * (xv[m][j][i + 1] * inv);
+          xv[m][j][i + 2] = gw[j][i + 2] * (xv[m][j][i + 2] * inv);
+          xv[m][j][i + 3] = gw[j][i + 3] * (xv[m][j][i + 3] * inv);
+          if (a.norm_out && blockIdx.x == 0 && wave == 0)
+            *reinterpret_cast<float4*>(a.norm_out + (size_t)m * a.ldno + k) =
+                make_float4(xv[m][j][i], xv[m][j][i + 1], xv[m][j][i + 2], xv[m][j][i + 3]);
+        }
+    }
+  }
+
+  float acc[RW][NS][M];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) t = fmaf(wv[r][s][j][i], xv[m][j][i], t);
+        acc[r][s][m] = wave_sum_dpp(t);
+      }
+
+  if (lane < M) {
+    const int m = lane;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int n = row0 + r;
+      if (n >= a.N) continue;
+      float v = acc[r][0][0];
+#pragma unroll
+      for (int mm = 1; mm < M; ++mm)
+        if (mm == m) v = acc[r][0][mm];
+      float u = v;
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm)
+        if (mm == m) u = acc[r][NS - 1][mm];
+      if (EPI == EPI_BIAS || EPI == EPI_RESID) v += epi[r];
+      if (EPI == EPI_SWIGLU) v = v / (1.0f + expf(-v)) * u;
+      a.out[(size_t)m * a.ldo + n] = v;
+    }
+  }
+}
+
 // ------------------------------------------------------------ RMSNorm rows
 // out[b] = w * (x[b] (+ x2[b]) * 1/sqrt(mean(.^2) + eps)); grid = rows.
 // Rows with active[b] == 0 are left untouched (prefill of ragged rows).
@@ -259,108 +420,153 @@ __global__ __launch_bounds__(NT) void rmsnorm_rows_kernel(const float* x, const 
 // ------------------------------------------------------------ attention
 // One decode token per row against that row's own cache (per-row length and
 // RoPE position; CFG rows differ in length).  Grid (chunks, Hkv, rows); the
-// workgroup of chunk c handles KV tokens [c*64, c*64+64).  Each workgroup
-// applies q_norm/k_norm + RoPE itself (Qwen3 norms per head before RoPE); the
-// workgroup owning the new token also appends it to the cache.  Partial
-// (max, sum, o) per chunk go to scratch; the last workgroup of a (row, kv head)
-// to finish merges them in chunk order, so results do not depend on timing.
+// workgroup of chunk c handles KV tokens [c*32, c*32+32).
+//
+// Round trips are what cost here, so a workgroup issues every load that does
+// not depend on the row's length at entry: its raw q/k/v, norm gains and RoPE
+// frequencies first, then the K and V rows of its whole chunk (16 dims of one
+// token per lane).  The chunk rows are read speculatively (the cache is
+// allocated to max_ctx, so they are in bounds); tokens at or past the row's
+// length are masked once kv_len arrives.  Queries and the new key get Qwen3's
+// per-head RMSNorm then rotate-half RoPE with angle = fp32(pos * inv_freq)
+// and cos/sin evaluated in double, rounded once.  The workgroup owning the new
+// token appends it to the cache.  Partial (max, sum, o) per chunk go to
+// scratch, merged by attention_combine_kernel.
 struct AttnArgs {
   const float* qkv; int ldqkv;           // [rows][(Hq + 2 Hkv) hd] raw projections
   float* kc; float* vc;                  // this layer: [rows][Hkv][max_ctx][hd]
   const float* qn_w; const float* kn_w; float eps;
-  const float* rope_cos; const float* rope_sin;  // [max_ctx][hd/2]
+  const float* inv_freq;                 // [hd/2]
   const int* kv_len; const int* pos; const int* active;
-  float* part; int* counters;            // [rows][Hq][max_chunks][hd+2], [rows][Hkv]
+  float* part;                           // [rows][Hq][max_chunks][hd+2]
   float* out; int ldo;                   // [rows][Hq hd]
   int Hq, Hkv, hd, max_ctx, max_chunks;
   float scale;
 };
 
+constexpr int ATT_DPL = 16;  // head dims per lane
+
+__host__ __device__ constexpr size_t attn_smem_floats(int G, int hd) {
+  return ((size_t)G * hd + 2 * hd + (size_t)G * ATT_CHUNK + 2 * G + 3 * (hd / 2) + 2 * hd + 3) / 4 * 4 +
+         (size_t)ATT_CHUNK * hd;
+}
+
 __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
-  extern __shared__ float sm[];
+  extern __shared__ __attribute__((aligned(16))) float sm[];
   const int c = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
-  if (!a.active[r]) return;
-  const int T = a.kv_len[r];             // cached tokens; the new one goes to slot T
-  const int ctx = T + 1;
-  const int nch = (ctx + ATT_CHUNK - 1) / ATT_CHUNK;
-  if (c >= nch) return;
   const int G = a.Hq / a.Hkv, hd = a.hd, half = hd / 2;
-  const int p = a.pos[r];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const bool last = (c == nch - 1);
+  const int t_begin = c * ATT_CHUNK;
+  const size_t head_base = ((size_t)r * a.Hkv + h) * a.max_ctx;
 
   float* qs = sm;                        // [G][hd]
   float* knew = qs + G * hd;             // [hd]
   float* vnew = knew + hd;               // [hd]
   float* sc = vnew + hd;                 // [G][CHUNK]
   float* mls = sc + G * ATT_CHUNK;       // [G][2]
-  __shared__ int is_last;
+  float* fq = mls + 2 * G;               // [hd/2] inv_freq
+  float* fc = fq + half;                 // [hd/2] cos
+  float* fs = fc + half;                 // [hd/2] sin
+  float* qw = fs + half;                 // [hd] q_norm gain
+  float* kw = qw + hd;                   // [hd] k_norm gain
+  float* vs = sm + attn_smem_floats(G, hd) - (size_t)ATT_CHUNK * hd;  // [CHUNK][hd]
 
+  // Loads that do not depend on the row's length, small ones first.
+  const int T = a.kv_len[r];
+  const int p = a.pos[r];
+  const int act = a.active[r];
   const float* row = a.qkv + (size_t)r * a.ldqkv;
   for (int i = tid; i < G * hd; i += NT) qs[i] = row[(size_t)h * G * hd + i];
-  if (last)
-    for (int i = tid; i < hd; i += NT) {
-      knew[i] = row[(size_t)a.Hq * hd + (size_t)h * hd + i];
-      vnew[i] = row[(size_t)(a.Hq + a.Hkv) * hd + (size_t)h * hd + i];
+  for (int i = tid; i < hd; i += NT) {
+    knew[i] = row[(size_t)a.Hq * hd + (size_t)h * hd + i];
+    vnew[i] = row[(size_t)(a.Hq + a.Hkv) * hd + (size_t)h * hd + i];
+    qw[i] = a.qn_w[i];
+    kw[i] = a.kn_w[i];
+  }
+  for (int i = tid; i < half; i += NT) fq[i] = a.inv_freq[i];
+
+  const int LPT = hd / ATT_DPL;
+  const int TPP = NT / LPT;              // tokens per pass
+  const int npass = (ATT_CHUNK + TPP - 1) / TPP;
+  const int sub = tid % LPT;
+  float4 kr[ATT_DPL / 4], vr[ATT_DPL / 4];
+  {
+    const int t = t_begin + tid / LPT;
+    if (tid / LPT < ATT_CHUNK && t < a.max_ctx) {
+      const float4* kp = reinterpret_cast<const float4*>(a.kc + (head_base + t) * hd + sub * ATT_DPL);
+      const float4* vp = reinterpret_cast<const float4*>(a.vc + (head_base + t) * hd + sub * ATT_DPL);
+#pragma unroll
+      for (int i = 0; i < ATT_DPL / 4; ++i) { kr[i] = kp[i]; vr[i] = vp[i]; }
     }
+  }
+  const int ctx = T + 1;
+  const int nch = (ctx + ATT_CHUNK - 1) / ATT_CHUNK;
+  if (!act || c >= nch) return;
+  const bool last = (c == nch - 1);
+  const int n_t = min(ATT_CHUNK, ctx - t_begin);
+  for (int i = tid; i < half; i += NT) {
+    const float ang = (float)p * fq[i];
+    fc[i] = (float)cos((double)ang);
+    fs[i] = (float)sin((double)ang);
+  }
   __syncthreads();
 
   // Per-head RMSNorm over hd, then rotate-half RoPE; one wave per head.
   const int nheads = G + (last ? 1 : 0);
-  const float* cs = a.rope_cos + (size_t)p * half;
-  const float* sn = a.rope_sin + (size_t)p * half;
   for (int j = wave; j < nheads; j += WAVES) {
     float* v = (j < G) ? qs + j * hd : knew;
-    const float* w = (j < G) ? a.qn_w : a.kn_w;
+    const float* w = (j < G) ? qw : kw;
     float s = 0.f;
     for (int d = lane; d < hd; d += 64) s += v[d] * v[d];
     const float inv = 1.0f / sqrtf(wave_sum(s) / (float)hd + a.eps);
     for (int d = lane; d < half; d += 64) {
       const float x1 = w[d] * (v[d] * inv);
       const float x2 = w[d + half] * (v[d + half] * inv);
-      v[d] = x1 * cs[d] - x2 * sn[d];
-      v[d + half] = x2 * cs[d] + x1 * sn[d];
+      v[d] = x1 * fc[d] - x2 * fs[d];
+      v[d + half] = x2 * fc[d] + x1 * fs[d];
     }
   }
   __syncthreads();
-
-  const size_t head_base = ((size_t)r * a.Hkv + h) * a.max_ctx;
   if (last)
     for (int d = tid; d < hd; d += NT) {
       a.kc[(head_base + T) * hd + d] = knew[d];
       a.vc[(head_base + T) * hd + d] = vnew[d];
     }
 
-  // Scores: LPT lanes per token, 8 dims per lane.
-  const int LPT = hd / 8;
-  const int TPI = NT / LPT;
-  const int grp = tid / LPT, sub = tid % LPT;
-  const int t_begin = c * ATT_CHUNK;
-  const int n_t = min(ATT_CHUNK, ctx - t_begin);
-  for (int t0 = 0; t0 < ATT_CHUNK; t0 += TPI) {
-    const int tl = t0 + grp;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int tl = pass * TPP + tid / LPT;
     const int t = t_begin + tl;
-    float kv8[8];
-    if (tl < n_t) {
-      if (t == T) {
+    if (pass > 0 && tl < n_t && t < T) {
+      const float4* kp = reinterpret_cast<const float4*>(a.kc + (head_base + t) * hd + sub * ATT_DPL);
+      const float4* vp = reinterpret_cast<const float4*>(a.vc + (head_base + t) * hd + sub * ATT_DPL);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) kv8[j] = knew[sub * 8 + j];
-      } else {
-        const float4* kp = reinterpret_cast<const float4*>(a.kc + (head_base + t) * hd + sub * 8);
-        const float4 k0 = kp[0], k1 = kp[1];
-        kv8[0] = k0.x; kv8[1] = k0.y; kv8[2] = k0.z; kv8[3] = k0.w;
-        kv8[4] = k1.x; kv8[5] = k1.y; kv8[6] = k1.z; kv8[7] = k1.w;
+      for (int i = 0; i < ATT_DPL / 4; ++i) { kr[i] = kp[i]; vr[i] = vp[i]; }
+    }
+    if (tl < n_t && t == T) {
+#pragma unroll
+      for (int i = 0; i < ATT_DPL / 4; ++i) {
+        const int d = sub * ATT_DPL + 4 * i;
+        kr[i] = make_float4(knew[d], knew[d + 1], knew[d + 2], knew[d + 3]);
+        vr[i] = make_float4(vnew[d], vnew[d + 1], vnew[d + 2], vnew[d + 3]);
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kv8[j] = 0.f;
     }
     for (int g = 0; g < G; ++g) {
+      const float* qg = qs + g * hd + sub * ATT_DPL;
       float s = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s = fmaf(qs[g * hd + sub * 8 + j], kv8[j], s);
+      for (int i = 0; i < ATT_DPL / 4; ++i) {
+        s = fmaf(qg[4 * i], kr[i].x, s);
+        s = fmaf(qg[4 * i + 1], kr[i].y, s);
+        s = fmaf(qg[4 * i + 2], kr[i].z, s);
+        s = fmaf(qg[4 * i + 3], kr[i].w, s);
+      }
       for (int o = LPT / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
       if (sub == 0 && tl < n_t) sc[g * ATT_CHUNK + tl] = s * a.scale;
+    }
+    if (tl < n_t) {
+      float4* vd = reinterpret_cast<float4*>(vs + (size_t)tl * hd + sub * ATT_DPL);
+#pragma unroll
+      for (int i = 0; i < ATT_DPL / 4; ++i) vd[i] = vr[i];
     }
   }
   __syncthreads();
@@ -371,7 +577,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
     const float m = wave_max(v);
     const float e = (lane < n_t) ? expf(v - m) : 0.f;
     const float l = wave_sum(e);
-    sc[g * ATT_CHUNK + lane] = e;
+    if (lane < ATT_CHUNK) sc[g * ATT_CHUNK + lane] = e;
     if (lane == 0) { mls[2 * g] = m; mls[2 * g + 1] = l; }
   }
   __syncthreads();
@@ -380,38 +586,54 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   for (int i = tid; i < G * hd; i += NT) {
     const int g = i / hd, d = i - g * hd;
     float o = 0.f;
-    for (int tl = 0; tl < n_t; ++tl) {
-      const int t = t_begin + tl;
-      const float v = (t == T) ? vnew[d] : a.vc[(head_base + t) * hd + d];
-      o = fmaf(sc[g * ATT_CHUNK + tl], v, o);
-    }
+    for (int tl = 0; tl < n_t; ++tl) o = fmaf(sc[g * ATT_CHUNK + tl], vs[(size_t)tl * hd + d], o);
     float* pp = a.part + (((size_t)r * a.Hq + h * G + g) * a.max_chunks + c) * stride;
     pp[d] = o;
     if (d == 0) { pp[hd] = mls[2 * g]; pp[hd + 1] = mls[2 * g + 1]; }
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int old = atomicAdd(&a.counters[r * a.Hkv + h], 1);
-    is_last = (old == nch - 1);
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  for (int i = tid; i < G * hd; i += NT) {
-    const int g = i / hd, d = i - g * hd;
-    const float* pp = a.part + (((size_t)r * a.Hq + h * G + g) * a.max_chunks) * stride;
-    float M = -INFINITY;
-    for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, __builtin_nontemporal_load(&pp[cc * stride + hd]));
-    float L = 0.f, O = 0.f;
-    for (int cc = 0; cc < nch; ++cc) {
-      const float f = expf(__builtin_nontemporal_load(&pp[cc * stride + hd]) - M);
-      L = fmaf(__builtin_nontemporal_load(&pp[cc * stride + hd + 1]), f, L);
-      O = fmaf(__builtin_nontemporal_load(&pp[cc * stride + d]), f, O);
+}
+
+// Merge the chunk partials of one (row, q head) in chunk order: one thread
+// per head dim.  The partials of up to 16 chunks are loaded together with
+// kv_len (speculatively, in bounds) and masked once the chunk count is known.
+// A kernel of its own, so the partials need no device-scope fence.
+__global__ __launch_bounds__(512) void attention_combine_kernel(AttnArgs a) {
+  const int hq = blockIdx.x, r = blockIdx.y, d = threadIdx.x;
+  if (d >= a.hd) return;
+  const int hd = a.hd, stride = hd + 2;
+  const float* pp = a.part + ((size_t)r * a.Hq + hq) * a.max_chunks * stride;
+  constexpr int CB = 16;
+  const int T = a.kv_len[r];
+  const int act = a.active[r];
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int c0 = 0; c0 < a.max_chunks; c0 += CB) {
+    float mv[CB], lv[CB], ov[CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const int cc = min(c0 + j, a.max_chunks - 1);
+      mv[j] = pp[cc * stride + hd];
+      lv[j] = pp[cc * stride + hd + 1];
+      ov[j] = pp[cc * stride + d];
     }
-    a.out[(size_t)r * a.ldo + (size_t)(h * G + g) * hd + d] = O / L;
+    const int nch = (T + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
+    if (c0 >= nch) break;
+    float Mb = M;
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+      if (c0 + j < nch) Mb = fmaxf(Mb, mv[j]);
+    const float rescale = expf(M - Mb);   // 0 on the first block (M = -inf)
+    L *= rescale;
+    O *= rescale;
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+      if (c0 + j < nch) {
+        const float f = expf(mv[j] - Mb);
+        L = fmaf(lv[j], f, L);
+        O = fmaf(ov[j], f, O);
+      }
+    M = Mb;
   }
-  if (tid == 0) a.counters[r * a.Hkv + h] = 0;
+  if (act) a.out[(size_t)r * a.ldo + (size_t)hq * hd + d] = O / L;
 }
 
 // ------------------------------------------------------------ sampler
@@ -436,12 +658,63 @@ struct SampleSmem {
   int scan[WAVES];
   int n;
   int code;
-  uint32_t prefix;
   int sel_digit;
   int sel_excl;
+  int sel_cnt;
   float bv[WAVES];
   int bi[WAVES];
 };
+
+__device__ __forceinline__ bool before(float va, int ia, float vb, int ib) {
+  return (va > vb) || (va == vb && ia < ib);
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), lane);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+  return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+
+// Inverse-CDF draw over n <= 64 candidates (cv/ci in LDS, any order),
+// run by one wave.  Each lane ranks its candidate against all n (value desc,
+// index asc) and writes it to its sorted slot in LDS (sv/si, 64 entries);
+// then w_i = exp(x_i - x_0) in float64, W_i = sequential prefix sums in
+// candidate order, n_keep = first i with W_i > p * W_{n-1} plus one (top-p,
+// first always kept), and the code is the first candidate with
+// W_j > u * W_{n_keep-1}.
+__device__ int draw_wave(const float* cv, const int* ci, int n, float top_p, double u, float* sv,
+                         int* si) {
+  const int lane = threadIdx.x & 63;
+  float v = (lane < n) ? cv[lane] : -INFINITY;
+  int id = (lane < n) ? ci[lane] : 0x7fffffff;
+  int rank = 0;
+  for (int j = 0; j < n; ++j) {
+    const float vj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+    const int ij = __builtin_amdgcn_readlane(id, j);
+    rank += before(vj, ij, v, id) ? 1 : 0;
+  }
+  if (lane < n) { sv[rank] = v; si[rank] = id; }
+  __builtin_amdgcn_wave_barrier();
+  if (lane < n) { v = sv[lane]; id = si[lane]; }
+  const double top = (double)__shfl(v, 0, 64);
+  const double w = (lane < n) ? exp((double)v - top) : 0.0;
+  double acc = 0.0, Wl = 0.0;
+  for (int i = 0; i < n; ++i) {
+    acc += readlane_f64(w, i);
+    if (lane == i) Wl = acc;
+  }
+  int nk = n;
+  if (top_p > 0.f && top_p < 1.f) {
+    const double thr = (double)top_p * acc;
+    const unsigned long long b = __ballot(lane + 1 < n && Wl > thr);
+    if (b) nk = __ffsll((long long)b);
+  }
+  const double target = u * readlane_f64(Wl, nk - 1);
+  const unsigned long long b = __ballot(lane < nk && Wl > target);
+  const int j = b ? __ffsll((long long)b) - 1 : nk - 1;
+  return __shfl(id, j, 64);
+}
 
 // x[0..V) in LDS (already CFG-merged and masked).  Follows model.py:686-708:
 // greedy argmax when temperature <= 0; else x / T, top-k (ties kept), top-p
@@ -476,7 +749,9 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
   for (int v = tid; v < V; v += NT) x[v] = x[v] / temp;
   __syncthreads();
 
-  // k-th largest key by 8-bit radix select (MSB first).
+  // k-th largest key by 8-bit radix select (MSB first); stops early once
+  // the selected digit's bin holds exactly the remaining rank (then every
+  // key at or above that digit prefix is a top-k member).
   uint32_t cut = 0u;
   if (top_k > 0 && top_k < V) {
     uint32_t prefix = 0u, pmask = 0u;
@@ -501,12 +776,14 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
       __syncthreads();
       for (int w = 0; w < wave; ++w) incl += s.scan[w];
       const int excl = incl - cnt;
-      if (cnt > 0 && excl < kr && kr <= incl) { s.sel_digit = 255 - tid; s.sel_excl = excl; }
+      if (cnt > 0 && excl < kr && kr <= incl) { s.sel_digit = 255 - tid; s.sel_excl = excl; s.sel_cnt = cnt; }
       __syncthreads();
       prefix |= (uint32_t)s.sel_digit << shift;
       pmask |= 255u << shift;
       kr -= s.sel_excl;
+      const bool done = (s.sel_cnt == kr);
       __syncthreads();
+      if (done) break;
     }
     cut = prefix;
   }
@@ -522,11 +799,19 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
   }
   __syncthreads();
   const int n = s.n;
+  if (n <= 64) {
+    if (wave == 0) {
+      const int code = (n == 0) ? 0 : draw_wave(cv, ci, n, top_p, u, cv + 64, ci + 64);
+      if (lane == 0) s.code = code;
+    }
+    __syncthreads();
+    return s.code;
+  }
   int P = 1;
   while (P < n) P <<= 1;
   for (int i = n + tid; i < P; i += NT) { cv[i] = -INFINITY; ci[i] = 0x7fffffff; }
   __syncthreads();
-  // Bitonic sort: "before" = larger value, then smaller index.
+  // Bitonic sort in LDS: "before" = larger value, then smaller index.
   for (int k = 2; k <= P; k <<= 1)
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int i = tid; i < P; i += NT) {
@@ -534,9 +819,7 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
         if (l > i) {
           const float vi = cv[i], vl = cv[l];
           const int ii = ci[i], il = ci[l];
-          const bool l_before = (vl > vi) || (vl == vi && il < ii);
-          const bool i_before = (vi > vl) || (vi == vl && ii < il);
-          const bool swap = ((i & k) == 0) ? l_before : i_before;
+          const bool swap = ((i & k) == 0) ? before(vl, il, vi, ii) : before(vi, ii, vl, il);
           if (swap) { cv[i] = vl; cv[l] = vi; ci[i] = il; ci[l] = ii; }
         }
       }
@@ -545,15 +828,14 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
   const double top = (double)cv[0];
   for (int i = tid; i < n; i += NT) W[i] = exp((double)cv[i] - top);
   __syncthreads();
-  if (tid == 0 && n == 0) s.code = 0;  // no finite logit (non-finite input): fixed, in-range code
-  if (tid == 0 && n > 0) {
+  if (tid == 0) {
     double acc = 0.0;
     for (int i = 0; i < n; ++i) { acc += W[i]; W[i] = acc; }
     int nk = n;
     if (top_p > 0.f && top_p < 1.f) {
-      const double pp = (double)top_p;
+      const double thr = (double)top_p * acc;
       for (int i = 0; i + 1 < n; ++i)
-        if (W[i] / acc > pp) { nk = i + 1; break; }
+        if (W[i] > thr) { nk = i + 1; break; }
     }
     const double target = u * W[nk - 1];
     int j = nk - 1;
@@ -566,15 +848,25 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
 }
 
 // CFG merge u + s (c - u) without contraction, then BOS/PAD (and EOS) -> -inf
-// (model.py:579-584).
+// (model.py:579-584), into x[] in LDS.  Logits loads are issued first.
+constexpr int SAMPLE_VPT = MAX_V / NT;   // logits per thread
 __device__ __forceinline__ void merge_mask(const float* lc, const float* lu, float s, int V,
-                                           int bos, int eos, int pad, bool mask_eos, float* x) {
-  for (int v = threadIdx.x; v < V; v += NT) {
-    float m = lc[v];
-    if (lu) {
-      const float uu = lu[v];
-      m = __fadd_rn(uu, __fmul_rn(s, __fsub_rn(m, uu)));
-    }
+                                           int bos, int eos, int pad, const int* mask_flag,
+                                           bool force_mask, float* x) {
+  float cvv[SAMPLE_VPT], uvv[SAMPLE_VPT];
+#pragma unroll
+  for (int i = 0; i < SAMPLE_VPT; ++i) {
+    const int v = threadIdx.x + i * NT;
+    cvv[i] = (v < V) ? lc[v] : 0.f;
+    uvv[i] = (lu && v < V) ? lu[v] : 0.f;
+  }
+  const bool mask_eos = force_mask || (mask_flag && *mask_flag != 0);
+#pragma unroll
+  for (int i = 0; i < SAMPLE_VPT; ++i) {
+    const int v = threadIdx.x + i * NT;
+    if (v >= V) break;
+    float m = cvv[i];
+    if (lu) m = __fadd_rn(uvv[i], __fmul_rn(s, __fsub_rn(m, uvv[i])));
     if (v == bos || v == pad || (mask_eos && v == eos)) m = -INFINITY;
     x[v] = m;
   }
@@ -584,10 +876,11 @@ struct SampleArgs {
   const float* logits; int ldl; int rows_per_utt; int V;
   const SkParams* params;
   const int* fc;                       // device frame counter -> ring slot
-  const double* u_ring;                // [frames][n_utts][Q]
-  const int* flag_ring;                // [frames][2] (mask_eos_q0, forced)
+  const double* u_cur;                 // [n_utts][Q] this frame's draws
+  const int* flag_cur;                 // [2] this frame's (mask_eos_q0, forced)
   const int64_t* forced_ring;          // [frames][n_utts][Q]
   int64_t* codes_ring;                 // [frames][n_utts][Q]
+  int* codes_cur;                      // [n_utts][Q] this frame's codes
   float* dbg;                          // [n_utts][Q][V]
   const void* table;                   // [Q][V][d]
   float* prefix; float* xnext;         // [rows][d]
@@ -599,7 +892,9 @@ struct SampleArgs {
 // One workgroup per utterance, launched once per codebook q.  Samples the
 // code, records it, advances both rows' prefix (model.py:600-605) and, after
 // the last codebook, writes the frame embedding (model.py:105-114) as the next
-// trunk input and clears the prefix.
+// trunk input and clears the prefix.  Every input that does not depend on the
+// code is loaded in the first round trip (this frame's draws and flags sit at
+// fixed addresses, so nothing waits on the frame counter).
 template <typename TL>
 __global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
   extern __shared__ unsigned char raw[];
@@ -608,17 +903,19 @@ __global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
   float* cv = x + MAX_V;
   int* ci = reinterpret_cast<int*>(cv + MAX_V);
   __shared__ SampleSmem s;
-  __shared__ int64_t codes_l[64];
+  __shared__ int codes_l[64];
 
   const int ut = blockIdx.x;
-  const SkParams P = *a.params;
-  const int slot = *a.fc;
-  const int* flags = a.flag_ring + 2 * slot;
   const int r0 = ut * a.rows_per_utt;
   const float* lc = a.logits + (size_t)r0 * a.ldl;
   const float* lu = (a.rows_per_utt == 2) ? lc + a.ldl : nullptr;
-  const bool mask_eos = (q != 0) || flags[0] != 0;
-  merge_mask(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, mask_eos, x);
+  const double u = a.u_cur[(size_t)ut * a.Q + q];
+  const int forced = a.flag_cur[1];
+  const int slot = *a.fc;
+  const SkParams P = *a.params;
+  if (q + 1 == a.Q && threadIdx.x < a.Q && threadIdx.x != q)
+    codes_l[threadIdx.x] = a.codes_cur[(size_t)ut * a.Q + threadIdx.x];
+  merge_mask(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, a.flag_cur, q != 0, x);
   __syncthreads();
   if (P.record_logits)
     for (int v = threadIdx.x; v < a.V; v += NT)
@@ -627,11 +924,14 @@ __global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
   const float temp = q0 ? P.temperature_q0 : P.temperature;
   const int topk = q0 ? P.top_k_q0 : P.top_k;
   const float topp = q0 ? P.top_p_q0 : P.top_p;
+  int code = sample_core(x, a.V, temp, topk, topp, u, cv, ci, W, s);
   const size_t uoff = ((size_t)slot * a.n_utts + ut) * a.Q + q;
-  int code = sample_core(x, a.V, temp, topk, topp, a.u_ring[uoff], cv, ci, W, s);
-  if (flags[1]) code = (int)a.forced_ring[uoff];
+  if (forced) code = (int)a.forced_ring[uoff];
   code = min(max(code, 0), a.V - 1);
-  if (threadIdx.x == 0) a.codes_ring[uoff] = code;
+  if (threadIdx.x == 0) {
+    a.codes_ring[uoff] = code;
+    a.codes_cur[(size_t)ut * a.Q + q] = code;
+  }
 
   const size_t row_stride = (size_t)a.V * a.d;
   if (q + 1 < a.Q) {
@@ -644,15 +944,20 @@ __global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
       }
     }
   } else {
-    if (threadIdx.x < a.Q)
-      codes_l[threadIdx.x] = (threadIdx.x == q) ? (int64_t)code
-                                                : a.codes_ring[((size_t)slot * a.n_utts + ut) * a.Q + threadIdx.x];
+    if (threadIdx.x == 0) codes_l[q] = code;
     __syncthreads();
     for (int dd = threadIdx.x; dd < a.d; dd += NT) {
       float e = 0.f;
-      for (int j = 0; j < a.Q; ++j) {
-        const float t = TL::get(a.table, (size_t)j * row_stride + (size_t)codes_l[j] * a.d + dd);
-        e = (j == 0) ? t : __fadd_rn(e, t);
+      for (int j0 = 0; j0 < a.Q; j0 += 16) {
+        float t[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          t[j] = (j0 + j < a.Q)
+                     ? TL::get(a.table, (size_t)(j0 + j) * row_stride + (size_t)codes_l[j0 + j] * a.d + dd)
+                     : 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (j0 + j < a.Q) e = (j0 + j == 0) ? t[j] : __fadd_rn(e, t[j]);
       }
       e = __fmul_rn(e, a.scale);
       for (int rr = 0; rr < a.rows_per_utt; ++rr) {
@@ -674,7 +979,7 @@ __global__ __launch_bounds__(NT) void sample_op_kernel(const float* logits, int 
   float* cv = x + MAX_V;
   int* ci = reinterpret_cast<int*>(cv + MAX_V);
   __shared__ SampleSmem s;
-  merge_mask(logits, rows == 2 ? logits + V : nullptr, cfg, V, bos, eos, pad,
+  merge_mask(logits, rows == 2 ? logits + V : nullptr, cfg, V, bos, eos, pad, nullptr,
              (q != 0) || mask_eos_q0 != 0, x);
   __syncthreads();
   const int code = sample_core(x, V, temp, top_k, top_p, u, cv, ci, W, s);
@@ -684,12 +989,16 @@ __global__ __launch_bounds__(NT) void sample_op_kernel(const float* logits, int 
 constexpr size_t SAMPLE_SMEM = (size_t)MAX_V * (sizeof(double) + 2 * sizeof(float) + sizeof(int));
 
 // ------------------------------------------------------------ small kernels
-// Final trunk norm + per-row step bookkeeping.  mode 0: decode frame (every
-// row advances, frame counter += 1); mode 1: prefill token (active rows only,
-// prefill step += 1).
+// Final trunk norm + per-row step bookkeeping.  Decode (ring != null): every
+// row advances, the frame counter moves on and the next frame's draws and
+// flags are copied from the ring to the fixed current-frame slots.  Prefill
+// (ring == null): active rows only, the prefill step moves on.
 __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const float* w, float eps,
                                                         int D, float* hidden, int* kv_len, int* pos,
-                                                        const int* active, int* counter) {
+                                                        const int* active, int* counter,
+                                                        const double* u_ring, const int* flag_ring,
+                                                        double* u_cur, int* flag_cur, int nq,
+                                                        int max_frames) {
   __shared__ float red[WAVES];
   const int b = blockIdx.x;
   if (active[b]) {
@@ -700,7 +1009,15 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
     for (int k = threadIdx.x; k < D; k += NT) hidden[(size_t)b * D + k] = w[k] * (xr[k] * inv);
     if (threadIdx.x == 0) { kv_len[b] += 1; pos[b] += 1; }
   }
-  if (b == 0 && threadIdx.x == 0) *counter += 1;
+  if (b == 0) {
+    const int next = *counter + 1;
+    __syncthreads();
+    if (threadIdx.x == 0) *counter = next;
+    if (u_ring && next < max_frames) {
+      for (int i = threadIdx.x; i < nq; i += NT) u_cur[i] = u_ring[(size_t)next * nq + i];
+      if (threadIdx.x < 2) flag_cur[threadIdx.x] = flag_ring[2 * next + threadIdx.x];
+    }
+  }
 }
 
 // Prefill token t = *step: row b takes embeds[b][t] if t < len[b].

@@ -37,10 +37,69 @@ static hipError_t launch_gemv_m(int M, const GemvArgs& a, hipStream_t st) {
   }
 }
 
+// ---- compile-time-K GEMV (all of a wave's loads issued up front) ----------
+template <int M, int KT, int RW, int PRO, int EPI, typename WL>
+static hipError_t launch_fast_t(const GemvArgs& a, hipStream_t st) {
+  constexpr int NS = (EPI == EPI_SWIGLU) ? 2 : 1;
+  constexpr int NV = KT / (64 * WL::VEC);
+  if constexpr (RW > 1 && RW * NS * NV > 16) {
+    return launch_fast_t<M, KT, RW / 2, PRO, EPI, WL>(a, st);
+  } else {
+    const int grid = (a.N + WAVES * RW - 1) / (WAVES * RW);
+    hipLaunchKernelGGL((gemv_fast_kernel<M, KT, RW, PRO, EPI, WL>), dim3(grid), dim3(NT), 0, st, a);
+    return hipGetLastError();
+  }
+}
+
+// Rows per wave: as many as keep <= 16 loads per lane in flight while the
+// grid still has >= 256 workgroups (one per CU).
+template <int M, int KT, int PRO, int EPI, typename WL>
+static hipError_t launch_fast_k(const GemvArgs& a, hipStream_t st) {
+  constexpr int NS = (EPI == EPI_SWIGLU) ? 2 : 1;
+  constexpr int NV = KT / (64 * WL::VEC);
+  int rw = 4;
+  while (rw > 1 && (rw * NS * NV > 16 || a.N / (WAVES * rw) < 256)) rw /= 2;
+  switch (rw) {
+    case 4: return launch_fast_t<M, KT, 4, PRO, EPI, WL>(a, st);
+    case 2: return launch_fast_t<M, KT, 2, PRO, EPI, WL>(a, st);
+    default: return launch_fast_t<M, KT, 1, PRO, EPI, WL>(a, st);
+  }
+}
+
+// K values with a specialised kernel: the decode shapes' hidden sizes for
+// GEMVs fed by a norm / SwiGLU / classifier, and the inner sizes for the
+// down / output projections.  Returns false when no specialisation applies.
+template <int M, int PRO, int EPI, typename WL>
+static bool launch_fast(const GemvArgs& a, hipStream_t st, hipError_t* err) {
+  if constexpr (PRO == PRO_NONE && EPI == EPI_RESID) {
+    switch (a.K) {
+      case 2048: *err = launch_fast_k<M, 2048, PRO, EPI, WL>(a, st); return true;
+      case 3072: *err = launch_fast_k<M, 3072, PRO, EPI, WL>(a, st); return true;
+      case 4096: *err = launch_fast_k<M, 4096, PRO, EPI, WL>(a, st); return true;
+      case 6144: *err = launch_fast_k<M, 6144, PRO, EPI, WL>(a, st); return true;
+      default: return false;
+    }
+  } else {
+    switch (a.K) {
+      case 1024: *err = launch_fast_k<M, 1024, PRO, EPI, WL>(a, st); return true;
+      case 2048: *err = launch_fast_k<M, 2048, PRO, EPI, WL>(a, st); return true;
+      default: return false;
+    }
+  }
+}
+
+template <int PRO, int EPI, typename WL>
+static hipError_t launch_gemv_w(int M, const GemvArgs& a, hipStream_t st) {
+  hipError_t err = hipSuccess;
+  if (M == 1 && launch_fast<1, PRO, EPI, WL>(a, st, &err)) return err;
+  if (M == 2 && launch_fast<2, PRO, EPI, WL>(a, st, &err)) return err;
+  return launch_gemv_m<PRO, EPI, WL>(M, a, st);
+}
+
 template <int PRO, int EPI>
 static hipError_t launch_gemv(int wdtype, int M, const GemvArgs& a, hipStream_t st) {
-  return wdtype == SK_BF16 ? launch_gemv_m<PRO, EPI, WBF16>(M, a, st)
-                           : launch_gemv_m<PRO, EPI, WF32>(M, a, st);
+  return wdtype == SK_BF16 ? launch_gemv_w<PRO, EPI, WBF16>(M, a, st)
+                           : launch_gemv_w<PRO, EPI, WF32>(M, a, st);
 }
 
 static inline GemvArgs gemv_args(const void* w, int N, int K, const float* x, int ldx, float* out,

@@ -18,7 +18,8 @@ pick the same code:
 
 1. candidates = finite values that survive top-k, ordered by value
    descending, ties by lower index first;
-2. ``w_i = exp(x_i - x_0)`` in float64, ``W_i`` = sequential prefix sums;
+2. ``w_i = exp(x_i - x_0)`` in float64, ``W_i`` = prefix sums in a fixed
+   order (``scan_sums``: 64-wide Hillis-Steele groups plus a running carry);
 3. top-p keeps the leading candidates up to and including the first i with
    ``W_i > p * W_{n-1}`` (all n if none; p taken as an FP32 value promoted to
    float64, the product rounded once), i.e. ``cum > p`` shifted right by one;
@@ -71,12 +72,32 @@ def candidates(x, top_k):
     return idx[np.lexsort((idx, -x[idx].astype(np.float64)))]
 
 
+def scan_sums(w) -> np.ndarray:
+    """Inclusive float64 prefix sums in the fixed order both sides use:
+    groups of 64 candidates, each scanned Hillis-Steele style (offsets 1, 2,
+    4, ..., 32, every step adding the pre-step neighbour), plus the running
+    total of the earlier groups (carry + group scan, one rounding)."""
+    w = np.asarray(w, np.float64)
+    n = w.size
+    out = np.empty(n, np.float64)
+    carry = 0.0
+    for g0 in range(0, n, 64):
+        m = min(64, n - g0)
+        blk = np.zeros(64, np.float64)
+        blk[:m] = w[g0:g0 + m]
+        for off in (1, 2, 4, 8, 16, 32):
+            blk[off:] = blk[off:] + blk[:-off]
+        out[g0:g0 + m] = carry + blk[:m]
+        carry = carry + blk[63]
+    return out
+
+
 def topp_weights(vals, top_p):
-    """float64 weights, sequential prefix sums and the kept count
-    (model.py:700-706 restated in float64)."""
+    """float64 weights, prefix sums and the kept count (model.py:700-706
+    restated in float64)."""
     v = np.asarray(vals, np.float32).astype(np.float64)
     w = np.exp(v - v[0])
-    W = np.add.accumulate(w)
+    W = scan_sums(w)
     n = v.size
     n_keep = n
     if top_p is not None and 0 < top_p < 1:

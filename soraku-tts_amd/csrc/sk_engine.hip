@@ -101,8 +101,8 @@ int validate_config(const sk_config* c) {
   SK_CHECK(c->n_q_heads > 0 && c->n_kv_heads > 0 && c->n_q_heads % c->n_kv_heads == 0, SK_EINVAL,
            "n_q_heads must be a positive multiple of n_kv_heads");
   const int hd = c->head_dim;
-  SK_CHECK(hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256 || hd == 512,
-           SK_EINVAL, "head_dim must be a power of two in [16, 512]");
+  SK_CHECK(hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256,
+           SK_EINVAL, "head_dim must be a power of two in [16, 256]");
   SK_CHECK(c->trunk_inter > 0 && c->trunk_inter % 8 == 0, SK_EINVAL, "trunk_inter must be a positive multiple of 8");
   SK_CHECK(c->depth_inner > 0 && c->depth_inner % 8 == 0, SK_EINVAL, "depth_inner must be a positive multiple of 8");
   SK_CHECK(c->n_codebooks > 0 && c->n_codebooks <= 64, SK_EINVAL, "n_codebooks must be in [1, 64]");
@@ -120,7 +120,8 @@ int validate_config(const sk_config* c) {
   SK_CHECK(c->max_ctx >= 2 && c->max_ctx <= 65536, SK_EINVAL, "max_ctx must be in [2, 65536]");
   SK_CHECK(c->max_frames >= 1, SK_EINVAL, "max_frames must be positive");
   SK_CHECK(c->n_language == 0 || c->n_language == 4, SK_EINVAL, "n_language must be 0 or 4");
-  SK_CHECK((c->n_q_heads / c->n_kv_heads) * hd <= 4096, SK_EINVAL, "GQA group too large");
+  SK_CHECK((c->n_q_heads / c->n_kv_heads) * hd <= 256 && c->n_q_heads / c->n_kv_heads <= 8, SK_EINVAL,
+           "GQA group too large (<= 8 q heads per kv head, q heads x head_dim <= 256)");
   return SK_OK;
 }
 
@@ -172,17 +173,16 @@ hipError_t enqueue_trunk(sk_engine* e) {
     at.vc = e->vc + (size_t)l * kv_layer_elems(e);
     at.qn_w = w.q_norm; at.kn_w = w.k_norm; at.eps = c.trunk_eps;
     at.inv_freq = e->inv_freq;
+    at.part = e->part; at.max_chunks = e->max_chunks;
     at.kv_len = e->kv_len; at.pos = e->pos; at.active = e->active;
-    at.part = e->part;
     at.out = e->attn; at.ldo = c.n_q_heads * hd;
     at.Hq = c.n_q_heads; at.Hkv = c.n_kv_heads; at.hd = hd; at.max_ctx = c.max_ctx;
-    at.max_chunks = e->max_chunks;
     at.scale = 1.0f / sqrtf((float)hd);
     const size_t asmem = attn_smem_floats(e->G, hd) * sizeof(float);
     hipLaunchKernelGGL(attention_kernel, dim3(e->max_chunks, c.n_kv_heads, M), dim3(NT), asmem,
                        e->stream, at);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(c.n_q_heads, M), dim3(hd), 0, e->stream, at);
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(c.n_q_heads, M), dim3(NT), 0, e->stream, at);
     if ((err = hipGetLastError()) != hipSuccess) return err;
 
     a = gemv_args(w.o, d, c.n_q_heads * hd, e->attn, c.n_q_heads * hd, e->x, d);
@@ -369,6 +369,10 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   e->p_host.temperature = 0.0f;
   if (he == hipSuccess) he = hipMemcpy(e->params, &e->p_host, sizeof(SkParams), hipMemcpyHostToDevice);
   if (he == hipSuccess) he = prepare_sampler();
+  if (he == hipSuccess)
+    he = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)(attn_smem_floats(e->G, c.head_dim) * sizeof(float)));
   if (he != hipSuccess) { fail(SK_EHIP, "engine init: %s", hipGetErrorString(he)); return bail(SK_EHIP); }
   *out = e;
   return SK_OK;

@@ -444,13 +444,47 @@ struct AttnArgs {
   float scale;
 };
 
-constexpr int ATT_DPL = 16;  // head dims per lane
+constexpr int ATT_DPL = 16;      // head dims per lane
 
 __host__ __device__ constexpr size_t attn_smem_floats(int G, int hd) {
-  return ((size_t)G * hd + 2 * hd + (size_t)G * ATT_CHUNK + 2 * G + 3 * (hd / 2) + 2 * hd + 3) / 4 * 4 +
+  return ((size_t)G * hd + 4 * (size_t)hd + 3 * (size_t)(hd / 2) + (size_t)G * ATT_CHUNK + (size_t)G * 2 + 3) /
+             4 * 4 +
          (size_t)ATT_CHUNK * hd;
 }
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_keep(float v) {   // disabled lanes keep v
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_keep<0xb1, 0xf>(v));
+  v = fmaxf(v, dpp_keep<0x4e, 0xf>(v));
+  v = fmaxf(v, dpp_keep<0x114, 0xf>(v));
+  v = fmaxf(v, dpp_keep<0x118, 0xf>(v));
+  v = fmaxf(v, dpp_keep<0x142, 0xa>(v));
+  v = fmaxf(v, dpp_keep<0x143, 0xc>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// Sum over each aligned group of `lpt` lanes (1..16); valid in the group's
+// first lane.
+__device__ __forceinline__ float group_sum_first(float v, int lpt) {
+  if (lpt >= 2) v += dpp<0xb1, 0xf, true>(v);   // quad_perm [1,0,3,2]
+  if (lpt >= 4) v += dpp<0x4e, 0xf, true>(v);   // quad_perm [2,3,0,1]
+  if (lpt >= 8) v += dpp<0x12c, 0xf, true>(v);  // row_ror:12 (lane i reads lane i+4 of its row)
+  if (lpt >= 16) v += dpp<0x128, 0xf, true>(v); // row_ror:8  (lane i reads lane i+8 of its row)
+  return v;
+}
+
+// Grid (chunks, Hkv, rows); the workgroup of chunk c handles KV tokens
+// [c*32, c*32+32) of one (row, kv head) and writes that chunk's (o, max, sum)
+// for the G query heads; attention_combine_kernel merges the chunks.  Every
+// load that does not depend on the row's length is issued at entry: raw
+// q/k/v, norm gains, RoPE frequencies, then the chunk's K and V rows (16 dims
+// of one token per lane; in bounds because the cache is allocated to max_ctx)
+// -- tokens at or past the length are masked once kv_len arrives.  Queries
+// and the new key get Qwen3's per-head RMSNorm then rotate-half RoPE with
+// angle = fp32(pos * inv_freq) and cos/sin evaluated in double, rounded once;
+// the workgroup owning the new token appends its K/V to the cache.
 __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int c = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
@@ -462,16 +496,15 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   float* qs = sm;                        // [G][hd]
   float* knew = qs + G * hd;             // [hd]
   float* vnew = knew + hd;               // [hd]
-  float* sc = vnew + hd;                 // [G][CHUNK]
-  float* mls = sc + G * ATT_CHUNK;       // [G][2]
-  float* fq = mls + 2 * G;               // [hd/2] inv_freq
-  float* fc = fq + half;                 // [hd/2] cos
-  float* fs = fc + half;                 // [hd/2] sin
-  float* qw = fs + half;                 // [hd] q_norm gain
+  float* qw = vnew + hd;                 // [hd] q_norm gain
   float* kw = qw + hd;                   // [hd] k_norm gain
+  float* fq = kw + hd;                   // [hd/2] inv_freq
+  float* fcs = fq + half;                // [hd/2] cos
+  float* fsn = fcs + half;               // [hd/2] sin
+  float* sc = fsn + half;                // [G][CHUNK]
+  float* st = sc + G * ATT_CHUNK;        // [G][2]
   float* vs = sm + attn_smem_floats(G, hd) - (size_t)ATT_CHUNK * hd;  // [CHUNK][hd]
 
-  // Loads that do not depend on the row's length, small ones first.
   const int T = a.kv_len[r];
   const int p = a.pos[r];
   const int act = a.active[r];
@@ -488,17 +521,19 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   const int LPT = hd / ATT_DPL;
   const int TPP = NT / LPT;              // tokens per pass
   const int npass = (ATT_CHUNK + TPP - 1) / TPP;
-  const int sub = tid % LPT;
+  const int sub = tid % LPT, tok = tid / LPT;
   float4 kr[ATT_DPL / 4], vr[ATT_DPL / 4];
-  {
-    const int t = t_begin + tid / LPT;
-    if (tid / LPT < ATT_CHUNK && t < a.max_ctx) {
+  auto load_tok = [&](int pass) {
+    const int tl = pass * TPP + tok;
+    const int t = t_begin + tl;
+    if (tl < ATT_CHUNK && t < a.max_ctx) {
       const float4* kp = reinterpret_cast<const float4*>(a.kc + (head_base + t) * hd + sub * ATT_DPL);
       const float4* vp = reinterpret_cast<const float4*>(a.vc + (head_base + t) * hd + sub * ATT_DPL);
 #pragma unroll
       for (int i = 0; i < ATT_DPL / 4; ++i) { kr[i] = kp[i]; vr[i] = vp[i]; }
     }
-  }
+  };
+  load_tok(0);
   const int ctx = T + 1;
   const int nch = (ctx + ATT_CHUNK - 1) / ATT_CHUNK;
   if (!act || c >= nch) return;
@@ -506,11 +541,10 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   const int n_t = min(ATT_CHUNK, ctx - t_begin);
   for (int i = tid; i < half; i += NT) {
     const float ang = (float)p * fq[i];
-    fc[i] = (float)cos((double)ang);
-    fs[i] = (float)sin((double)ang);
+    fcs[i] = (float)cos((double)ang);
+    fsn[i] = (float)sin((double)ang);
   }
   __syncthreads();
-
   // Per-head RMSNorm over hd, then rotate-half RoPE; one wave per head.
   const int nheads = G + (last ? 1 : 0);
   for (int j = wave; j < nheads; j += WAVES) {
@@ -518,12 +552,12 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
     const float* w = (j < G) ? qw : kw;
     float s = 0.f;
     for (int d = lane; d < hd; d += 64) s += v[d] * v[d];
-    const float inv = 1.0f / sqrtf(wave_sum(s) / (float)hd + a.eps);
+    const float inv = 1.0f / sqrtf(wave_sum_dpp(s) / (float)hd + a.eps);
     for (int d = lane; d < half; d += 64) {
       const float x1 = w[d] * (v[d] * inv);
       const float x2 = w[d + half] * (v[d + half] * inv);
-      v[d] = x1 * fc[d] - x2 * fs[d];
-      v[d + half] = x2 * fc[d] + x1 * fs[d];
+      v[d] = x1 * fcs[d] - x2 * fsn[d];
+      v[d + half] = x2 * fcs[d] + x1 * fsn[d];
     }
   }
   __syncthreads();
@@ -534,14 +568,9 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
     }
 
   for (int pass = 0; pass < npass; ++pass) {
-    const int tl = pass * TPP + tid / LPT;
+    const int tl = pass * TPP + tok;
     const int t = t_begin + tl;
-    if (pass > 0 && tl < n_t && t < T) {
-      const float4* kp = reinterpret_cast<const float4*>(a.kc + (head_base + t) * hd + sub * ATT_DPL);
-      const float4* vp = reinterpret_cast<const float4*>(a.vc + (head_base + t) * hd + sub * ATT_DPL);
-#pragma unroll
-      for (int i = 0; i < ATT_DPL / 4; ++i) { kr[i] = kp[i]; vr[i] = vp[i]; }
-    }
+    if (pass > 0) load_tok(pass);
     if (tl < n_t && t == T) {
 #pragma unroll
       for (int i = 0; i < ATT_DPL / 4; ++i) {
@@ -560,36 +589,37 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
         s = fmaf(qg[4 * i + 2], kr[i].z, s);
         s = fmaf(qg[4 * i + 3], kr[i].w, s);
       }
-      for (int o = LPT / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+      s = group_sum_first(s, LPT);
       if (sub == 0 && tl < n_t) sc[g * ATT_CHUNK + tl] = s * a.scale;
     }
-    if (tl < n_t) {
+    if (tl < ATT_CHUNK) {
       float4* vd = reinterpret_cast<float4*>(vs + (size_t)tl * hd + sub * ATT_DPL);
+      const bool ok = tl < n_t;
 #pragma unroll
-      for (int i = 0; i < ATT_DPL / 4; ++i) vd[i] = vr[i];
+      for (int i = 0; i < ATT_DPL / 4; ++i) vd[i] = ok ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
   __syncthreads();
-
   // Chunk softmax statistics: one wave per q head, one lane per token.
   for (int g = wave; g < G; g += WAVES) {
     const float v = (lane < n_t) ? sc[g * ATT_CHUNK + lane] : -INFINITY;
-    const float m = wave_max(v);
+    const float m = wave_max_dpp(v);
     const float e = (lane < n_t) ? expf(v - m) : 0.f;
-    const float l = wave_sum(e);
+    const float l = wave_sum_dpp(e);
     if (lane < ATT_CHUNK) sc[g * ATT_CHUNK + lane] = e;
-    if (lane == 0) { mls[2 * g] = m; mls[2 * g + 1] = l; }
+    if (lane == 0) { st[2 * g] = m; st[2 * g + 1] = l; }
   }
   __syncthreads();
-
   const int stride = hd + 2;
   for (int i = tid; i < G * hd; i += NT) {
     const int g = i / hd, d = i - g * hd;
+    const float* eg = sc + g * ATT_CHUNK;
     float o = 0.f;
-    for (int tl = 0; tl < n_t; ++tl) o = fmaf(sc[g * ATT_CHUNK + tl], vs[(size_t)tl * hd + d], o);
+#pragma unroll 8
+    for (int tl = 0; tl < ATT_CHUNK; ++tl) o = fmaf(eg[tl], vs[(size_t)tl * hd + d], o);
     float* pp = a.part + (((size_t)r * a.Hq + h * G + g) * a.max_chunks + c) * stride;
     pp[d] = o;
-    if (d == 0) { pp[hd] = mls[2 * g]; pp[hd + 1] = mls[2 * g + 1]; }
+    if (d == 0) { pp[hd] = st[2 * g]; pp[hd + 1] = st[2 * g + 1]; }
   }
 }
 
@@ -597,7 +627,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
 // per head dim.  The partials of up to 16 chunks are loaded together with
 // kv_len (speculatively, in bounds) and masked once the chunk count is known.
 // A kernel of its own, so the partials need no device-scope fence.
-__global__ __launch_bounds__(512) void attention_combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   const int hq = blockIdx.x, r = blockIdx.y, d = threadIdx.x;
   if (d >= a.hd) return;
   const int hd = a.hd, stride = hd + 2;
@@ -654,9 +684,9 @@ __device__ __forceinline__ uint32_t fkey(float f) {
 }
 
 struct SampleSmem {
-  int hist[256];
+  int hist[WAVES][8][256];   // radix histograms, private per (wave, lane & 7)
   int scan[WAVES];
-  int n;
+  int wcount[WAVES];
   int code;
   int sel_digit;
   int sel_excl;
@@ -669,6 +699,34 @@ __device__ __forceinline__ bool before(float va, int ia, float vb, int ib) {
   return (va > vb) || (va == vb && ia < ib);
 }
 
+template <int CTRL, int ROW_MASK, bool BOUND0>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, BOUND0);
+}
+// Inclusive prefix sum of an int over the 64 lanes (DPP row shifts + row broadcasts).
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += dpp_i<0x111, 0xf, true>(x);   // row_shr:1
+  x += dpp_i<0x112, 0xf, true>(x);   // row_shr:2
+  x += dpp_i<0x114, 0xf, true>(x);   // row_shr:4
+  x += dpp_i<0x118, 0xf, true>(x);   // row_shr:8
+  x += dpp_i<0x142, 0xa, false>(x);  // row_bcast:15
+  x += dpp_i<0x143, 0xc, false>(x);  // row_bcast:31
+  return x;
+}
+
+// Inclusive prefix sum in float64 over the 64 lanes in the fixed
+// Hillis-Steele order (offsets 1, 2, 4, ..., 32).  The oracle repeats exactly
+// these additions, so both sides round identically.
+__device__ __forceinline__ double wave_scan_f64(double w) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const double t = __shfl_up(w, off, 64);
+    if (lane >= off) w += t;
+  }
+  return w;
+}
+
 __device__ __forceinline__ double readlane_f64(double v, int lane) {
   const long long b = __double_as_longlong(v);
   const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), lane);
@@ -676,59 +734,65 @@ __device__ __forceinline__ double readlane_f64(double v, int lane) {
   return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
 }
 
-// Inverse-CDF draw over n <= 64 candidates (cv/ci in LDS, any order),
-// run by one wave.  Each lane ranks its candidate against all n (value desc,
-// index asc) and writes it to its sorted slot in LDS (sv/si, 64 entries);
-// then w_i = exp(x_i - x_0) in float64, W_i = sequential prefix sums in
-// candidate order, n_keep = first i with W_i > p * W_{n-1} plus one (top-p,
-// first always kept), and the code is the first candidate with
-// W_j > u * W_{n_keep-1}.
-__device__ int draw_wave(const float* cv, const int* ci, int n, float top_p, double u, float* sv,
+// Inverse-CDF draw over n <= 64 candidates (cv/ci in LDS, any order), run by
+// one wave.  Each lane ranks its candidate against all n (value desc, index
+// asc) with broadcast LDS reads and moves it to its sorted slot (sv/si, 64
+// entries); then w_i = exp(x_i - x_0) in float64 and W = wave_scan_f64(w);
+// n_keep = first i with W_i > p * W_{n-1}, plus one (top-p, first always
+// kept); the code is the first candidate with W_j > u * W_{n_keep-1}.
+__device__ __forceinline__ int draw_wave(float* cv, int* ci, int n, float top_p, double u, float* sv,
                          int* si) {
   const int lane = threadIdx.x & 63;
-  float v = (lane < n) ? cv[lane] : -INFINITY;
-  int id = (lane < n) ? ci[lane] : 0x7fffffff;
+  const float v = (lane < n) ? cv[lane] : -INFINITY;
+  const int id = (lane < n) ? ci[lane] : 0x7fffffff;
+  const int n8 = (n + 7) & ~7;        // pad to 8 with sentinels that rank last
+  if (lane >= n && lane < n8) { cv[lane] = -INFINITY; ci[lane] = 0x7fffffff; }
+  __builtin_amdgcn_wave_barrier();
   int rank = 0;
-  for (int j = 0; j < n; ++j) {
-    const float vj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
-    const int ij = __builtin_amdgcn_readlane(id, j);
-    rank += before(vj, ij, v, id) ? 1 : 0;
+  for (int j0 = 0; j0 < n8; j0 += 8) {
+    float vv[8]; int ii[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { vv[j] = cv[j0 + j]; ii[j] = ci[j0 + j]; }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rank += before(vv[j], ii[j], v, id) ? 1 : 0;
   }
   if (lane < n) { sv[rank] = v; si[rank] = id; }
   __builtin_amdgcn_wave_barrier();
-  if (lane < n) { v = sv[lane]; id = si[lane]; }
-  const double top = (double)__shfl(v, 0, 64);
-  const double w = (lane < n) ? exp((double)v - top) : 0.0;
-  double acc = 0.0, Wl = 0.0;
-  for (int i = 0; i < n; ++i) {
-    acc += readlane_f64(w, i);
-    if (lane == i) Wl = acc;
-  }
+  const float vs = (lane < n) ? sv[lane] : -INFINITY;
+  const int ids = (lane < n) ? si[lane] : 0x7fffffff;
+  const double w = (lane < n) ? exp((double)vs - (double)sv[0]) : 0.0;
+  const double W = wave_scan_f64(w);
+  const double S = readlane_f64(W, n - 1);
   int nk = n;
   if (top_p > 0.f && top_p < 1.f) {
-    const double thr = (double)top_p * acc;
-    const unsigned long long b = __ballot(lane + 1 < n && Wl > thr);
+    const double thr = (double)top_p * S;
+    const unsigned long long b = __ballot(lane + 1 < n && W > thr);
     if (b) nk = __ffsll((long long)b);
   }
-  const double target = u * readlane_f64(Wl, nk - 1);
-  const unsigned long long b = __ballot(lane < nk && Wl > target);
+  const double target = u * readlane_f64(W, nk - 1);
+  const unsigned long long b = __ballot(lane < nk && W > target);
   const int j = b ? __ffsll((long long)b) - 1 : nk - 1;
-  return __shfl(id, j, 64);
+  return __builtin_amdgcn_readlane(ids, j);
 }
 
-// x[0..V) in LDS (already CFG-merged and masked).  Follows model.py:686-708:
-// greedy argmax when temperature <= 0; else x / T, top-k (ties kept), top-p
-// (shift-by-one, first kept) and the explicit-uniform inverse-CDF draw in
-// float64 over candidates ordered by value desc, index asc.
-// cv/ci: candidate arrays of MAX_V entries; W: MAX_V doubles.
-__device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, double u,
-                           float* cv, int* ci, double* W, SampleSmem& s) {
+constexpr int SAMPLE_VPT = MAX_V / NT;   // logits per thread
+
+// xr[i] = value of logit v = threadIdx.x + i*NT (registers): CFG-merged,
+// masked and, when temperature > 0, divided by the temperature.  Follows
+// model.py:686-708: greedy argmax when temperature <= 0; else top-k (ties
+// kept), top-p (shift-by-one, first kept) and the explicit-uniform
+// inverse-CDF draw in float64 over candidates ordered by value desc, index
+// asc.  cv/ci: MAX_V entries of LDS; W: MAX_V doubles of LDS.
+__device__ __forceinline__ int sample_core(const float (&xr)[SAMPLE_VPT], int V, float temp, int top_k,
+                                           float top_p, double u, float* cv, int* ci, double* W,
+                                           SampleSmem& s) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (!(temp > 0.f)) {
     float bv = -INFINITY; int bi = 0x7fffffff;
-    for (int v = tid; v < V; v += NT) {
-      const float f = x[v];
-      if (f > bv || bi == 0x7fffffff) { bv = f; bi = v; }
+#pragma unroll
+    for (int i = 0; i < SAMPLE_VPT; ++i) {
+      const int v = tid + i * NT;
+      if (v < V && (xr[i] > bv || bi == 0x7fffffff)) { bv = xr[i]; bi = v; }
     }
     for (int o = 32; o > 0; o >>= 1) {
       const float ov = __shfl_xor(bv, o, 64);
@@ -746,32 +810,33 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
     __syncthreads();
     return s.code;
   }
-  for (int v = tid; v < V; v += NT) x[v] = x[v] / temp;
-  __syncthreads();
+  uint32_t key[SAMPLE_VPT];
+#pragma unroll
+  for (int i = 0; i < SAMPLE_VPT; ++i) key[i] = fkey(xr[i]);
 
-  // k-th largest key by 8-bit radix select (MSB first); stops early once
-  // the selected digit's bin holds exactly the remaining rank (then every
-  // key at or above that digit prefix is a top-k member).
+  // k-th largest key by 8-bit radix select (MSB first).  Histograms are
+  // private per (wave, lane & 7) so same-bin LDS atomics rarely collide; the
+  // pass stops early once the selected bin holds exactly the remaining rank
+  // (then every key at or above that digit prefix is a top-k member).
   uint32_t cut = 0u;
   if (top_k > 0 && top_k < V) {
+    int* H = &s.hist[0][0][0];
+    int* Hw = H + (wave * 8 + (lane & 7)) * 256;
     uint32_t prefix = 0u, pmask = 0u;
     int kr = top_k;
     for (int shift = 24; shift >= 0; shift -= 8) {
-      s.hist[tid] = 0;
+      for (int i = tid * 4; i < WAVES * 8 * 256; i += NT * 4)
+        *reinterpret_cast<int4*>(&H[i]) = make_int4(0, 0, 0, 0);
       __syncthreads();
-      for (int v = tid; v < V; v += NT) {
-        const uint32_t key = fkey(x[v]);
-        if ((key & pmask) == prefix) atomicAdd(&s.hist[(key >> shift) & 255u], 1);
-      }
-      __syncthreads();
-      // Inclusive scan over bins 255..0 (thread t holds bin 255 - t).
-      const int cnt = s.hist[255 - tid];
-      int incl = cnt;
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-      }
+      for (int i = 0; i < SAMPLE_VPT; ++i)
+        if (tid + i * NT < V && (key[i] & pmask) == prefix) atomicAdd(&Hw[(key[i] >> shift) & 255u], 1);
+      __syncthreads();
+      // bin 255 - tid summed over the private copies, then a scan over bins.
+      int cnt = 0;
+#pragma unroll
+      for (int j = 0; j < WAVES * 8; ++j) cnt += H[j * 256 + (255 - tid)];
+      int incl = wave_incl_scan(cnt);
       if (lane == 63) s.scan[wave] = incl;
       __syncthreads();
       for (int w = 0; w < wave; ++w) incl += s.scan[w];
@@ -788,17 +853,29 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
     cut = prefix;
   }
 
-  if (tid == 0) s.n = 0;
-  __syncthreads();
-  for (int v = tid; v < V; v += NT) {
-    const float f = x[v];
-    if (isfinite(f) && fkey(f) >= cut) {
-      const int slot = atomicAdd(&s.n, 1);
-      cv[slot] = f; ci[slot] = v;
-    }
+  // Compact the candidates (finite, key >= cut): deterministic order
+  // (wave, lane, i), no atomics.
+  bool keep[SAMPLE_VPT];
+  int myc = 0;
+#pragma unroll
+  for (int i = 0; i < SAMPLE_VPT; ++i) {
+    keep[i] = (tid + i * NT < V) && isfinite(xr[i]) && key[i] >= cut;
+    myc += keep[i] ? 1 : 0;
   }
+  const int wincl = wave_incl_scan(myc);
+  if (lane == 63) s.wcount[wave] = wincl;
   __syncthreads();
-  const int n = s.n;
+  int base = 0, n = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    if (w < wave) base += s.wcount[w];
+    n += s.wcount[w];
+  }
+  base += wincl - myc;
+#pragma unroll
+  for (int i = 0; i < SAMPLE_VPT; ++i)
+    if (keep[i]) { cv[base] = xr[i]; ci[base] = tid + i * NT; ++base; }
+  __syncthreads();
   if (n <= 64) {
     if (wave == 0) {
       const int code = (n == 0) ? 0 : draw_wave(cv, ci, n, top_p, u, cv + 64, ci + 64);
@@ -828,12 +905,23 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
   const double top = (double)cv[0];
   for (int i = tid; i < n; i += NT) W[i] = exp((double)cv[i] - top);
   __syncthreads();
+  // Prefix sums: groups of 64 in candidate order, each scanned like
+  // wave_scan_f64, plus the running total of the earlier groups.
+  if (wave == 0) {
+    double carry = 0.0;
+    for (int g0 = 0; g0 < n; g0 += 64) {
+      const double w = (g0 + lane < n) ? W[g0 + lane] : 0.0;
+      const double sc = wave_scan_f64(w);
+      if (g0 + lane < n) W[g0 + lane] = carry + sc;
+      carry = carry + readlane_f64(sc, 63);
+    }
+  }
+  __syncthreads();
   if (tid == 0) {
-    double acc = 0.0;
-    for (int i = 0; i < n; ++i) { acc += W[i]; W[i] = acc; }
+    const double S = W[n - 1];
     int nk = n;
     if (top_p > 0.f && top_p < 1.f) {
-      const double thr = (double)top_p * acc;
+      const double thr = (double)top_p * S;
       for (int i = 0; i + 1 < n; ++i)
         if (W[i] > thr) { nk = i + 1; break; }
     }
@@ -848,27 +936,30 @@ __device__ int sample_core(float* x, int V, float temp, int top_k, float top_p, 
 }
 
 // CFG merge u + s (c - u) without contraction, then BOS/PAD (and EOS) -> -inf
-// (model.py:579-584), into x[] in LDS.  Logits loads are issued first.
-constexpr int SAMPLE_VPT = MAX_V / NT;   // logits per thread
+// (model.py:579-584); the merged row is optionally recorded, then kept in
+// registers divided by the temperature when sampling (model.py:696).
 __device__ __forceinline__ void merge_mask(const float* lc, const float* lu, float s, int V,
                                            int bos, int eos, int pad, const int* mask_flag,
-                                           bool force_mask, float* x) {
-  float cvv[SAMPLE_VPT], uvv[SAMPLE_VPT];
+                                           bool force_mask, float temp, float* dbg,
+                                           float (&xr)[SAMPLE_VPT]) {
+  float uvv[SAMPLE_VPT];
 #pragma unroll
   for (int i = 0; i < SAMPLE_VPT; ++i) {
     const int v = threadIdx.x + i * NT;
-    cvv[i] = (v < V) ? lc[v] : 0.f;
+    xr[i] = (v < V) ? lc[v] : -INFINITY;
     uvv[i] = (lu && v < V) ? lu[v] : 0.f;
   }
   const bool mask_eos = force_mask || (mask_flag && *mask_flag != 0);
+  const bool divide = temp > 0.f;
 #pragma unroll
   for (int i = 0; i < SAMPLE_VPT; ++i) {
     const int v = threadIdx.x + i * NT;
-    if (v >= V) break;
-    float m = cvv[i];
+    if (v >= V) continue;
+    float m = xr[i];
     if (lu) m = __fadd_rn(uvv[i], __fmul_rn(s, __fsub_rn(m, uvv[i])));
     if (v == bos || v == pad || (mask_eos && v == eos)) m = -INFINITY;
-    x[v] = m;
+    if (dbg) dbg[v] = m;
+    xr[i] = divide ? m / temp : m;
   }
 }
 
@@ -915,16 +1006,14 @@ __global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
   const SkParams P = *a.params;
   if (q + 1 == a.Q && threadIdx.x < a.Q && threadIdx.x != q)
     codes_l[threadIdx.x] = a.codes_cur[(size_t)ut * a.Q + threadIdx.x];
-  merge_mask(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, a.flag_cur, q != 0, x);
-  __syncthreads();
-  if (P.record_logits)
-    for (int v = threadIdx.x; v < a.V; v += NT)
-      a.dbg[((size_t)ut * a.Q + q) * a.V + v] = x[v];
   const bool q0 = (q == 0) && P.has_q0;
   const float temp = q0 ? P.temperature_q0 : P.temperature;
   const int topk = q0 ? P.top_k_q0 : P.top_k;
   const float topp = q0 ? P.top_p_q0 : P.top_p;
-  int code = sample_core(x, a.V, temp, topk, topp, u, cv, ci, W, s);
+  float xr[SAMPLE_VPT];
+  merge_mask(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, a.flag_cur, q != 0, temp,
+             P.record_logits ? a.dbg + ((size_t)ut * a.Q + q) * a.V : nullptr, xr);
+  int code = sample_core(xr, a.V, temp, topk, topp, u, cv, ci, W, s);
   const size_t uoff = ((size_t)slot * a.n_utts + ut) * a.Q + q;
   if (forced) code = (int)a.forced_ring[uoff];
   code = min(max(code, 0), a.V - 1);
@@ -979,10 +1068,10 @@ __global__ __launch_bounds__(NT) void sample_op_kernel(const float* logits, int 
   float* cv = x + MAX_V;
   int* ci = reinterpret_cast<int*>(cv + MAX_V);
   __shared__ SampleSmem s;
+  float xr[SAMPLE_VPT];
   merge_mask(logits, rows == 2 ? logits + V : nullptr, cfg, V, bos, eos, pad, nullptr,
-             (q != 0) || mask_eos_q0 != 0, x);
-  __syncthreads();
-  const int code = sample_core(x, V, temp, top_k, top_p, u, cv, ci, W, s);
+             (q != 0) || mask_eos_q0 != 0, temp, nullptr, xr);
+  const int code = sample_core(xr, V, temp, top_k, top_p, u, cv, ci, W, s);
   if (threadIdx.x == 0) *code_out = code;
 }
 

@@ -107,6 +107,19 @@ def cpu_baseline(shape, weights, text, prompt, uncond, u, n_frames=6, n_warm=1):
                        f"{dt / n_frames * 1e3:.1f} ms/frame; host {cpu_info()}")}
 
 
+def copy_probe(mib):
+    """A plain device-to-device copy of known size: reading FETCH_SIZE / WRITE_SIZE
+    for it gives the factor that turns those counters into HBM bytes."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_each_way": n * 4, "copies": 4}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,7 +127,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 4 device copies of MIB MiB each (HBM counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): utterances shard across GPUs "
               "with no per-frame exchange, so the per-GPU figure is the N=1 line.", file=sys.stderr)

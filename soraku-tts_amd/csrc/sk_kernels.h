@@ -267,15 +267,18 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // RMSNorm prologue is computed per wave from those registers with a DPP
 // reduction.  Rows past N re-read row N-1 (in bounds) and are discarded.
 template <int M, int KT, int RW, int PRO, int EPI, typename WL>
-__global__ __launch_bounds__(NT) void gemv_fast_kernel(GemvArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemv_fast_kernel(GemvArgs a) {
   constexpr int VEC = WL::VEC;
   constexpr int NV = KT / (64 * VEC);
   constexpr int NS = (EPI == EPI_SWIGLU) ? 2 : 1;
   static_assert(KT % (64 * VEC) == 0, "K must be a multiple of 64 * VEC");
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // wave index as a scalar, so row and segment selection stay in SGPRs and
+  // no weight load waits on a vector-loaded pointer
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int row0 = (blockIdx.x * WAVES + wave) * RW;
 
   float xv[M][NV][VEC];
+  float x2v[PRO == PRO_ADDNORM ? M : 1][PRO == PRO_ADDNORM ? NV : 1][VEC];
 #pragma unroll
   for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -283,12 +286,12 @@ __global__ __launch_bounds__(NT) void gemv_fast_kernel(GemvArgs a) {
 #pragma unroll
       for (int i = 0; i < VEC; i += 4) {
         const size_t k = (size_t)(j * 64 + lane) * VEC + i;
-        float4 t = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + k);
+        const float4 t = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + k);
+        xv[m][j][i] = t.x; xv[m][j][i + 1] = t.y; xv[m][j][i + 2] = t.z; xv[m][j][i + 3] = t.w;
         if (PRO == PRO_ADDNORM) {
           const float4 w = *reinterpret_cast<const float4*>(a.x2 + (size_t)m * a.ldx2 + k);
-          t.x += w.x; t.y += w.y; t.z += w.z; t.w += w.w;
+          x2v[m][j][i] = w.x; x2v[m][j][i + 1] = w.y; x2v[m][j][i + 2] = w.z; x2v[m][j][i + 3] = w.w;
         }
-        xv[m][j][i] = t.x; xv[m][j][i + 1] = t.y; xv[m][j][i + 2] = t.z; xv[m][j][i + 3] = t.w;
       }
 
   // Small operands next (norm gains, residual / bias for this lane's
@@ -322,10 +325,9 @@ __global__ __launch_bounds__(NT) void gemv_fast_kernel(GemvArgs a) {
       if (NS > 1) base[NS - 1] = a.w[1];
       off = (size_t)n * KT;
     } else {
-      int seg = 0, local = n;
-      while (seg < 2 && local >= a.seg_rows[seg]) { local -= a.seg_rows[seg]; ++seg; }
-      base[0] = a.w[seg];
-      off = (size_t)local * KT;
+      const int s0 = a.seg_rows[0], s1 = a.seg_rows[1];
+      base[0] = n < s0 ? a.w[0] : (n - s0 < s1 ? a.w[1] : a.w[2]);
+      off = (size_t)(n < s0 ? n : (n - s0 < s1 ? n - s0 : n - s0 - s1)) * KT;
     }
 #pragma unroll
     for (int s = 0; s < NS; ++s)
@@ -333,6 +335,15 @@ __global__ __launch_bounds__(NT) void gemv_fast_kernel(GemvArgs a) {
       for (int j = 0; j < NV; ++j) WL::load(base[s], off + (size_t)(j * 64 + lane) * VEC, wv[r][s][j]);
   }
 
+  // x + x2 only now, so the weight loads above were not held back by it
+  if (PRO == PRO_ADDNORM) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) xv[m][j][i] += x2v[m][j][i];
+  }
   if (PRO != PRO_NONE) {
 #pragma unroll
     for (int m = 0; m < M; ++m) {

@@ -519,30 +519,34 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   const int T = a.kv_len[r];
   const int p = a.pos[r];
   const int act = a.active[r];
+  // Every load goes to registers first (one element per thread: G*hd <= NT
+  // and hd <= NT), then the chunk's K/V rows; LDS is written only once all of
+  // them are in flight, so no load waits behind another's round trip.
   const float* row = a.qkv + (size_t)r * a.ldqkv;
-  for (int i = tid; i < G * hd; i += NT) qs[i] = row[(size_t)h * G * hd + i];
-  for (int i = tid; i < hd; i += NT) {
-    knew[i] = row[(size_t)a.Hq * hd + (size_t)h * hd + i];
-    vnew[i] = row[(size_t)(a.Hq + a.Hkv) * hd + (size_t)h * hd + i];
-    qw[i] = a.qn_w[i];
-    kw[i] = a.kn_w[i];
+  float q_r = 0.f, kn_r = 0.f, vn_r = 0.f, qw_r = 0.f, kw_r = 0.f, fq_r = 0.f;
+  if (tid < G * hd) q_r = row[(size_t)h * G * hd + tid];
+  if (tid < hd) {
+    kn_r = row[(size_t)a.Hq * hd + (size_t)h * hd + tid];
+    vn_r = row[(size_t)(a.Hq + a.Hkv) * hd + (size_t)h * hd + tid];
+    qw_r = a.qn_w[tid];
+    kw_r = a.kn_w[tid];
   }
-  for (int i = tid; i < half; i += NT) fq[i] = a.inv_freq[i];
+  if (tid < half) fq_r = a.inv_freq[tid];
 
   const int LPT = hd / ATT_DPL;
   const int TPP = NT / LPT;              // tokens per pass
   const int npass = (ATT_CHUNK + TPP - 1) / TPP;
   const int sub = tid % LPT, tok = tid / LPT;
   float4 kr[ATT_DPL / 4], vr[ATT_DPL / 4];
+  // Unconditional (token index clamped into the cache), so the compiler can
+  // count these loads exactly and wait on the small ones above separately.
   auto load_tok = [&](int pass) {
-    const int tl = pass * TPP + tok;
-    const int t = t_begin + tl;
-    if (tl < ATT_CHUNK && t < a.max_ctx) {
-      const float4* kp = reinterpret_cast<const float4*>(a.kc + (head_base + t) * hd + sub * ATT_DPL);
-      const float4* vp = reinterpret_cast<const float4*>(a.vc + (head_base + t) * hd + sub * ATT_DPL);
+    const int tl = min(pass * TPP + tok, ATT_CHUNK - 1);
+    const int t = min(t_begin + tl, a.max_ctx - 1);
+    const float4* kp = reinterpret_cast<const float4*>(a.kc + (head_base + t) * hd + sub * ATT_DPL);
+    const float4* vp = reinterpret_cast<const float4*>(a.vc + (head_base + t) * hd + sub * ATT_DPL);
 #pragma unroll
-      for (int i = 0; i < ATT_DPL / 4; ++i) { kr[i] = kp[i]; vr[i] = vp[i]; }
-    }
+    for (int i = 0; i < ATT_DPL / 4; ++i) { kr[i] = kp[i]; vr[i] = vp[i]; }
   };
   load_tok(0);
   const int ctx = T + 1;
@@ -550,10 +554,12 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   if (!act || c >= nch) return;
   const bool last = (c == nch - 1);
   const int n_t = min(ATT_CHUNK, ctx - t_begin);
-  for (int i = tid; i < half; i += NT) {
-    const float ang = (float)p * fq[i];
-    fcs[i] = (float)cos((double)ang);
-    fsn[i] = (float)sin((double)ang);
+  if (tid < G * hd) qs[tid] = q_r;
+  if (tid < hd) { knew[tid] = kn_r; vnew[tid] = vn_r; qw[tid] = qw_r; kw[tid] = kw_r; }
+  if (tid < half) {
+    const float ang = (float)p * fq_r;
+    fcs[tid] = (float)cos((double)ang);
+    fsn[tid] = (float)sin((double)ang);
   }
   __syncthreads();
   // Per-head RMSNorm over hd, then rotate-half RoPE; one wave per head.
@@ -640,24 +646,28 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
 // A kernel of its own, so the partials need no device-scope fence.
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   const int hq = blockIdx.x, r = blockIdx.y, d = threadIdx.x;
-  if (d >= a.hd) return;
   const int hd = a.hd, stride = hd + 2;
+  const int dd = min(d, hd - 1);         // lanes past hd mirror the last dim, no branch
   const float* pp = a.part + ((size_t)r * a.Hq + hq) * a.max_chunks * stride;
   constexpr int CB = 16;
-  const int T = a.kv_len[r];
-  const int act = a.active[r];
-  float M = -INFINITY, L = 0.f, O = 0.f;
-  for (int c0 = 0; c0 < a.max_chunks; c0 += CB) {
-    float mv[CB], lv[CB], ov[CB];
+  float mv[CB], lv[CB], ov[CB];
+  auto load_block = [&](int c0) {
 #pragma unroll
     for (int j = 0; j < CB; ++j) {
       const int cc = min(c0 + j, a.max_chunks - 1);
       mv[j] = pp[cc * stride + hd];
       lv[j] = pp[cc * stride + hd + 1];
-      ov[j] = pp[cc * stride + d];
+      ov[j] = pp[cc * stride + dd];
     }
-    const int nch = (T + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
-    if (c0 >= nch) break;
+  };
+  load_block(0);
+  // Keep the first block's loads ahead of the length lookup they do not need.
+  asm volatile("" ::: "memory");
+  const int nch = (a.kv_len[r] + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
+  const int act = a.active[r];
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int c0 = 0; c0 < nch; c0 += CB) {
+    if (c0 > 0) load_block(c0);
     float Mb = M;
 #pragma unroll
     for (int j = 0; j < CB; ++j)
@@ -674,7 +684,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
       }
     M = Mb;
   }
-  if (act) a.out[(size_t)r * a.ldo + (size_t)hq * hd + d] = O / L;
+  if (act && d < hd) a.out[(size_t)r * a.ldo + (size_t)hq * hd + d] = O / L;
 }
 
 // ------------------------------------------------------------ sampler
@@ -1103,10 +1113,31 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
   const int b = blockIdx.x;
   if (active[b]) {
     const float* xr = x + (size_t)b * D;
-    float s = 0.f;
-    for (int k = threadIdx.x; k < D; k += NT) s += xr[k] * xr[k];
-    const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
-    for (int k = threadIdx.x; k < D; k += NT) hidden[(size_t)b * D + k] = w[k] * (xr[k] * inv);
+    constexpr int PER = 16;              // D <= 4096 in registers, all loads issued at once
+    if (D <= NT * PER) {
+      float xv[PER], wv[PER];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int k = min((int)threadIdx.x + i * NT, D - 1);
+        xv[i] = xr[k];
+        wv[i] = w[k];
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if ((int)threadIdx.x + i * NT < D) s += xv[i] * xv[i];
+      const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int k = threadIdx.x + i * NT;
+        if (k < D) hidden[(size_t)b * D + k] = wv[i] * (xv[i] * inv);
+      }
+    } else {
+      float s = 0.f;
+      for (int k = threadIdx.x; k < D; k += NT) s += xr[k] * xr[k];
+      const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
+      for (int k = threadIdx.x; k < D; k += NT) hidden[(size_t)b * D + k] = w[k] * (xr[k] * inv);
+    }
     if (threadIdx.x == 0) { kv_len[b] += 1; pos[b] += 1; }
   }
   if (b == 0) {

@@ -19,7 +19,8 @@ pick the same code:
 1. candidates = finite values that survive top-k, ordered by value
    descending, ties by lower index first;
 2. ``w_i = exp(x_i - x_0)`` in float64, ``W_i`` = prefix sums in a fixed
-   order (``scan_sums``: 64-wide Hillis-Steele groups plus a running carry);
+   order (``scan_sums``: groups of 64 scanned as rows of 16 then across
+   rows, plus a running carry);
 3. top-p keeps the leading candidates up to and including the first i with
    ``W_i > p * W_{n-1}`` (all n if none; p taken as an FP32 value promoted to
    float64, the product rounded once), i.e. ``cum > p`` shifted right by one;
@@ -72,10 +73,28 @@ def candidates(x, top_k):
     return idx[np.lexsort((idx, -x[idx].astype(np.float64)))]
 
 
+def _scan64(blk):
+    """Inclusive float64 scan of 64 values in the fixed order: within each
+    row of 16 lanes add the value 1, 2, 4, 8 lanes below (same row only),
+    then rows 1 and 3 add the last value of the row before, then rows 2 and
+    3 add value 31.  Every step adds pre-step values, one rounding each."""
+    b = np.array(blk, np.float64)
+    lane = np.arange(64)
+    for off in (1, 2, 4, 8):
+        src = b.copy()
+        on = (lane % 16) >= off
+        b[on] = src[on] + src[lane[on] - off]
+    src = b.copy()
+    for r in (1, 3):
+        b[16 * r:16 * r + 16] = src[16 * r:16 * r + 16] + src[16 * r - 1]
+    src = b.copy()
+    b[32:] = src[32:] + src[31]
+    return b
+
+
 def scan_sums(w) -> np.ndarray:
     """Inclusive float64 prefix sums in the fixed order both sides use:
-    groups of 64 candidates, each scanned Hillis-Steele style (offsets 1, 2,
-    4, ..., 32, every step adding the pre-step neighbour), plus the running
+    groups of 64 candidates, each scanned by ``_scan64``, plus the running
     total of the earlier groups (carry + group scan, one rounding)."""
     w = np.asarray(w, np.float64)
     n = w.size
@@ -85,8 +104,7 @@ def scan_sums(w) -> np.ndarray:
         m = min(64, n - g0)
         blk = np.zeros(64, np.float64)
         blk[:m] = w[g0:g0 + m]
-        for off in (1, 2, 4, 8, 16, 32):
-            blk[off:] = blk[off:] + blk[:-off]
+        blk = _scan64(blk)
         out[g0:g0 + m] = carry + blk[:m]
         carry = carry + blk[63]
     return out

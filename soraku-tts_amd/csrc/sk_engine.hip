@@ -58,7 +58,8 @@ struct sk_engine {
   const void *d_gate = nullptr, *d_up = nullptr, *d_down = nullptr;
 
   // device buffers (owned)
-  float *x = nullptr, *hidden = nullptr, *prefix = nullptr, *abuf = nullptr, *ybuf = nullptr;
+  float *x = nullptr, *hidden = nullptr, *prefix = nullptr, *prefix2 = nullptr, *abuf = nullptr,
+        *ybuf = nullptr;
   float *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
   float *kc = nullptr, *vc = nullptr, *inv_freq = nullptr;
   float *part = nullptr, *dbg = nullptr, *embeds = nullptr;
@@ -213,11 +214,25 @@ hipError_t enqueue_frame(sk_engine* e) {
   s.codes_ring = e->codes_ring; s.codes_cur = e->codes_cur; s.dbg = e->dbg; s.table = e->table;
   s.prefix = e->prefix; s.xnext = e->x; s.d = d; s.Q = c.n_codebooks; s.scale = c.frame_scale;
   s.bos = c.bos_id; s.eos = c.eos_id; s.pad = c.pad_id; s.n_utts = c.n_utts;
+  // Codebook prefix: step 0 reads `prefix` (all zero); step q >= 1 reads the
+  // previous step's prefix, adds the embedding of code q-1 and writes the
+  // result to the other buffer of the pair (readers of one launch never see
+  // its own writes).  The last sampler launch zeroes `prefix` again.
   for (int q = 0; q < c.n_codebooks; ++q) {
     GemvArgs a = gemv_args(e->d_gate, c.depth_inner, d, e->hidden, d, e->act, e->inner_max);
-    a.w[1] = e->d_up; a.x2 = e->prefix; a.ldx2 = d;
+    a.w[1] = e->d_up; a.ldx2 = d;
     a.norm_w = e->d_norm_in; a.eps = c.depth_eps; a.norm_out = e->abuf; a.ldno = d;
-    if ((err = launch_gemv<PRO_ADDNORM, EPI_SWIGLU>(wt, M, a, e->stream)) != hipSuccess) return err;
+    if (q == 0) {
+      a.x2 = e->prefix;
+      if ((err = launch_gemv<PRO_ADDNORM, EPI_SWIGLU>(wt, M, a, e->stream)) != hipSuccess) return err;
+    } else {
+      a.x2 = (q % 2 == 1) ? e->prefix : e->prefix2;
+      a.gout = (q % 2 == 1) ? e->prefix2 : e->prefix; a.ldgo = d;
+      a.gcode = e->codes_cur + (q - 1); a.g_rpu = c.cfg_rows; a.gstride = c.n_codebooks;
+      a.gtable = static_cast<const char*>(e->table) + (size_t)(q - 1) * V * d * tsz;
+      a.gscale = c.frame_scale;
+      if ((err = launch_gemv<PRO_ADDGATHER, EPI_SWIGLU>(wt, M, a, e->stream)) != hipSuccess) return err;
+    }
 
     a = gemv_args(e->d_down, d, c.depth_inner, e->act, e->inner_max, e->ybuf, d);
     a.res = e->abuf; a.ldr = d;
@@ -228,11 +243,9 @@ hipError_t enqueue_frame(sk_engine* e) {
     a.norm_w = e->d_norm_out; a.eps = c.depth_eps; a.bias = e->d_bias + (size_t)q * V;
     if ((err = launch_gemv<PRO_NORM, EPI_BIAS>(wt, M, a, e->stream)) != hipSuccess) return err;
 
-    if (wt == SK_BF16)
-      hipLaunchKernelGGL(sample_step_kernel<WBF16>, dim3(c.n_utts), dim3(NT), SAMPLE_SMEM, e->stream, s, q);
-    else
-      hipLaunchKernelGGL(sample_step_kernel<WF32>, dim3(c.n_utts), dim3(NT), SAMPLE_SMEM, e->stream, s, q);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
+    err = (wt == SK_BF16) ? launch_sample_step<WBF16>(s, q, c.n_utts, e->stream)
+                          : launch_sample_step<WF32>(s, q, c.n_utts, e->stream);
+    if (err != hipSuccess) return err;
   }
   if ((err = enqueue_trunk(e)) != hipSuccess) return err;
   hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x, e->final_norm,
@@ -331,7 +344,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     return bail(SK_EHIP);
   }
   const size_t R = e->rows, d = c.d_model, Q = c.n_codebooks, V = c.audio_vocab;
-  ALLOC(e->x, R * d); ALLOC(e->hidden, R * d); ALLOC(e->prefix, R * d);
+  ALLOC(e->x, R * d); ALLOC(e->hidden, R * d); ALLOC(e->prefix, R * d); ALLOC(e->prefix2, R * d);
   ALLOC(e->abuf, R * d); ALLOC(e->ybuf, R * d);
   ALLOC(e->qkv, R * e->nqkv); ALLOC(e->attn, R * c.n_q_heads * c.head_dim);
   ALLOC(e->act, R * e->inner_max); ALLOC(e->logits, R * V);
@@ -360,6 +373,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   if (he == hipSuccess) he = hipMemset(e->flag_cur, 0, 2 * sizeof(int));
   if (he == hipSuccess) he = hipMemset(e->x, 0, R * d * sizeof(float));
   if (he == hipSuccess) he = hipMemset(e->prefix, 0, R * d * sizeof(float));
+  if (he == hipSuccess) he = hipMemset(e->prefix2, 0, R * d * sizeof(float));
   if (he == hipSuccess) he = hipMemset(e->kv_len, 0, R * sizeof(int));
   if (he == hipSuccess) he = hipMemset(e->pos, 0, R * sizeof(int));
   if (he == hipSuccess) he = hipMemset(e->fc, 0, sizeof(int));
@@ -382,7 +396,7 @@ int sk_destroy(sk_engine* e) {
   if (!e) return SK_OK;
   if (e->stream) hipStreamSynchronize(e->stream);
   drop_graphs(e);
-  void* bufs[] = {e->x, e->hidden, e->prefix, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
+  void* bufs[] = {e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
                   e->kc, e->vc, e->inv_freq, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->pf_t, e->flag_ring, e->u_ring,
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
@@ -506,6 +520,7 @@ int sk_prefill_run(sk_engine* e) {
   SK_HIP(hipMemsetAsync(e->pf_t, 0, sizeof(int), e->stream));
   SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
   SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
+  SK_HIP(hipMemsetAsync(e->prefix2, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
   SK_HIP(hipStreamSynchronize(e->stream));
   if (!e->pf_exec) {
     rc = capture(e, enqueue_prefill_step, &e->pf_graph, &e->pf_exec);

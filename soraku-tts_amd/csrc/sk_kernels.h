@@ -78,7 +78,10 @@ struct WBF16 {
 
 // ------------------------------------------------------------ GEMV family
 // y[m][n] = sum_k x[m][k] * W[n][k] for M activation rows (decode rows).
-enum { PRO_NONE = 0, PRO_NORM = 1, PRO_ADDNORM = 2 };
+// PRO_ADDGATHER: x + (x2 + scale * table[code]) -- the depth head's codebook
+// prefix advanced by the previous step's code (model.py:600-605) inside the
+// consumer of the prefix; block 0 writes the advanced prefix to gout.
+enum { PRO_NONE = 0, PRO_NORM = 1, PRO_ADDNORM = 2, PRO_ADDGATHER = 3 };
 enum { EPI_STORE = 0, EPI_BIAS = 1, EPI_RESID = 2, EPI_SWIGLU = 3 };
 
 struct GemvArgs {
@@ -94,21 +97,35 @@ struct GemvArgs {
   float* out; int ldo;
   const float* res; int ldr;   // EPI_RESID (may alias out: one lane owns each element)
   const float* bias;           // EPI_BIAS
+  // PRO_ADDGATHER: row m takes code gcode[(m / g_rpu) * gstride] of table
+  // gtable ([V][K], weight dtype); the advanced prefix goes to gout[m][K].
+  const int* gcode; int g_rpu, gstride;
+  const void* gtable; float gscale;
+  float* gout; int ldgo;
 };
 
 // Stage x (+ x2) into LDS xs[M][K], applying the RMSNorm prologue if asked.
-template <int M, int PRO>
+template <int M, int PRO, typename WL>
 __device__ __forceinline__ void stage_x(const GemvArgs& a, int K, float* xs, float (*red)[WAVES]) {
   const int tid = threadIdx.x;
-  for (int m = 0; m < M; ++m)
+  for (int m = 0; m < M; ++m) {
+    const size_t trow = (PRO == PRO_ADDGATHER) ? (size_t)a.gcode[(m / a.g_rpu) * a.gstride] * K : 0;
     for (int k = tid * 4; k < K; k += NT * 4) {
       float4 v = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + k);
-      if (PRO == PRO_ADDNORM) {
-        const float4 w = *reinterpret_cast<const float4*>(a.x2 + (size_t)m * a.ldx2 + k);
-        v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+      if (PRO == PRO_ADDNORM || PRO == PRO_ADDGATHER) {
+        float4 w = *reinterpret_cast<const float4*>(a.x2 + (size_t)m * a.ldx2 + k);
+        if (PRO == PRO_ADDGATHER) {
+          w.x = __fadd_rn(w.x, __fmul_rn(WL::get(a.gtable, trow + k), a.gscale));
+          w.y = __fadd_rn(w.y, __fmul_rn(WL::get(a.gtable, trow + k + 1), a.gscale));
+          w.z = __fadd_rn(w.z, __fmul_rn(WL::get(a.gtable, trow + k + 2), a.gscale));
+          w.w = __fadd_rn(w.w, __fmul_rn(WL::get(a.gtable, trow + k + 3), a.gscale));
+          if (blockIdx.x == 0) *reinterpret_cast<float4*>(a.gout + (size_t)m * a.ldgo + k) = w;
+        }
+        v.x = __fadd_rn(v.x, w.x); v.y = __fadd_rn(v.y, w.y); v.z = __fadd_rn(v.z, w.z); v.w = __fadd_rn(v.w, w.w);
       }
       *reinterpret_cast<float4*>(&xs[m * K + k]) = v;
     }
+  }
   if (PRO != PRO_NONE) {
     __syncthreads();
     float ss[M];
@@ -152,7 +169,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
   __shared__ float red[M][WAVES];
   const int tid = threadIdx.x;
   const int K = a.K;
-  stage_x<M, PRO>(a, K, xs, red);
+  stage_x<M, PRO, WL>(a, K, xs, red);
 
   constexpr int VEC = WL::VEC;
   constexpr int NS = (EPI == EPI_SWIGLU) ? 2 : 1;
@@ -277,8 +294,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int row0 = (blockIdx.x * WAVES + wave) * RW;
 
+  constexpr bool ADD = (PRO == PRO_ADDNORM || PRO == PRO_ADDGATHER);
   float xv[M][NV][VEC];
-  float x2v[PRO == PRO_ADDNORM ? M : 1][PRO == PRO_ADDNORM ? NV : 1][VEC];
+  float x2v[ADD ? M : 1][ADD ? NV : 1][VEC];
 #pragma unroll
   for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -288,11 +306,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
         const size_t k = (size_t)(j * 64 + lane) * VEC + i;
         const float4 t = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + k);
         xv[m][j][i] = t.x; xv[m][j][i + 1] = t.y; xv[m][j][i + 2] = t.z; xv[m][j][i + 3] = t.w;
-        if (PRO == PRO_ADDNORM) {
+        if (ADD) {
           const float4 w = *reinterpret_cast<const float4*>(a.x2 + (size_t)m * a.ldx2 + k);
           x2v[m][j][i] = w.x; x2v[m][j][i + 1] = w.y; x2v[m][j][i + 2] = w.z; x2v[m][j][i + 3] = w.w;
         }
       }
+  // Codes of the gathered table rows (uniform: scalar loads, which no
+  // vector load waits on).
+  int gc[M];
+  if (PRO == PRO_ADDGATHER) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) gc[m] = a.gcode[(m / a.g_rpu) * a.gstride];
+  }
 
   // Small operands next (norm gains, residual / bias for this lane's
   // outputs), so waiting on them never waits on the weight stream.
@@ -335,14 +360,35 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
       for (int j = 0; j < NV; ++j) WL::load(base[s], off + (size_t)(j * 64 + lane) * VEC, wv[r][s][j]);
   }
 
-  // x + x2 only now, so the weight loads above were not held back by it
-  if (PRO == PRO_ADDNORM) {
+  // The gathered rows are loaded after the weights (their address waits on
+  // the code), and x + x2 is formed only now, so neither holds the weight
+  // stream back.
+  if (PRO == PRO_ADDGATHER) {
+    float tv[M][NV][VEC];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) WL::load(a.gtable, (size_t)gc[m] * KT + (size_t)(j * 64 + lane) * VEC, tv[m][j]);
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) x2v[m][j][i] = __fadd_rn(x2v[m][j][i], __fmul_rn(tv[m][j][i], a.gscale));
+        if (blockIdx.x == 0 && wave == 0)
+#pragma unroll
+          for (int i = 0; i < VEC; i += 4)
+            *reinterpret_cast<float4*>(a.gout + (size_t)m * a.ldgo + (size_t)(j * 64 + lane) * VEC + i) =
+                make_float4(x2v[m][j][i], x2v[m][j][i + 1], x2v[m][j][i + 2], x2v[m][j][i + 3]);
+      }
+  }
+  if (ADD) {
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
       for (int j = 0; j < NV; ++j)
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) xv[m][j][i] += x2v[m][j][i];
+        for (int i = 0; i < VEC; ++i) xv[m][j][i] = __fadd_rn(xv[m][j][i], x2v[m][j][i]);
   }
   if (PRO != PRO_NONE) {
 #pragma unroll
@@ -708,16 +754,28 @@ struct SampleSmem {
   int hist[WAVES][8][256];   // radix histograms, private per (wave, lane & 7)
   int scan[WAVES];
   int wcount[WAVES];
+  unsigned lvc[WAVES][8];    // per-wave distance-level counts, 16 levels x 16 bits
+  float bv[WAVES];
+  float bs[WAVES];
+  int bi[WAVES];
+  unsigned long long bk[WAVES];
   int code;
   int sel_digit;
   int sel_excl;
   int sel_cnt;
-  float bv[WAVES];
-  int bi[WAVES];
 };
 
-__device__ __forceinline__ bool before(float va, int ia, float vb, int ib) {
-  return (va > vb) || (va == vb && ia < ib);
+// Sort key of candidate (value, index): a larger key comes first in the
+// order value desc, index asc.  Key 0 sorts after every real candidate.
+__device__ __forceinline__ unsigned long long skey(float v, int idx) {
+  return ((unsigned long long)fkey(v) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ float key_value(unsigned long long k) {
+  const uint32_t u = (uint32_t)(k >> 32);
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+__device__ __forceinline__ int key_index(unsigned long long k) {
+  return (int)(0xffffffffu - (uint32_t)k);
 }
 
 template <int CTRL, int ROW_MASK, bool BOUND0>
@@ -734,17 +792,67 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
   x += dpp_i<0x143, 0xc, false>(x);  // row_bcast:31
   return x;
 }
-
-// Inclusive prefix sum in float64 over the 64 lanes in the fixed
-// Hillis-Steele order (offsets 1, 2, 4, ..., 32).  The oracle repeats exactly
-// these additions, so both sides round identically.
-__device__ __forceinline__ double wave_scan_f64(double w) {
-  const int lane = threadIdx.x & 63;
+// Sum of an int over the 64 lanes, returned to every lane.
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += dpp_i<0xb1, 0xf, true>(v);
+  v += dpp_i<0x4e, 0xf, true>(v);
+  v += dpp_i<0x114, 0xf, true>(v);
+  v += dpp_i<0x118, 0xf, true>(v);
+  v += dpp_i<0x142, 0xa, false>(v);
+  v += dpp_i<0x143, 0xc, false>(v);
+  return __builtin_amdgcn_readlane(v, 63);
+}
+// Sums of 8 words over the 64 lanes at once: every lane gets the total of
+// word (lane >> 3).  Halving steps over lane bits 5 and 4 (permlane swaps)
+// and 3 (row mirror), then plain sums within each group of 8 lanes.
+__device__ __forceinline__ unsigned wave_reduce8(const unsigned (&w)[8], int lane) {
+  unsigned v[4], t[2];
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const double t = __shfl_up(w, off, 64);
-    if (lane >= off) w += t;
+  for (int i = 0; i < 4; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(w[i], w[i + 4], false, false);
+    v[i] = r[0] + r[1];
   }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v[i], v[i + 2], false, false);
+    t[i] = r[0] + r[1];
+  }
+  const bool hi = (lane >> 3) & 1;
+  const unsigned keep = hi ? t[1] : t[0], send = hi ? t[0] : t[1];
+  unsigned x = keep + (unsigned)dpp_i<0x140, 0xf, false>((int)send);   // row_mirror
+  x += (unsigned)dpp_i<0x141, 0xf, false>((int)x);                    // row_half_mirror
+  x += (unsigned)dpp_i<0x4e, 0xf, false>((int)x);                     // quad_perm [2,3,0,1]
+  x += (unsigned)dpp_i<0xb1, 0xf, false>((int)x);                     // quad_perm [1,0,3,2]
+  return x;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long t = __shfl_xor(k, o, 64);
+    k = t > k ? t : k;
+  }
+  return k;
+}
+
+template <int CTRL, int ROW_MASK, bool BOUND0>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(b & 0xffffffffll), CTRL, ROW_MASK, 0xf, BOUND0);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, ROW_MASK, 0xf, BOUND0);
+  return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+// Inclusive prefix sum in float64 over the 64 lanes, in this fixed order:
+// within each row of 16 lanes add the value 1, 2, 4, 8 lanes below (same
+// row); then rows 1 and 3 add the last lane of the row before; then rows 2
+// and 3 add lane 31.  The oracle repeats exactly these additions, so both
+// sides round identically.
+__device__ __forceinline__ double wave_scan_f64(double w) {
+  w += dpp_f64<0x111, 0xf, true>(w);
+  w += dpp_f64<0x112, 0xf, true>(w);
+  w += dpp_f64<0x114, 0xf, true>(w);
+  w += dpp_f64<0x118, 0xf, true>(w);
+  w += dpp_f64<0x142, 0xa, false>(w);
+  w += dpp_f64<0x143, 0xc, false>(w);
   return w;
 }
 
@@ -755,92 +863,262 @@ __device__ __forceinline__ double readlane_f64(double v, int lane) {
   return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
 }
 
-// Inverse-CDF draw over n <= 64 candidates (cv/ci in LDS, any order), run by
-// one wave.  Each lane ranks its candidate against all n (value desc, index
-// asc) with broadcast LDS reads and moves it to its sorted slot (sv/si, 64
-// entries); then w_i = exp(x_i - x_0) in float64 and W = wave_scan_f64(w);
-// n_keep = first i with W_i > p * W_{n-1}, plus one (top-p, first always
-// kept); the code is the first candidate with W_j > u * W_{n_keep-1}.
-__device__ __forceinline__ int draw_wave(float* cv, int* ci, int n, float top_p, double u, float* sv,
-                         int* si) {
+// Inverse-CDF draw over the first n keys of a sorted list (value desc,
+// index asc), run by one wave: w_i = exp(x_i - x_0) in float64, W = prefix
+// sums (wave_scan_f64 per group of 64, plus the running total of the earlier
+// groups); n_keep = first i with W_i > p * W_{n-1}, plus one (top-p, first
+// always kept); the code is the first candidate with W_j > u * W_{n_keep-1}.
+// Wg: n doubles of LDS (used when n > 64).
+__device__ __forceinline__ int draw_sorted(const unsigned long long* sk, int n, float top_p, double u,
+                                           double* Wg) {
   const int lane = threadIdx.x & 63;
-  const float v = (lane < n) ? cv[lane] : -INFINITY;
-  const int id = (lane < n) ? ci[lane] : 0x7fffffff;
-  const int n8 = (n + 7) & ~7;        // pad to 8 with sentinels that rank last
-  if (lane >= n && lane < n8) { cv[lane] = -INFINITY; ci[lane] = 0x7fffffff; }
-  __builtin_amdgcn_wave_barrier();
-  int rank = 0;
-  for (int j0 = 0; j0 < n8; j0 += 8) {
-    float vv[8]; int ii[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) { vv[j] = cv[j0 + j]; ii[j] = ci[j0 + j]; }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) rank += before(vv[j], ii[j], v, id) ? 1 : 0;
+  const double top = (double)key_value(sk[0]);
+  if (n <= 64) {
+    const unsigned long long k = sk[min(lane, n - 1)];
+    const double w = (lane < n) ? exp((double)key_value(k) - top) : 0.0;
+    const double W = wave_scan_f64(w);
+    const double S = readlane_f64(W, n - 1);
+    int nk = n;
+    if (top_p > 0.f && top_p < 1.f) {
+      const unsigned long long b = __ballot(lane + 1 < n && W > (double)top_p * S);
+      if (b) nk = __ffsll((long long)b);
+    }
+    const double target = u * readlane_f64(W, nk - 1);
+    const unsigned long long b = __ballot(lane < nk && W > target);
+    const int j = b ? __ffsll((long long)b) - 1 : nk - 1;
+    return key_index(sk[j]);
   }
-  if (lane < n) { sv[rank] = v; si[rank] = id; }
+  double carry = 0.0;
+  for (int g0 = 0; g0 < n; g0 += 64) {
+    const unsigned long long k = sk[min(g0 + lane, n - 1)];
+    const double w = (g0 + lane < n) ? exp((double)key_value(k) - top) : 0.0;
+    const double sc = wave_scan_f64(w);
+    if (g0 + lane < n) Wg[g0 + lane] = carry + sc;
+    carry = carry + readlane_f64(sc, 63);
+  }
   __builtin_amdgcn_wave_barrier();
-  const float vs = (lane < n) ? sv[lane] : -INFINITY;
-  const int ids = (lane < n) ? si[lane] : 0x7fffffff;
-  const double w = (lane < n) ? exp((double)vs - (double)sv[0]) : 0.0;
-  const double W = wave_scan_f64(w);
-  const double S = readlane_f64(W, n - 1);
+  const double S = Wg[n - 1];
   int nk = n;
   if (top_p > 0.f && top_p < 1.f) {
     const double thr = (double)top_p * S;
-    const unsigned long long b = __ballot(lane + 1 < n && W > thr);
-    if (b) nk = __ffsll((long long)b);
+    for (int g0 = 0; g0 + 1 < n; g0 += 64) {
+      const unsigned long long b = __ballot(g0 + lane + 1 < n && Wg[min(g0 + lane, n - 1)] > thr);
+      if (b) { nk = g0 + __ffsll((long long)b); break; }
+    }
   }
-  const double target = u * readlane_f64(W, nk - 1);
-  const unsigned long long b = __ballot(lane < nk && W > target);
-  const int j = b ? __ffsll((long long)b) - 1 : nk - 1;
-  return __builtin_amdgcn_readlane(ids, j);
+  const double target = u * Wg[nk - 1];
+  int j = nk - 1;
+  for (int g0 = 0; g0 < nk; g0 += 64) {
+    const unsigned long long b = __ballot(g0 + lane < nk && Wg[min(g0 + lane, nk - 1)] > target);
+    if (b) { j = g0 + __ffsll((long long)b) - 1; break; }
+  }
+  return key_index(sk[j]);
 }
 
-constexpr int SAMPLE_VPT = MAX_V / NT;   // logits per thread
-
-// xr[i] = value of logit v = threadIdx.x + i*NT (registers): CFG-merged,
-// masked and, when temperature > 0, divided by the temperature.  Follows
-// model.py:686-708: greedy argmax when temperature <= 0; else top-k (ties
-// kept), top-p (shift-by-one, first kept) and the explicit-uniform
-// inverse-CDF draw in float64 over candidates ordered by value desc, index
-// asc.  cv/ci: MAX_V entries of LDS; W: MAX_V doubles of LDS.
-__device__ __forceinline__ int sample_core(const float (&xr)[SAMPLE_VPT], int V, float temp, int top_k,
-                                           float top_p, double u, float* cv, int* ci, double* W,
-                                           SampleSmem& s) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (!(temp > 0.f)) {
-    float bv = -INFINITY; int bi = 0x7fffffff;
+// Rank of key K among ck[0, n2) (n2 even, padded with key 0): the number of
+// keys that sort before it.
+__device__ __forceinline__ int key_rank(const unsigned long long* ck, int n2, unsigned long long K) {
+  int rank = 0;
+  int j = 0;
+  for (; j + 8 <= n2; j += 8) {          // four 16-byte reads in flight per step
+    ulonglong2 kk[4];
 #pragma unroll
-    for (int i = 0; i < SAMPLE_VPT; ++i) {
-      const int v = tid + i * NT;
-      if (v < V && (xr[i] > bv || bi == 0x7fffffff)) { bv = xr[i]; bi = v; }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    if (lane == 0) { s.bv[wave] = bv; s.bi[wave] = bi; }
-    __syncthreads();
-    if (tid == 0) {
-      float b = s.bv[0]; int i = s.bi[0];
-      for (int w = 1; w < WAVES; ++w)
-        if (s.bv[w] > b || (s.bv[w] == b && s.bi[w] < i)) { b = s.bv[w]; i = s.bi[w]; }
-      s.code = i;
-    }
-    __syncthreads();
-    return s.code;
+    for (int t = 0; t < 4; ++t) kk[t] = *reinterpret_cast<const ulonglong2*>(ck + j + 2 * t);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) rank += (kk[t].x > K ? 1 : 0) + (kk[t].y > K ? 1 : 0);
   }
-  uint32_t key[SAMPLE_VPT];
-#pragma unroll
-  for (int i = 0; i < SAMPLE_VPT; ++i) key[i] = fkey(xr[i]);
+  for (; j < n2; j += 2) {
+    const ulonglong2 kk = *reinterpret_cast<const ulonglong2*>(ck + j);
+    rank += (kk.x > K ? 1 : 0) + (kk.y > K ? 1 : 0);
+  }
+  return rank;
+}
 
-  // k-th largest key by 8-bit radix select (MSB first).  Histograms are
-  // private per (wave, lane & 7) so same-bin LDS atomics rarely collide; the
-  // pass stops early once the selected bin holds exactly the remaining rank
-  // (then every key at or above that digit prefix is a top-k member).
+// Number of leading sorted candidates that survive top-k with ties kept:
+// every value >= the k-th largest (model.py:697-699); k <= 0 keeps all.
+__device__ __forceinline__ int topk_count(const unsigned long long* sk, int n, int k) {
+  if (k <= 0 || k >= n) return n;
+  const uint32_t kth = (uint32_t)(sk[k - 1] >> 32);
+  const int lane = threadIdx.x & 63;
+  int cnt = k;
+  for (int g0 = k; g0 < n; g0 += 64) {
+    const unsigned long long b =
+        __ballot(g0 + lane < n && (uint32_t)(sk[min(g0 + lane, n - 1)] >> 32) >= kth);
+    cnt += __popcll(b);
+    if (b != ~0ull) break;
+  }
+  return cnt;
+}
+
+constexpr int FILTER_MAX = 256;          // largest candidate set the distance filter ranks directly
+
+// xr[i] = value of logit v = threadIdx.x + i*NT (registers; -inf past V):
+// CFG-merged, masked and, when temperature > 0, divided by the temperature.
+// Follows model.py:686-708: greedy argmax when temperature <= 0; else top-k
+// (ties kept), top-p (shift-by-one, first kept) and the explicit-uniform
+// inverse-CDF draw in float64 over candidates ordered by value desc, index
+// asc.  ck: MAX_V keys of LDS; sk: FILTER_MAX keys of LDS; W: MAX_V doubles
+// of LDS.  The code is valid in every lane of wave 0.
+//
+// Top-k selection.  One barrier gives the block maximum M and mean; a
+// second gives, per wave, how many values fall in each of 16 distance levels
+// lvl(x) = min(15, floor((M - x) * 16 / (M - mean))) (monotone in x, so
+// {lvl <= L} is a set {x >= t}).  With L the first level whose cumulative
+// count reaches k, that set holds every top-k member; when it has at most
+// FILTER_MAX entries it is compacted and ranked exactly (one wave when it
+// has at most 64).  Otherwise (flat distributions, top-k off) an exact
+// 8-bit radix select finds the k-th key and the candidates are sorted.
+template <int VPT>
+__device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float temp, int top_k, float top_p,
+                                           double u, unsigned long long* ck, unsigned long long* sk,
+                                           double* W, SampleSmem& s) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (!(temp > 0.f)) {
+    unsigned long long best = 0ull;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const unsigned long long k = skey(xr[i], tid + i * NT);
+      best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) s.bk[wave] = best;
+    __syncthreads();
+    unsigned long long b = s.bk[0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) b = s.bk[w] > b ? s.bk[w] : b;
+    return key_index(b);
+  }
+
+  // ---- block maximum, sum and count of the finite values
+  float mx = -INFINITY, sm = 0.f;
+  int nf = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const bool f = isfinite(xr[i]);
+    mx = f ? fmaxf(mx, xr[i]) : mx;
+    sm += f ? xr[i] : 0.f;
+    nf += f ? 1 : 0;
+  }
+  mx = wave_max_dpp(mx);
+  sm = wave_sum_dpp(sm);
+  nf = wave_sum_i(nf);
+  if (lane == 0) { s.bv[wave] = mx; s.bs[wave] = sm; s.bi[wave] = nf; }
+  __syncthreads();
+  float M = s.bv[0], S = s.bs[0];
+  int nfin = s.bi[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) { M = fmaxf(M, s.bv[w]); S += s.bs[w]; nfin += s.bi[w]; }
+  if (nfin == 0) return 0;               // every entry masked: nothing to draw
+
+  // ---- distance levels lvl = min(15, floor((M - x) * 16 / (M - mean))),
+  // counted in 4-bit fields (two accumulators when a thread holds > 15)
+  const float spread = M - S / (float)nfin;
+  const float inv_step = spread > 0.f ? 16.f / spread : 0.f;
+  int lvl[VPT];
+  unsigned long long cnt[2] = {0ull, 0ull};
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const bool f = isfinite(xr[i]);
+    lvl[i] = f ? (int)fminf((M - xr[i]) * inv_step, 15.f) : 16;
+    const unsigned long long one = f ? (1ull << (4 * (lvl[i] & 15))) : 0ull;
+    cnt[VPT > 15 ? (i & 1) : 0] += one;
+  }
+  unsigned w8[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    unsigned t = 0;
+#pragma unroll
+    for (int a = 0; a < (VPT > 15 ? 2 : 1); ++a) {
+      const unsigned byte = (unsigned)(cnt[a] >> (8 * m)) & 0xffu;
+      t += (byte & 0xfu) | ((byte >> 4) << 16);
+    }
+    w8[m] = t;
+  }
+  const unsigned red = wave_reduce8(w8, lane);
+  if ((lane & 7) == 0) s.lvc[wave][lane >> 3] = red;
+  __syncthreads();
+  // All counts into registers at once (uniform values), then scalar math.
+  uint4 lv[WAVES][2];
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    lv[w][0] = *reinterpret_cast<const uint4*>(&s.lvc[w][0]);
+    lv[w][1] = *reinterpret_cast<const uint4*>(&s.lvc[w][4]);
+  }
+  auto word = [&](int w, int m) -> unsigned {
+    const uint4 q4 = lv[w][m >> 2];
+    const int r = m & 3;
+    return r == 0 ? q4.x : r == 1 ? q4.y : r == 2 ? q4.z : q4.w;
+  };
+  // per level: total over waves, and the count of the waves before this one
+  int tot[16], before_w[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    int t = 0, b = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const int f = (int)((word(w, j >> 1) >> (16 * (j & 1))) & 0xffffu);
+      t += f;
+      b += (w < wave) ? f : 0;
+    }
+    tot[j] = t;
+    before_w[j] = b;
+  }
+  const bool use_k = top_k > 0 && top_k < V;
+  const int keff = use_k ? min(top_k, nfin) : nfin;
+  int L = 15, cum = 0, wbase = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (cum < keff || j == 0) {
+      L = j;
+      cum += tot[j];
+      wbase += before_w[j];
+    }
+  }
+
+  if (cum <= FILTER_MAX) {
+    // ---- compact {lvl <= L} as sort keys: deterministic order (wave, lane,
+    // i).  Every value is written, the rejected ones to a scratch tail of ck,
+    // so the loop has no branches.
+    int myc = 0;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) myc += (lvl[i] <= L) ? 1 : 0;
+    int pos = wave_incl_scan(myc) - myc + wbase;
+    unsigned long long* trash = ck + MAX_V - 64 + lane;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const bool in = lvl[i] <= L;
+      *(in ? ck + pos : trash) = skey(xr[i], tid + i * NT);
+      pos += in ? 1 : 0;
+    }
+    const int n = cum;
+    const int n2 = (n + 1) & ~1;
+    if (tid == n && n < n2) ck[n] = 0ull;
+    __syncthreads();
+    if (n <= 64) {
+      if (wave == 0) {
+        const unsigned long long K = (lane < n) ? ck[lane] : 0ull;
+        const int rank = key_rank(ck, n2, K);
+        if (lane < n) sk[rank] = K;
+        __builtin_amdgcn_wave_barrier();
+        return draw_sorted(sk, use_k ? topk_count(sk, n, top_k) : n, top_p, u, W);
+      }
+      return 0;
+    }
+    if (tid < n) {
+      const unsigned long long K = ck[tid];
+      sk[key_rank(ck, n2, K)] = K;
+    }
+    __syncthreads();
+    if (wave == 0) return draw_sorted(sk, use_k ? topk_count(sk, n, top_k) : n, top_p, u, W);
+    return 0;
+  }
+
+  // ---- general path: exact radix select of the k-th key, then sort
+  uint32_t key[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) key[i] = fkey(xr[i]);
   uint32_t cut = 0u;
-  if (top_k > 0 && top_k < V) {
+  if (use_k) {
     int* H = &s.hist[0][0][0];
     int* Hw = H + (wave * 8 + (lane & 7)) * 256;
     uint32_t prefix = 0u, pmask = 0u;
@@ -850,7 +1128,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[SAMPLE_VPT], int V,
         *reinterpret_cast<int4*>(&H[i]) = make_int4(0, 0, 0, 0);
       __syncthreads();
 #pragma unroll
-      for (int i = 0; i < SAMPLE_VPT; ++i)
+      for (int i = 0; i < VPT; ++i)
         if (tid + i * NT < V && (key[i] & pmask) == prefix) atomicAdd(&Hw[(key[i] >> shift) & 255u], 1);
       __syncthreads();
       // bin 255 - tid summed over the private copies, then a scan over bins.
@@ -874,13 +1152,12 @@ __device__ __forceinline__ int sample_core(const float (&xr)[SAMPLE_VPT], int V,
     cut = prefix;
   }
 
-  // Compact the candidates (finite, key >= cut): deterministic order
-  // (wave, lane, i), no atomics.
-  bool keep[SAMPLE_VPT];
+  // Compact the candidates (finite, key >= cut) as sort keys.
+  bool keep[VPT];
   int myc = 0;
 #pragma unroll
-  for (int i = 0; i < SAMPLE_VPT; ++i) {
-    keep[i] = (tid + i * NT < V) && isfinite(xr[i]) && key[i] >= cut;
+  for (int i = 0; i < VPT; ++i) {
+    keep[i] = isfinite(xr[i]) && key[i] >= cut;
     myc += keep[i] ? 1 : 0;
   }
   const int wincl = wave_incl_scan(myc);
@@ -894,92 +1171,58 @@ __device__ __forceinline__ int sample_core(const float (&xr)[SAMPLE_VPT], int V,
   }
   base += wincl - myc;
 #pragma unroll
-  for (int i = 0; i < SAMPLE_VPT; ++i)
-    if (keep[i]) { cv[base] = xr[i]; ci[base] = tid + i * NT; ++base; }
-  __syncthreads();
-  if (n <= 64) {
-    if (wave == 0) {
-      const int code = (n == 0) ? 0 : draw_wave(cv, ci, n, top_p, u, cv + 64, ci + 64);
-      if (lane == 0) s.code = code;
-    }
-    __syncthreads();
-    return s.code;
-  }
+  for (int i = 0; i < VPT; ++i)
+    if (keep[i]) ck[base++] = skey(xr[i], tid + i * NT);
   int P = 1;
   while (P < n) P <<= 1;
-  for (int i = n + tid; i < P; i += NT) { cv[i] = -INFINITY; ci[i] = 0x7fffffff; }
   __syncthreads();
-  // Bitonic sort in LDS: "before" = larger value, then smaller index.
+  for (int i = n + tid; i < P; i += NT) ck[i] = 0ull;
+  __syncthreads();
+  // Bitonic sort of the keys in LDS, largest first.
   for (int k = 2; k <= P; k <<= 1)
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int i = tid; i < P; i += NT) {
         const int l = i ^ j;
         if (l > i) {
-          const float vi = cv[i], vl = cv[l];
-          const int ii = ci[i], il = ci[l];
-          const bool swap = ((i & k) == 0) ? before(vl, il, vi, ii) : before(vi, ii, vl, il);
-          if (swap) { cv[i] = vl; cv[l] = vi; ci[i] = il; ci[l] = ii; }
+          const unsigned long long ki = ck[i], kl = ck[l];
+          const bool swap = ((i & k) == 0) ? (kl > ki) : (ki > kl);
+          if (swap) { ck[i] = kl; ck[l] = ki; }
         }
       }
       __syncthreads();
     }
-  const double top = (double)cv[0];
-  for (int i = tid; i < n; i += NT) W[i] = exp((double)cv[i] - top);
-  __syncthreads();
-  // Prefix sums: groups of 64 in candidate order, each scanned like
-  // wave_scan_f64, plus the running total of the earlier groups.
-  if (wave == 0) {
-    double carry = 0.0;
-    for (int g0 = 0; g0 < n; g0 += 64) {
-      const double w = (g0 + lane < n) ? W[g0 + lane] : 0.0;
-      const double sc = wave_scan_f64(w);
-      if (g0 + lane < n) W[g0 + lane] = carry + sc;
-      carry = carry + readlane_f64(sc, 63);
-    }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    const double S = W[n - 1];
-    int nk = n;
-    if (top_p > 0.f && top_p < 1.f) {
-      const double thr = (double)top_p * S;
-      for (int i = 0; i + 1 < n; ++i)
-        if (W[i] > thr) { nk = i + 1; break; }
-    }
-    const double target = u * W[nk - 1];
-    int j = nk - 1;
-    for (int i = 0; i < nk; ++i)
-      if (W[i] > target) { j = i; break; }
-    s.code = ci[j];
-  }
-  __syncthreads();
-  return s.code;
+  if (wave == 0) return draw_sorted(ck, n, top_p, u, W);
+  return 0;
 }
 
 // CFG merge u + s (c - u) without contraction, then BOS/PAD (and EOS) -> -inf
 // (model.py:579-584); the merged row is optionally recorded, then kept in
-// registers divided by the temperature when sampling (model.py:696).
-__device__ __forceinline__ void merge_mask(const float* lc, const float* lu, float s, int V,
-                                           int bos, int eos, int pad, const int* mask_flag,
-                                           bool force_mask, float temp, float* dbg,
-                                           float (&xr)[SAMPLE_VPT]) {
-  float uvv[SAMPLE_VPT];
+// registers divided by the temperature when sampling (model.py:696).  Loads
+// are clamped into the row and entries past V become -inf afterwards, so no
+// load sits behind a branch.
+template <int VPT>
+__device__ __forceinline__ void merge_mask(const float* lc, const float* lu, float s, int V, int bos, int eos,
+                                           int pad, const int* mask_flag, bool force_mask, float temp,
+                                           float* dbg, float (&xr)[VPT]) {
+  float cvv[VPT], uvv[VPT];
 #pragma unroll
-  for (int i = 0; i < SAMPLE_VPT; ++i) {
-    const int v = threadIdx.x + i * NT;
-    xr[i] = (v < V) ? lc[v] : -INFINITY;
-    uvv[i] = (lu && v < V) ? lu[v] : 0.f;
+  for (int i = 0; i < VPT; ++i) {
+    const int v = min((int)threadIdx.x + i * NT, V - 1);
+    cvv[i] = lc[v];
+    uvv[i] = lu ? lu[v] : 0.f;
   }
   const bool mask_eos = force_mask || (mask_flag && *mask_flag != 0);
   const bool divide = temp > 0.f;
+  // Chunks below the lowest special id need no mask compares (uniform test).
+  const int lo_special = min(min(bos, pad), mask_eos ? min(eos, V) : V);
 #pragma unroll
-  for (int i = 0; i < SAMPLE_VPT; ++i) {
+  for (int i = 0; i < VPT; ++i) {
     const int v = threadIdx.x + i * NT;
-    if (v >= V) continue;
-    float m = xr[i];
+    float m = cvv[i];
     if (lu) m = __fadd_rn(uvv[i], __fmul_rn(s, __fsub_rn(m, uvv[i])));
-    if (v == bos || v == pad || (mask_eos && v == eos)) m = -INFINITY;
-    if (dbg) dbg[v] = m;
+    if ((i + 1) * NT > lo_special)
+      if (v == bos || v == pad || (mask_eos && v == eos) || v >= V) m = -INFINITY;
+    if (dbg && v < V) dbg[v] = m;
     xr[i] = divide ? m / temp : m;
   }
 }
@@ -1002,18 +1245,19 @@ struct SampleArgs {
 };
 
 // One workgroup per utterance, launched once per codebook q.  Samples the
-// code, records it, advances both rows' prefix (model.py:600-605) and, after
-// the last codebook, writes the frame embedding (model.py:105-114) as the next
-// trunk input and clears the prefix.  Every input that does not depend on the
-// code is loaded in the first round trip (this frame's draws and flags sit at
-// fixed addresses, so nothing waits on the frame counter).
-template <typename TL>
+// code and records it; the next depth step's first GEMV advances the prefix
+// with it (model.py:600-605).  After the last codebook it writes the frame
+// embedding (model.py:105-114) as the next trunk input and clears the prefix
+// the next frame starts from.  Every input that does not depend on the code
+// is loaded in the first round trip (this frame's draws and flags sit at
+// fixed addresses, so nothing waits on the frame counter).  VPT = logits per
+// thread, ceil(V / NT).
+template <typename TL, int VPT>
 __global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
   extern __shared__ unsigned char raw[];
   double* W = reinterpret_cast<double*>(raw);
-  float* x = reinterpret_cast<float*>(W + MAX_V);
-  float* cv = x + MAX_V;
-  int* ci = reinterpret_cast<int*>(cv + MAX_V);
+  unsigned long long* ck = reinterpret_cast<unsigned long long*>(W + MAX_V);
+  unsigned long long* sk = ck + MAX_V;
   __shared__ SampleSmem s;
   __shared__ int codes_l[64];
 
@@ -1025,78 +1269,70 @@ __global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
   const int forced = a.flag_cur[1];
   const int slot = *a.fc;
   const SkParams P = *a.params;
-  if (q + 1 == a.Q && threadIdx.x < a.Q && threadIdx.x != q)
+  const bool last = (q + 1 == a.Q);
+  if (last && threadIdx.x < a.Q && threadIdx.x != q)
     codes_l[threadIdx.x] = a.codes_cur[(size_t)ut * a.Q + threadIdx.x];
   const bool q0 = (q == 0) && P.has_q0;
   const float temp = q0 ? P.temperature_q0 : P.temperature;
   const int topk = q0 ? P.top_k_q0 : P.top_k;
   const float topp = q0 ? P.top_p_q0 : P.top_p;
-  float xr[SAMPLE_VPT];
-  merge_mask(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, a.flag_cur, q != 0, temp,
-             P.record_logits ? a.dbg + ((size_t)ut * a.Q + q) * a.V : nullptr, xr);
-  int code = sample_core(xr, a.V, temp, topk, topp, u, cv, ci, W, s);
+  float xr[VPT];
+  merge_mask<VPT>(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, a.flag_cur, q != 0, temp,
+                  P.record_logits ? a.dbg + ((size_t)ut * a.Q + q) * a.V : nullptr, xr);
+  int code = sample_core<VPT>(xr, a.V, temp, topk, topp, u, ck, sk, W, s);
   const size_t uoff = ((size_t)slot * a.n_utts + ut) * a.Q + q;
-  if (forced) code = (int)a.forced_ring[uoff];
-  code = min(max(code, 0), a.V - 1);
   if (threadIdx.x == 0) {
+    if (forced) code = (int)a.forced_ring[uoff];
+    code = min(max(code, 0), a.V - 1);
     a.codes_ring[uoff] = code;
     a.codes_cur[(size_t)ut * a.Q + q] = code;
+    codes_l[q] = code;
   }
+  if (!last) return;
 
+  __syncthreads();
   const size_t row_stride = (size_t)a.V * a.d;
-  if (q + 1 < a.Q) {
-    const size_t base = (size_t)q * row_stride + (size_t)code * a.d;
-    for (int dd = threadIdx.x; dd < a.d; dd += NT) {
-      const float t = __fmul_rn(TL::get(a.table, base + dd), a.scale);
-      for (int rr = 0; rr < a.rows_per_utt; ++rr) {
-        float* pr = a.prefix + (size_t)(r0 + rr) * a.d;
-        pr[dd] = __fadd_rn(pr[dd], t);
-      }
+  for (int dd = threadIdx.x; dd < a.d; dd += NT) {
+    float e = 0.f;
+    for (int j0 = 0; j0 < a.Q; j0 += 16) {
+      float t[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        t[j] = (j0 + j < a.Q)
+                   ? TL::get(a.table, (size_t)(j0 + j) * row_stride + (size_t)codes_l[j0 + j] * a.d + dd)
+                   : 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (j0 + j < a.Q) e = (j0 + j == 0) ? t[j] : __fadd_rn(e, t[j]);
     }
-  } else {
-    if (threadIdx.x == 0) codes_l[q] = code;
-    __syncthreads();
-    for (int dd = threadIdx.x; dd < a.d; dd += NT) {
-      float e = 0.f;
-      for (int j0 = 0; j0 < a.Q; j0 += 16) {
-        float t[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          t[j] = (j0 + j < a.Q)
-                     ? TL::get(a.table, (size_t)(j0 + j) * row_stride + (size_t)codes_l[j0 + j] * a.d + dd)
-                     : 0.f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (j0 + j < a.Q) e = (j0 + j == 0) ? t[j] : __fadd_rn(e, t[j]);
-      }
-      e = __fmul_rn(e, a.scale);
-      for (int rr = 0; rr < a.rows_per_utt; ++rr) {
-        a.xnext[(size_t)(r0 + rr) * a.d + dd] = e;
-        a.prefix[(size_t)(r0 + rr) * a.d + dd] = 0.f;
-      }
+    e = __fmul_rn(e, a.scale);
+    for (int rr = 0; rr < a.rows_per_utt; ++rr) {
+      a.xnext[(size_t)(r0 + rr) * a.d + dd] = e;
+      a.prefix[(size_t)(r0 + rr) * a.d + dd] = 0.f;
     }
   }
 }
 
 // Standalone sampler (operator API): one utterance, parameters by value.
-__global__ __launch_bounds__(NT) void sample_op_kernel(const float* logits, int rows, int V,
-                                                       float cfg, int q, int mask_eos_q0, int bos,
-                                                       int eos, int pad, float temp, int top_k,
-                                                       float top_p, double u, int64_t* code_out) {
+template <int VPT>
+__global__ __launch_bounds__(NT) void sample_op_kernel(const float* logits, int rows, int V, float cfg, int q,
+                                                       int mask_eos_q0, int bos, int eos, int pad, float temp,
+                                                       int top_k, float top_p, double u, int64_t* code_out) {
   extern __shared__ unsigned char raw[];
   double* W = reinterpret_cast<double*>(raw);
-  float* x = reinterpret_cast<float*>(W + MAX_V);
-  float* cv = x + MAX_V;
-  int* ci = reinterpret_cast<int*>(cv + MAX_V);
+  unsigned long long* ck = reinterpret_cast<unsigned long long*>(W + MAX_V);
+  unsigned long long* sk = ck + MAX_V;
   __shared__ SampleSmem s;
-  float xr[SAMPLE_VPT];
-  merge_mask(logits, rows == 2 ? logits + V : nullptr, cfg, V, bos, eos, pad, nullptr,
-             (q != 0) || mask_eos_q0 != 0, temp, nullptr, xr);
-  const int code = sample_core(xr, V, temp, top_k, top_p, u, cv, ci, W, s);
+  float xr[VPT];
+  merge_mask<VPT>(logits, rows == 2 ? logits + V : nullptr, cfg, V, bos, eos, pad, nullptr,
+                  (q != 0) || mask_eos_q0 != 0, temp, nullptr, xr);
+  const int code = sample_core<VPT>(xr, V, temp, top_k, top_p, u, ck, sk, W, s);
   if (threadIdx.x == 0) *code_out = code;
 }
 
-constexpr size_t SAMPLE_SMEM = (size_t)MAX_V * (sizeof(double) + 2 * sizeof(float) + sizeof(int));
+// Dynamic LDS of the samplers: W (MAX_V doubles), compaction / sort keys
+// (MAX_V), sorted filter keys (FILTER_MAX).
+constexpr size_t SAMPLE_SMEM = (size_t)MAX_V * sizeof(double) + (size_t)(MAX_V + FILTER_MAX) * 8;
 
 // ------------------------------------------------------------ small kernels
 // Final trunk norm + per-row step bookkeeping.  Decode (ring != null): every

@@ -3,6 +3,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "sk_kernels.h"
 #include "soraku_mi355x.h"
 
@@ -113,17 +115,43 @@ static inline GemvArgs gemv_args(const void* w, int N, int K, const float* x, in
   return a;
 }
 
+// Sampler launches pick the instantiation with the fewest logits per thread
+// that covers V: 1, 2, 4, 9 or 16 (V <= MAX_V).
+template <typename F>
+static hipError_t with_vpt(int V, F&& f) {
+  const int need = (V + NT - 1) / NT;
+  if (need <= 1) return f(std::integral_constant<int, 1>{});
+  if (need <= 2) return f(std::integral_constant<int, 2>{});
+  if (need <= 4) return f(std::integral_constant<int, 4>{});
+  if (need <= 9) return f(std::integral_constant<int, 9>{});
+  return f(std::integral_constant<int, 16>{});
+}
+
+template <typename TL>
+static hipError_t launch_sample_step(const SampleArgs& a, int q, int n_utts, hipStream_t st) {
+  return with_vpt(a.V, [&](auto vpt) {
+    hipLaunchKernelGGL((sample_step_kernel<TL, decltype(vpt)::value>), dim3(n_utts), dim3(NT), SAMPLE_SMEM, st,
+                       a, q);
+    return hipGetLastError();
+  });
+}
+
 static inline hipError_t prepare_sampler() {
   static bool done = false;
   if (done) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sample_step_kernel<WF32>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)SAMPLE_SMEM);
-  if (e == hipSuccess)
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(sample_step_kernel<WBF16>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)SAMPLE_SMEM);
-  if (e == hipSuccess)
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(sample_op_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)SAMPLE_SMEM);
+  hipError_t e = hipSuccess;
+  auto set = [&](const void* fn) {
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)SAMPLE_SMEM);
+  };
+  for (int V : {NT, 2 * NT, 4 * NT, 9 * NT, 16 * NT})
+    with_vpt(V, [&](auto vpt) {
+      constexpr int P = decltype(vpt)::value;
+      set(reinterpret_cast<const void*>(sample_step_kernel<WF32, P>));
+      set(reinterpret_cast<const void*>(sample_step_kernel<WBF16, P>));
+      set(reinterpret_cast<const void*>(sample_op_kernel<P>));
+      return e;
+    });
   if (e == hipSuccess) done = true;
   return e;
 }

@@ -164,3 +164,41 @@ def test_planted_mistakes_are_caught():
         assert err() > 1e-3
     finally:
         og.cfg_merge = orig_merge
+
+
+def test_scan_sums_is_an_inclusive_prefix_sum():
+    """The fixed-order float64 scan of the draw: equal to the running sum
+    exactly for small integers (exact in float64 at any order), within a few
+    ulps of np.cumsum for random weights, at group sizes around 16/64."""
+    from oracle.sampler import scan_sums
+
+    rng = np.random.default_rng(7)
+    for n in (1, 2, 15, 16, 17, 31, 33, 63, 64, 65, 127, 128, 129, 200, 300):
+        ints = rng.integers(0, 1000, n).astype(np.float64)
+        np.testing.assert_array_equal(scan_sums(ints), np.cumsum(ints))
+        w = np.exp(-rng.exponential(3.0, n))
+        got, ref = scan_sums(w), np.cumsum(w)
+        assert np.all(np.abs(got - ref) <= 8 * np.finfo(np.float64).eps * ref), n
+        assert np.all(np.diff(got) >= 0)
+
+
+def test_scan_sums_order_is_the_row_scheme():
+    """The addition order shows in the last bits.  Lanes 0-15 = 1, lane 16 =
+    2^53, lanes 17-31 = 1, lane 32 = 2^53 (spacing 2 above 2^53, 4 above
+    2^54, ties to even).  Row-of-16 scheme by hand: row 0 gives 16 at lane 15;
+    row 1 locally reaches 2^53 + 14 at lane 31 (the first 1 is absorbed,
+    pairs survive), + 16 from row 0 = 2^53 + 30; lane 32 = 2^53 + (2^53 + 30)
+    = 2^54 + 30 -> 2^54 + 32.  A left-to-right sum gives 2^54 + 16 there and
+    a 64-wide Hillis-Steele scan 2^54 + 28."""
+    from oracle.sampler import scan_sums
+
+    w = np.zeros(64)
+    w[0:16] = 1.0
+    w[16] = 2.0 ** 53
+    w[17:32] = 1.0
+    w[32] = 2.0 ** 53
+    got = scan_sums(w)
+    assert got[15] == 16.0
+    assert got[31] == 2.0 ** 53 + 30.0
+    assert got[32] == 2.0 ** 54 + 32.0
+    assert np.cumsum(w)[32] == 2.0 ** 54 + 16.0

@@ -295,6 +295,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
   const int row0 = (blockIdx.x * WAVES + wave) * RW;
 
   constexpr bool ADD = (PRO == PRO_ADDNORM || PRO == PRO_ADDGATHER);
+  // Codes of the gathered table rows first, as vector loads (an opaque zero
+  // lane offset keeps them off the scalar path): waiting on them later then
+  // never waits on the weight stream issued after them.
+  int gc[M];
+  if (PRO == PRO_ADDGATHER) {
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+#pragma unroll
+    for (int m = 0; m < M; ++m) gc[m] = a.gcode[(m / a.g_rpu) * a.gstride + zero];
+  }
   float xv[M][NV][VEC];
   float x2v[ADD ? M : 1][ADD ? NV : 1][VEC];
 #pragma unroll
@@ -311,13 +321,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
           x2v[m][j][i] = w.x; x2v[m][j][i + 1] = w.y; x2v[m][j][i + 2] = w.z; x2v[m][j][i + 3] = w.w;
         }
       }
-  // Codes of the gathered table rows (uniform: scalar loads, which no
-  // vector load waits on).
-  int gc[M];
-  if (PRO == PRO_ADDGATHER) {
-#pragma unroll
-    for (int m = 0; m < M; ++m) gc[m] = a.gcode[(m / a.g_rpu) * a.gstride];
-  }
 
   // Small operands next (norm gains, residual / bias for this lane's
   // outputs), so waiting on them never waits on the weight stream.

@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import re
 import os
 import platform
 import subprocess
@@ -105,6 +106,24 @@ def cpu_baseline(shape, weights, text, prompt, uncond, u, n_frames=6, n_warm=1):
                        f"{n_frames} frames timed after {n_warm} warm-up at prefixes "
                        f"{text.size + 1 + prompt.shape[0]}/{uncond.size + 1 + prompt.shape[0]}; "
                        f"{dt / n_frames * 1e3:.1f} ms/frame; host {cpu_info()}")}
+
+
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "hbm_traffic_decode_frame_q06b_f32.md")
+
+
+def measured_traffic():
+    """HBM bytes per frame from the committed counter summary (FETCH_SIZE +
+    WRITE_SIZE passes, copy-calibrated); None when the summary is absent."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"```json\s*(\{.*?\})\s*```", text, re.S)
+    if not m:
+        return None
+    d = json.loads(m.group(1))
+    return float(d["read_bytes_per_frame"]) + float(d["write_bytes_per_frame"])
 
 
 def copy_probe(mib):
@@ -198,7 +217,9 @@ def main():
                    "us_per_frame_p90": float(np.percentile(per, 90)),
                    "prefill_ms": t_prefill * 1e3},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(),
+                     "traffic_source": "profiles/hbm_traffic_decode_frame_q06b_f32.md (rocprofv3 "
+                                       "FETCH_SIZE + WRITE_SIZE, copy-calibrated, bytes per frame)",
                      "unit_of_work": "one frame = one hipGraph launch",
                      "algorithmic_bytes_per_launch": alg},
     }

@@ -65,6 +65,7 @@ typedef struct sk_config {
   int32_t max_frames;     /* capacity of the per-frame input/code ring          */
   int32_t n_language;     /* language-token rows (0 or 4, model.py:186-197)     */
   int32_t language_ids[4];/* their text ids (model.py:326-338)                  */
+  int32_t kv_dtype;       /* KV cache element: SK_F32 (reference) or SK_BF16    */
 } sk_config;
 
 typedef struct sk_engine sk_engine;
@@ -100,7 +101,8 @@ int sk_prefill_run(sk_engine* e);
 /* Override one row's KV length and RoPE position (after an external prefill). */
 int sk_set_row_state(sk_engine* e, int32_t row, int32_t kv_len, int32_t position);
 /* Device address of layer `layer`'s K (kv=0) or V (kv=1) cache,
- * laid out [rows][n_kv_heads][max_ctx][head_dim] FP32. */
+ * laid out [rows][n_kv_heads][max_ctx][head_dim] of cfg->kv_dtype elements
+ * (FP32, or BF16 bits rounded to nearest even). */
 int sk_kv_ptr(sk_engine* e, int32_t layer, int32_t kv, void** out);
 /* Copy the current depth-input hidden state [rows][d] to host memory. */
 int sk_get_hidden(sk_engine* e, float* host_out);

@@ -105,6 +105,9 @@ def weight_shapes(s: Shape) -> dict[str, tuple[int, ...]]:
 
 
 def is_norm_gain(key: str) -> bool:
+    """Keys the synthetic draw sets to 1 (+ optional noise): the trunk's
+    RMSNorm and q/k-norm gains.  The depth head's ``norm_in`` / ``norm_out``
+    gains are drawn like matrices; the golden vectors were made that way."""
     return key.endswith("norm.weight") or key.endswith("layernorm.weight")
 
 
@@ -210,13 +213,21 @@ class RowState:
 
 
 class OracleModel:
+    """``kv_bf16``: keys (after QK-norm and RoPE) and values are rounded to
+    BF16 when appended to the cache, and every attention reads the rounded
+    values (the BF16-KV configuration; the reference itself keeps FP32)."""
+
     def __init__(self, shape: Shape, weights: dict[str, np.ndarray], dtype=np.float32,
-                 language_token_ids: tuple[int, ...] = ()):
+                 language_token_ids: tuple[int, ...] = (), kv_bf16: bool = False):
         self.s = shape
         self.dtype = np.dtype(dtype)
         self.w = {k: np.asarray(v, self.dtype) for k, v in weights.items()}
         self.language_token_ids = tuple(language_token_ids)
         self.scale_attn = self.dtype.type(shape.head_dim ** -0.5)
+        self.kv_bf16 = kv_bf16
+
+    def _kv_store(self, x):
+        return round_bf16(np.asarray(x, np.float32)).astype(self.dtype) if self.kv_bf16 else x
 
     # ---- embeddings -----------------------------------------------------
     def frame_embedding(self, codes) -> np.ndarray:
@@ -282,8 +293,8 @@ class OracleModel:
             q, k, v = self._qkv(i, h)
             q = apply_rope(q, cos[:, None, :], sin[:, None, :])
             k = apply_rope(k, cos[:, None, :], sin[:, None, :])
-            st.k[i, :, p0:ctx] = k.transpose(1, 0, 2)
-            st.v[i, :, p0:ctx] = v.transpose(1, 0, 2)
+            st.k[i, :, p0:ctx] = self._kv_store(k.transpose(1, 0, 2))
+            st.v[i, :, p0:ctx] = self._kv_store(v.transpose(1, 0, 2))
             kk = np.repeat(st.k[i, :, :ctx], rep, axis=0)
             vv = np.repeat(st.v[i, :, :ctx], rep, axis=0)
             sc = np.einsum("nhd,htd->hnt", q, kk) * self.scale_attn
@@ -310,8 +321,8 @@ class OracleModel:
             outs = []
             for r, st in enumerate(states):
                 t = st.kv_len
-                st.k[i, :, t] = k[r]
-                st.v[i, :, t] = v[r]
+                st.k[i, :, t] = self._kv_store(k[r])
+                st.v[i, :, t] = self._kv_store(v[r])
                 outs.append(attend(q[r], st.k[i, :, : t + 1], st.v[i, :, : t + 1], self.scale_attn))
             o = np.stack(outs).reshape(len(states), -1)
             h = h + o @ self._lw(i, "self_attn.o_proj.weight").T

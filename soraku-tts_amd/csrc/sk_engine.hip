@@ -61,7 +61,8 @@ struct sk_engine {
   float *x = nullptr, *hidden = nullptr, *prefix = nullptr, *prefix2 = nullptr, *abuf = nullptr,
         *ybuf = nullptr;
   float *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
-  float *kc = nullptr, *vc = nullptr, *inv_freq = nullptr;
+  char *kc = nullptr, *vc = nullptr;   // KV caches, cfg.kv_dtype elements
+  float *inv_freq = nullptr;
   float *part = nullptr, *dbg = nullptr, *embeds = nullptr;
   int *kv_len = nullptr, *pos = nullptr, *active = nullptr, *plen = nullptr;
   int *fc = nullptr, *pf_t = nullptr, *flag_ring = nullptr, *flag_cur = nullptr;
@@ -85,6 +86,9 @@ namespace {
 
 size_t kv_layer_elems(const sk_engine* e) {
   return (size_t)e->rows * e->c.n_kv_heads * e->c.max_ctx * e->c.head_dim;
+}
+size_t kv_layer_bytes(const sk_engine* e) {
+  return kv_layer_elems(e) * (e->c.kv_dtype == SK_BF16 ? 2 : 4);
 }
 
 void drop_graphs(sk_engine* e) {
@@ -115,6 +119,7 @@ int validate_config(const sk_config* c) {
   SK_CHECK(c->trunk_eps > 0.f && c->depth_eps > 0.f && c->rope_theta > 0.f, SK_EINVAL,
            "eps and rope_theta must be positive");
   SK_CHECK(c->weight_dtype == SK_F32 || c->weight_dtype == SK_BF16, SK_EINVAL, "weight_dtype must be SK_F32 or SK_BF16");
+  SK_CHECK(c->kv_dtype == SK_F32 || c->kv_dtype == SK_BF16, SK_EINVAL, "kv_dtype must be SK_F32 or SK_BF16");
   SK_CHECK(c->cfg_rows == 1 || c->cfg_rows == 2, SK_EINVAL, "cfg_rows must be 1 or 2");
   SK_CHECK(c->n_utts >= 1 && c->n_utts * c->cfg_rows <= 4, SK_EINVAL,
            "n_utts * cfg_rows must be in [1, 4] (decode rows)");
@@ -170,8 +175,8 @@ hipError_t enqueue_trunk(sk_engine* e) {
 
     AttnArgs at{};
     at.qkv = e->qkv; at.ldqkv = e->nqkv;
-    at.kc = e->kc + (size_t)l * kv_layer_elems(e);
-    at.vc = e->vc + (size_t)l * kv_layer_elems(e);
+    at.kc = e->kc + (size_t)l * kv_layer_bytes(e);
+    at.vc = e->vc + (size_t)l * kv_layer_bytes(e);
     at.qn_w = w.q_norm; at.kn_w = w.k_norm; at.eps = c.trunk_eps;
     at.inv_freq = e->inv_freq;
     at.part = e->part; at.max_chunks = e->max_chunks;
@@ -180,7 +185,11 @@ hipError_t enqueue_trunk(sk_engine* e) {
     at.Hq = c.n_q_heads; at.Hkv = c.n_kv_heads; at.hd = hd; at.max_ctx = c.max_ctx;
     at.scale = 1.0f / sqrtf((float)hd);
     const size_t asmem = attn_smem_floats(e->G, hd) * sizeof(float);
-    hipLaunchKernelGGL(attention_kernel, dim3(e->max_chunks, c.n_kv_heads, M), dim3(NT), asmem,
+    if (c.kv_dtype == SK_BF16)
+      hipLaunchKernelGGL(attention_kernel<uint16_t>, dim3(e->max_chunks, c.n_kv_heads, M), dim3(NT), asmem,
+                         e->stream, at);
+    else
+      hipLaunchKernelGGL(attention_kernel<float>, dim3(e->max_chunks, c.n_kv_heads, M), dim3(NT), asmem,
                        e->stream, at);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL(attention_combine_kernel, dim3(c.n_q_heads, M), dim3(NT), 0, e->stream, at);
@@ -348,8 +357,8 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   ALLOC(e->abuf, R * d); ALLOC(e->ybuf, R * d);
   ALLOC(e->qkv, R * e->nqkv); ALLOC(e->attn, R * c.n_q_heads * c.head_dim);
   ALLOC(e->act, R * e->inner_max); ALLOC(e->logits, R * V);
-  ALLOC(e->kc, (size_t)c.n_layers * kv_layer_elems(e));
-  ALLOC(e->vc, (size_t)c.n_layers * kv_layer_elems(e));
+  ALLOC(e->kc, (size_t)c.n_layers * kv_layer_bytes(e));
+  ALLOC(e->vc, (size_t)c.n_layers * kv_layer_bytes(e));
   ALLOC(e->inv_freq, (size_t)c.head_dim / 2);
   ALLOC(e->part, R * c.n_q_heads * e->max_chunks * (c.head_dim + 2));
   ALLOC(e->kv_len, R); ALLOC(e->pos, R); ALLOC(e->active, R); ALLOC(e->plen, R);
@@ -384,7 +393,8 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   if (he == hipSuccess) he = hipMemcpy(e->params, &e->p_host, sizeof(SkParams), hipMemcpyHostToDevice);
   if (he == hipSuccess) he = prepare_sampler();
   if (he == hipSuccess)
-    he = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
+    he = hipFuncSetAttribute(c.kv_dtype == SK_BF16 ? reinterpret_cast<const void*>(attention_kernel<uint16_t>)
+                                                   : reinterpret_cast<const void*>(attention_kernel<float>),
                              hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)(attn_smem_floats(e->G, c.head_dim) * sizeof(float)));
   if (he != hipSuccess) { fail(SK_EHIP, "engine init: %s", hipGetErrorString(he)); return bail(SK_EHIP); }
@@ -555,7 +565,7 @@ int sk_kv_ptr(sk_engine* e, int32_t layer, int32_t kv, void** out) {
   SK_CHECK(e && out, SK_EINVAL, "engine and out must be non-NULL");
   SK_CHECK(layer >= 0 && layer < e->c.n_layers, SK_EINVAL, "layer out of range");
   SK_CHECK(kv == 0 || kv == 1, SK_EINVAL, "kv must be 0 (K) or 1 (V)");
-  *out = (kv ? e->vc : e->kc) + (size_t)layer * kv_layer_elems(e);
+  *out = (kv ? e->vc : e->kc) + (size_t)layer * kv_layer_bytes(e);
   return SK_OK;
 }
 

@@ -494,7 +494,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_rows_kernel(const float* x, const 
 // scratch, merged by attention_combine_kernel.
 struct AttnArgs {
   const float* qkv; int ldqkv;           // [rows][(Hq + 2 Hkv) hd] raw projections
-  float* kc; float* vc;                  // this layer: [rows][Hkv][max_ctx][hd]
+  void* kc; void* vc;                    // this layer: [rows][Hkv][max_ctx][hd], FP32 or BF16
   const float* qn_w; const float* kn_w; float eps;
   const float* inv_freq;                 // [hd/2]
   const int* kv_len; const int* pos; const int* active;
@@ -545,6 +545,16 @@ __device__ __forceinline__ float group_sum_first(float v, int lpt) {
 // and the new key get Qwen3's per-head RMSNorm then rotate-half RoPE with
 // angle = fp32(pos * inv_freq) and cos/sin evaluated in double, rounded once;
 // the workgroup owning the new token appends its K/V to the cache.
+// FP32 -> BF16 bits, round to nearest even (the KV cache's BF16 storage).
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(bf16_bits(x) << 16); }
+
+// KT: element type of the KV cache, float or uint16_t (BF16 bits).
+template <typename KT>
 __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int c = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
@@ -586,16 +596,36 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   const int TPP = NT / LPT;              // tokens per pass
   const int npass = (ATT_CHUNK + TPP - 1) / TPP;
   const int sub = tid % LPT, tok = tid / LPT;
-  float4 kr[ATT_DPL / 4], vr[ATT_DPL / 4];
+  constexpr bool KBF = sizeof(KT) == 2;
+  constexpr int NLD = ATT_DPL * (int)sizeof(KT) / 16;   // 16-byte loads per row slice
+  uint4 kraw[NLD], vraw[NLD];
   // Unconditional (token index clamped into the cache), so the compiler can
   // count these loads exactly and wait on the small ones above separately.
   auto load_tok = [&](int pass) {
     const int tl = min(pass * TPP + tok, ATT_CHUNK - 1);
     const int t = min(t_begin + tl, a.max_ctx - 1);
-    const float4* kp = reinterpret_cast<const float4*>(a.kc + (head_base + t) * hd + sub * ATT_DPL);
-    const float4* vp = reinterpret_cast<const float4*>(a.vc + (head_base + t) * hd + sub * ATT_DPL);
+    const uint4* kp = reinterpret_cast<const uint4*>(static_cast<const KT*>(a.kc) + (head_base + t) * hd + sub * ATT_DPL);
+    const uint4* vp = reinterpret_cast<const uint4*>(static_cast<const KT*>(a.vc) + (head_base + t) * hd + sub * ATT_DPL);
 #pragma unroll
-    for (int i = 0; i < ATT_DPL / 4; ++i) { kr[i] = kp[i]; vr[i] = vp[i]; }
+    for (int i = 0; i < NLD; ++i) { kraw[i] = kp[i]; vraw[i] = vp[i]; }
+  };
+  // raw cache words -> 16 FP32 values
+  auto widen = [&](const uint4 (&raw)[NLD], float4 (&out)[ATT_DPL / 4]) {
+    if constexpr (KBF) {
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          out[2 * i + j] = make_float4(__uint_as_float(w[2 * j] << 16), __uint_as_float(w[2 * j] & 0xffff0000u),
+                                       __uint_as_float(w[2 * j + 1] << 16), __uint_as_float(w[2 * j + 1] & 0xffff0000u));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NLD; ++i)
+        out[i] = make_float4(__uint_as_float(raw[i].x), __uint_as_float(raw[i].y), __uint_as_float(raw[i].z),
+                             __uint_as_float(raw[i].w));
+    }
   };
   load_tok(0);
   const int ctx = T + 1;
@@ -627,16 +657,31 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
-  if (last)
+  // Append the new token.  A BF16 cache stores it rounded, and this step then
+  // attends to the rounded values too, as every later step will.
+  if (last) {
     for (int d = tid; d < hd; d += NT) {
-      a.kc[(head_base + T) * hd + d] = knew[d];
-      a.vc[(head_base + T) * hd + d] = vnew[d];
+      if constexpr (KBF) {
+        static_cast<KT*>(a.kc)[(head_base + T) * hd + d] = (KT)bf16_bits(knew[d]);
+        static_cast<KT*>(a.vc)[(head_base + T) * hd + d] = (KT)bf16_bits(vnew[d]);
+      } else {
+        static_cast<KT*>(a.kc)[(head_base + T) * hd + d] = knew[d];
+        static_cast<KT*>(a.vc)[(head_base + T) * hd + d] = vnew[d];
+      }
     }
+    if constexpr (KBF) {
+      for (int d = tid; d < hd; d += NT) { knew[d] = bf16_round(knew[d]); vnew[d] = bf16_round(vnew[d]); }
+      __syncthreads();                   // `last` is uniform over the workgroup
+    }
+  }
 
   for (int pass = 0; pass < npass; ++pass) {
     const int tl = pass * TPP + tok;
     const int t = t_begin + tl;
     if (pass > 0) load_tok(pass);
+    float4 kr[ATT_DPL / 4], vr[ATT_DPL / 4];
+    widen(kraw, kr);
+    widen(vraw, vr);
     if (tl < n_t && t == T) {
 #pragma unroll
       for (int i = 0; i < ATT_DPL / 4; ++i) {

@@ -31,6 +31,7 @@ class SkConfig(C.Structure):
         ("rope_theta", C.c_float), ("frame_scale", C.c_float), ("weight_dtype", C.c_int32),
         ("n_utts", C.c_int32), ("cfg_rows", C.c_int32), ("max_ctx", C.c_int32),
         ("max_frames", C.c_int32), ("n_language", C.c_int32), ("language_ids", C.c_int32 * 4),
+        ("kv_dtype", C.c_int32),
     ]
 
 

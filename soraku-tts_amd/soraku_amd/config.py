@@ -84,7 +84,7 @@ def shape_from_model(model) -> DecodeShape:
 
 
 def to_sk_config(s: DecodeShape, *, n_utts: int, cfg_rows: int, max_ctx: int, max_frames: int,
-                 bf16: bool = False, language_ids=()) -> SkConfig:
+                 bf16: bool = False, language_ids=(), kv_bf16: bool = False) -> SkConfig:
     c = SkConfig()
     c.d_model, c.n_layers, c.n_q_heads, c.n_kv_heads = s.d_model, s.n_layers, s.n_q_heads, s.n_kv_heads
     c.head_dim, c.trunk_inter, c.depth_inner = s.head_dim, s.trunk_inter, s.depth_inner
@@ -92,6 +92,7 @@ def to_sk_config(s: DecodeShape, *, n_utts: int, cfg_rows: int, max_ctx: int, ma
     c.bos_id, c.eos_id, c.pad_id = s.bos_id, s.eos_id, s.pad_id
     c.trunk_eps, c.depth_eps, c.rope_theta, c.frame_scale = s.trunk_eps, FLT_EPS, s.rope_theta, s.frame_scale
     c.weight_dtype = SK_BF16 if bf16 else SK_F32
+    c.kv_dtype = SK_BF16 if kv_bf16 else SK_F32
     c.n_utts, c.cfg_rows, c.max_ctx, c.max_frames = n_utts, cfg_rows, max_ctx, max_frames
     ids = list(language_ids)
     c.n_language = 4 if ids else 0

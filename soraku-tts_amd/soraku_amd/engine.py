@@ -53,7 +53,7 @@ class GraphFrameEngine:
     def __init__(self, model=None, *, device="cuda:0", max_cache_len: int, cfg_scale: float = 1.5,
                  batch: int = 2, state_dict=None, shape: DecodeShape | None = None,
                  language_token_ids=(), bf16: bool = False, max_frames: int | None = None,
-                 n_utts: int = 1):
+                 n_utts: int = 1, kv_bf16: bool = False):
         import torch
 
         if model is not None:
@@ -78,6 +78,7 @@ class GraphFrameEngine:
         self.Q = shape.n_codebooks
         self.V = shape.audio_vocab
         self.bf16 = bf16
+        self.kv_bf16 = kv_bf16
         self.language_token_ids = tuple(language_token_ids)
         self._weights: dict[str, "torch.Tensor"] = {}
         wdt = torch.bfloat16 if bf16 else torch.float32
@@ -99,7 +100,7 @@ class GraphFrameEngine:
             torch.cuda.synchronize(self.device)
             cfg = to_sk_config(shape, n_utts=n_utts, cfg_rows=batch, max_ctx=self.max_len,
                                max_frames=self.max_frames, bf16=bf16,
-                               language_ids=self.language_token_ids)
+                               language_ids=self.language_token_ids, kv_bf16=kv_bf16)
             h = C.c_void_p()
             check(lib().sk_create(C.byref(cfg), None, C.byref(h)))
         self._h = h

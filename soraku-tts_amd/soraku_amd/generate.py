@@ -28,6 +28,7 @@ class FastGenerator:
     def __init__(self, model=None, *, device="cuda:0", use_tilelang: bool = True,
                  compile_trunk: bool = False, batch_branches: bool = True,
                  native_sampling: bool = True, use_graph: bool = True, bf16: bool = False,
+                 kv_bf16: bool = False,
                  state_dict=None, shape: DecodeShape | None = None, language_token_ids=()):
         cfg = getattr(model, "config", None)
         if cfg is not None and getattr(cfg, "speaker_conditioning", False):
@@ -36,6 +37,7 @@ class FastGenerator:
         self.model = model
         self.device = device
         self.bf16 = bf16
+        self.kv_bf16 = kv_bf16
         self._state_dict = state_dict
         self._shape = shape
         self._language_token_ids = tuple(language_token_ids)
@@ -51,7 +53,7 @@ class FastGenerator:
             e = GraphFrameEngine(self.model, device=self.device, max_cache_len=max(max_len, 512),
                                  cfg_scale=cfg_scale, batch=batch, state_dict=self._state_dict,
                                  shape=self._shape, language_token_ids=self._language_token_ids,
-                                 bf16=self.bf16)
+                                 bf16=self.bf16, kv_bf16=self.kv_bf16)
             self._engine, self._engine_key = e, key
         return e
 

@@ -4,6 +4,8 @@ Weights are drawn in sorted state-dict-key order from
 ``numpy.random.default_rng(seed)``: matrices / embeddings / codebook tables
 N(0, 0.02) (model.py:103, initializer_range), RMSNorm gains 1 (or
 1 + N(0, norm_gain_std)), depth bias 0 (or N(0, bias_std), model.py:138-140).
+The depth head's ``norm_in`` / ``norm_out`` gains are drawn like the matrices
+(N(0, 0.02)); the committed golden vectors were made with that draw.
 """
 
 from __future__ import annotations
@@ -47,7 +49,8 @@ def weight_shapes(s: DecodeShape) -> dict[str, tuple[int, ...]]:
 def is_matrix(key: str) -> bool:
     """Tensors stored in the engine's weight dtype (everything but gains,
     bias and language rows)."""
-    return not (key.endswith("norm.weight") or key.endswith("layernorm.weight")
+    parts = key.split(".")
+    return not ((len(parts) >= 2 and "norm" in parts[-2])
                 or key in ("depth_head.bias", "language_embeddings.weight"))
 
 

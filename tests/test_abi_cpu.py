@@ -41,10 +41,20 @@ def test_binding_covers_header():
 
 
 def test_config_struct_layout_matches_header():
-    """sk_config: 23 int32/float fields then int32[4] = 108 bytes."""
+    """sk_config: 23 int32/float fields, int32[4], then kv_dtype = 112 bytes;
+    the field names and order are those of include/soraku_mi355x.h."""
+    import re
+
+    from conftest import ROOT
     from soraku_amd._lib import SkConfig
 
-    assert C.sizeof(SkConfig) == 23 * 4 + 16
+    assert C.sizeof(SkConfig) == 23 * 4 + 16 + 4
+    hdr = open(f"{ROOT}/include/soraku_mi355x.h").read()
+    body = hdr[hdr.index("typedef struct sk_config {"):hdr.index("} sk_config;")]
+    names = re.findall(r"(?:int32_t|float)\s+([^;]+);", body)
+    fields = [n.strip() for group in names for n in group.split(",")]
+    fields = [re.sub(r"\[.*\]", "", f).strip() for f in fields]
+    assert fields == [f[0] for f in SkConfig._fields_]
 
 
 def _good_config():
@@ -56,7 +66,7 @@ def _good_config():
 @pytest.mark.parametrize("field,value", [
     ("d_model", 12), ("head_dim", 24), ("n_kv_heads", 3), ("cfg_rows", 3), ("n_utts", 0),
     ("audio_vocab", 5000), ("max_ctx", 1), ("bos_id", 35), ("weight_dtype", 7), ("n_language", 2),
-    ("trunk_eps", 0.0),
+    ("trunk_eps", 0.0), ("kv_dtype", 5),
 ])
 def test_create_rejects_bad_config(L, field, value):
     from soraku_amd._lib import SK_EINVAL

@@ -178,3 +178,188 @@ def test_engine_error_paths(hip_device):
     with pytest.raises(ValueError):
         e.prefill(np.arange(n_prefix + 5) % s.text_vocab, f["uncond_ids"], f["prompt_codes"])
     e.close()
+
+
+def _oracle_forced_logits(m, s, text, prompt, uncond, codes, cfg, states=None):
+    """Masked merged logits [frames*Q, V] of the oracle under teacher forcing
+    (from prefilled ``states`` when given)."""
+    rec = Record()
+    n = codes.shape[0]
+    generate(m, input_ids=text, prompt_codes=prompt, uncond_input_ids=uncond, max_new_frames=n,
+             min_new_frames=0, temperature=0.0, cfg_scale=cfg, forced_codes=codes, batched=True,
+             record=rec, states=states)
+    out = [apply_masks(mg, q=q, frame_index=fi, min_new_frames=0, bos_id=s.bos_id, eos_id=s.eos_id,
+                       pad_id=s.pad_id)
+           for fi, fr in enumerate(rec.merged) for q, mg in enumerate(fr)]
+    return np.stack(out)
+
+
+def _engine_forced_logits(e, s, codes):
+    out = []
+    for fi in range(codes.shape[0]):
+        _, lg = e.step_frame(mask_eos_q0=False, uniforms=np.zeros(s.n_codebooks), forced_codes=codes[fi],
+                             return_logits=True)
+        out.extend(lg[0])
+    return np.stack(out)
+
+
+def _bf16_weights(w):
+    from oracle.model import round_bf16
+    from soraku_amd.synthetic import is_matrix
+
+    return {k: (round_bf16(v) if is_matrix(k) else v) for k, v in w.items()}
+
+
+@pytest.mark.parametrize("bf16_w,bf16_kv", [(False, True), (True, False), (True, True)])
+def test_bf16_weights_and_kv_cache_match_oracle(hip_device, bf16_w, bf16_kv):
+    """Tiny shape with BF16 matrices (FP32 accumulation) and / or a BF16 KV
+    cache, teacher-forced against the oracle holding the same BF16-rounded
+    weights and rounding K/V at append."""
+    from oracle.model import TINY
+    from soraku_amd import GraphFrameEngine
+
+    s = TINY
+    w = synthetic_weights(s, 21, norm_gain_std=0.1, bias_std=0.02)
+    if bf16_w:
+        w = _bf16_weights(w)
+    rng = np.random.default_rng(5)
+    text, uncond = rng.integers(0, s.text_vocab, 9), np.array([3])
+    prompt = rng.integers(0, s.codebook_size, (5, s.n_codebooks))
+    codes = rng.integers(0, s.codebook_size, (6, s.n_codebooks))
+    cfg = 1.5
+    ref = _oracle_forced_logits(OracleModel(s, w, np.float64, kv_bf16=bf16_kv), s, text, prompt, uncond,
+                                codes, cfg)
+    e = GraphFrameEngine(device=hip_device, max_cache_len=40, cfg_scale=cfg, batch=2, state_dict=w,
+                         shape=_shape(s), bf16=bf16_w, kv_bf16=bf16_kv)
+    e.set_temperature(0.0)
+    e.set_debug(True)
+    e.prefill(text, uncond, prompt)
+    e.capture()
+    got = _engine_forced_logits(e, s, codes)
+    e.close()
+    rel = _rowwise_rel(got, ref)
+    print(f"bf16 weights {bf16_w} kv {bf16_kv}: max row-relative logit error {rel:.3e}")
+    assert rel < LOGIT_TOL
+
+
+def _device_weights(s, seed, hip_device):
+    """Seeded N(0, 0.02) matrices drawn on the GPU and rounded to BF16 there
+    (round to nearest even, as round_bf16), unit norm gains, zero bias;
+    returned as FP32 NumPy arrays shared by oracle and engine."""
+    import torch
+    from soraku_amd.synthetic import is_matrix, weight_shapes
+
+    g = torch.Generator(device=hip_device)
+    g.manual_seed(seed)
+    out = {}
+    for key, shp in weight_shapes(s).items():
+        if is_matrix(key):
+            t = torch.randn(shp, generator=g, device=hip_device, dtype=torch.float32) * 0.02
+            t = t.to(torch.bfloat16).to(torch.float32)
+        elif key == "depth_head.bias":
+            t = torch.zeros(shp, device=hip_device)
+        else:
+            t = 1.0 + 0.1 * torch.randn(shp, generator=g, device=hip_device, dtype=torch.float32)
+        out[key] = t.cpu().numpy()
+    return out
+
+
+def _engine_kv_bits(e, layer, kv):
+    """Layer ``layer``'s BF16 K (kv=0) or V (kv=1) cache as uint16 bits
+    ``[rows, n_kv_heads, max_ctx, head_dim]``, copied through the HIP runtime
+    the library is linked against (the address comes from sk_kv_ptr)."""
+    import ctypes as C
+
+    from soraku_amd._lib import check, lib
+
+    p = C.c_void_p()
+    check(lib().sk_kv_ptr(e._h, layer, kv, C.byref(p)))
+    e.synchronize()
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    s = e.shape
+    out = np.empty((e.rows, s.n_kv_heads, e.max_len, s.head_dim), np.uint16)
+    assert hip.hipMemcpy(out.ctypes.data, p, out.nbytes, 2) == 0  # hipMemcpyDeviceToHost
+    return out
+
+
+def test_qwen3_17b_shape_bf16_weights_and_kv(hip_device):
+    """Larger backbone configuration: Qwen3-1.7B shape (d 2048, inter 6144,
+    depth inner 4096, 28 layers, 16 Q / 8 KV heads), BF16 weights with FP32
+    accumulation and a BF16 KV cache, CFG batch 2, 3 teacher-forced frames
+    after a short prefix.  The text vocabulary is cut to 4096 rows: only
+    prefix ids are ever embedded.
+
+    Rounding K/V to BF16 is discontinuous, so FP32-level differences that
+    land a value on the other side of a rounding boundary move it by one BF16
+    ulp (2^-8 relative), and 28 layers carry that to the logits: the oracle's
+    own FP32 run differs from its FP64 run by ~1.8e-3 on this case, against
+    ~5e-6 with an FP32 cache.  So the checks are (1) layer 0, whose inputs
+    are the same embeddings in both, holds the FP64 oracle's BF16 cache
+    except at rare near-ties (< 0.5% of elements), and every cached value is
+    the unrounded FP64 value to within half an ulp plus FP32 noise, and
+    (2) the logits sit within max(1e-3, 2 x that FP32-vs-FP64 spread) of the
+    FP64 oracle: no further from it than an FP32 restatement is.  The FP32-KV
+    case of the same weights is held to 1e-3 (it measures ~2e-6)."""
+    import dataclasses
+
+    from oracle.generate import start_states
+    from oracle.model import QWEN3_17B
+    from soraku_amd import GraphFrameEngine
+
+    s = dataclasses.replace(QWEN3_17B, text_vocab=4096)
+    w = _device_weights(s, 8, hip_device)
+    rng = np.random.default_rng(6)
+    text, uncond = rng.integers(0, s.text_vocab, 12), np.array([7])
+    prompt = rng.integers(0, s.codebook_size, (3, s.n_codebooks))
+    codes = rng.integers(0, s.codebook_size, (3, s.n_codebooks))
+    cfg, max_len = 1.5, 32
+
+    def oracle(dtype, kv_bf16):
+        m = OracleModel(s, w, dtype, kv_bf16=kv_bf16)
+        st = start_states(m, text, prompt, uncond, cfg, max_len)
+        return _oracle_forced_logits(m, s, text, prompt, uncond, codes, cfg, states=st), st
+
+    def engine(kv_bf16):
+        e = GraphFrameEngine(device=hip_device, max_cache_len=max_len, cfg_scale=cfg, batch=2,
+                             state_dict=w, shape=_shape(s), bf16=True, kv_bf16=kv_bf16)
+        e.set_temperature(0.0)
+        e.set_debug(True)
+        e.prefill(text, uncond, prompt)
+        e.capture()
+        got = _engine_forced_logits(e, s, codes)
+        kv = [_engine_kv_bits(e, 0, j) for j in (0, 1)] if kv_bf16 else None
+        e.close()
+        return got, kv
+
+    ref64, st_exact = oracle(np.float64, False)
+    got, _ = engine(False)
+    rel = _rowwise_rel(got, ref64)
+    print(f"Qwen3-1.7B BF16 weights, FP32 KV: max row-relative logit error {rel:.3e}")
+    assert rel < LOGIT_TOL
+
+    ref64, st64 = oracle(np.float64, True)
+    ref32, _ = oracle(np.float32, True)
+    got, kv = engine(True)
+    spread = _rowwise_rel(ref32, ref64)
+    rel = _rowwise_rel(got, ref64)
+    tol = max(LOGIT_TOL, 2 * spread)
+    for j, name in enumerate(("k", "v")):
+        mism, total = 0, 0
+        for r, (st, sx) in enumerate(zip(st64, st_exact)):
+            n = st.kv_len - 1  # the oracle appends the last frame's token before the engine does
+            ref_bits = (getattr(st, name)[0, :, :n].astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+            mine = kv[j][r, :, :n]
+            mism += int((mine != ref_bits).sum())
+            total += mine.size
+            # every value is the unrounded FP64 one to within half a BF16 ulp
+            # plus FP32-level noise (1e-5 of the head vector's largest entry)
+            exact = getattr(sx, name)[0, :, :n]
+            val = (mine.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+            ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(exact), 1e-30))) - 7)
+            amax = np.abs(exact).max(axis=-1, keepdims=True)
+            assert (np.abs(val - exact) <= 0.5 * ulp + 1e-5 * amax).all(), (name, r)
+        print(f"layer 0 {name}: {mism} of {total} BF16 values differ from the FP64 oracle's rounding")
+        assert mism <= total // 200
+    print(f"Qwen3-1.7B BF16 weights + BF16 KV: engine {rel:.3e}, oracle FP32 vs FP64 {spread:.3e}")
+    assert rel < tol

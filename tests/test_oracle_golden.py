@@ -202,3 +202,38 @@ def test_scan_sums_order_is_the_row_scheme():
     assert got[31] == 2.0 ** 53 + 30.0
     assert got[32] == 2.0 ** 54 + 32.0
     assert np.cumsum(w)[32] == 2.0 ** 54 + 16.0
+
+
+def test_bf16_kv_option_rounds_only_the_cache():
+    """kv_bf16 changes nothing but the stored K/V: with weights whose K and V
+    projections are exactly representable after the norm (zero K/V weights)
+    the two modes agree bitwise; with random weights every cached value is a
+    BF16 value and the hidden state moves only by the rounding (< 1e-2
+    relative on the tiny shape)."""
+    from oracle.model import TINY, RowState, round_bf16
+
+    w = synthetic_weights(TINY, 3)
+    emb = np.random.default_rng(4).normal(0, 1, (6, TINY.d_model)).astype(np.float32)
+    outs = []
+    for kv_bf16 in (False, True):
+        m = OracleModel(TINY, w, np.float32, kv_bf16=kv_bf16)
+        st = RowState(TINY, 16, np.float32)
+        outs.append((m.prefill(st, emb), st))
+    (h32, s32), (h16, s16) = outs
+    k = s16.k[:, :, :6]
+    assert np.array_equal(k, round_bf16(k)) and not np.array_equal(s32.k[:, :, :6], round_bf16(s32.k[:, :, :6]))
+    # layer 0 sees identical inputs in both modes: its cache is the rounded FP32 cache
+    assert np.array_equal(round_bf16(s32.k[0, :, :6]), s16.k[0, :, :6])
+    assert np.array_equal(round_bf16(s32.v[0, :, :6]), s16.v[0, :, :6])
+    rel = np.abs(h16 - h32).max() / np.abs(h32).max()
+    assert 0 < rel < 1e-2
+    wz = dict(w)
+    for i in range(TINY.n_layers):
+        for n in ("k_proj", "v_proj"):
+            wz[f"trunk.layers.{i}.self_attn.{n}.weight"] = np.zeros_like(w[f"trunk.layers.{i}.self_attn.{n}.weight"])
+    hz = []
+    for kv_bf16 in (False, True):
+        m = OracleModel(TINY, wz, np.float32, kv_bf16=kv_bf16)
+        st = RowState(TINY, 16, np.float32)
+        hz.append(m.prefill(st, emb))
+    assert np.array_equal(hz[0], hz[1])

@@ -798,15 +798,19 @@ __device__ __forceinline__ uint32_t fkey(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Sampler workgroups: SNT threads, two waves per SIMD, so the latency of
+// one wave's reduction chains is hidden behind the other's.
+constexpr int SNT = 512;
+constexpr int SWAVES = SNT / 64;
+
 struct SampleSmem {
-  int hist[WAVES][8][256];   // radix histograms, private per (wave, lane & 7)
-  int scan[WAVES];
-  int wcount[WAVES];
-  unsigned lvc[WAVES][8];    // per-wave distance-level counts, 16 levels x 16 bits
-  float bv[WAVES];
-  float bs[WAVES];
-  int bi[WAVES];
-  unsigned long long bk[WAVES];
+  int hist[SWAVES][4][256];   // radix histograms, private per (wave, lane & 3)
+  int scan[SWAVES];
+  int wcount[SWAVES];
+  unsigned lvc[SWAVES][8];    // per-wave distance-level counts, 16 levels x 16 bits
+  float4 bst[SWAVES];          // per-wave (max, sum, finite count as int bits, -)
+  unsigned long long bk[SWAVES];
+  int prk[SWAVES][64];        // per-wave partial ranks of the first 64 keys
   int code;
   int sel_digit;
   int sel_excl;
@@ -1000,7 +1004,7 @@ __device__ __forceinline__ int topk_count(const unsigned long long* sk, int n, i
 
 constexpr int FILTER_MAX = 256;          // largest candidate set the distance filter ranks directly
 
-// xr[i] = value of logit v = threadIdx.x + i*NT (registers; -inf past V):
+// xr[i] = value of logit v = threadIdx.x + i*SNT (registers; -inf past V):
 // CFG-merged, masked and, when temperature > 0, divided by the temperature.
 // Follows model.py:686-708: greedy argmax when temperature <= 0; else top-k
 // (ties kept), top-p (shift-by-one, first kept) and the explicit-uniform
@@ -1025,7 +1029,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
     unsigned long long best = 0ull;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const unsigned long long k = skey(xr[i], tid + i * NT);
+      const unsigned long long k = skey(xr[i], tid + i * SNT);
       best = k > best ? k : best;
     }
     best = wave_max_u64(best);
@@ -1033,11 +1037,11 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
     __syncthreads();
     unsigned long long b = s.bk[0];
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) b = s.bk[w] > b ? s.bk[w] : b;
+    for (int w = 1; w < SWAVES; ++w) b = s.bk[w] > b ? s.bk[w] : b;
     return key_index(b);
   }
 
-  // ---- block maximum, sum and count of the finite values
+  // ---- block maximum, sum and count of the finite values (count by ballot)
   float mx = -INFINITY, sm = 0.f;
   int nf = 0;
 #pragma unroll
@@ -1045,23 +1049,28 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
     const bool f = isfinite(xr[i]);
     mx = f ? fmaxf(mx, xr[i]) : mx;
     sm += f ? xr[i] : 0.f;
-    nf += f ? 1 : 0;
+    nf += __popcll(__ballot(f));
   }
   mx = wave_max_dpp(mx);
   sm = wave_sum_dpp(sm);
-  nf = wave_sum_i(nf);
-  if (lane == 0) { s.bv[wave] = mx; s.bs[wave] = sm; s.bi[wave] = nf; }
+  if (lane == 0) s.bst[wave] = make_float4(mx, sm, __int_as_float(nf), 0.f);
   __syncthreads();
-  float M = s.bv[0], S = s.bs[0];
-  int nfin = s.bi[0];
+  float4 b0 = s.bst[0];
+  float M = b0.x, S = b0.y;
+  int nfin = __float_as_int(b0.z);
 #pragma unroll
-  for (int w = 1; w < WAVES; ++w) { M = fmaxf(M, s.bv[w]); S += s.bs[w]; nfin += s.bi[w]; }
+  for (int w = 1; w < SWAVES; ++w) {
+    const float4 bw = s.bst[w];
+    M = fmaxf(M, bw.x); S += bw.y; nfin += __float_as_int(bw.z);
+  }
   if (nfin == 0) return 0;               // every entry masked: nothing to draw
 
   // ---- distance levels lvl = min(15, floor((M - x) * 16 / (M - mean))),
   // counted in 4-bit fields (two accumulators when a thread holds > 15)
-  const float spread = M - S / (float)nfin;
-  const float inv_step = spread > 0.f ? 16.f / spread : 0.f;
+  // Any monotone level function keeps the selection exact: approximate
+  // reciprocals suffice.
+  const float spread = M - S * __builtin_amdgcn_rcpf((float)nfin);
+  const float inv_step = spread > 0.f ? 16.f * __builtin_amdgcn_rcpf(spread) : 0.f;
   int lvl[VPT];
   unsigned long long cnt[2] = {0ull, 0ull};
 #pragma unroll
@@ -1085,67 +1094,76 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
   const unsigned red = wave_reduce8(w8, lane);
   if ((lane & 7) == 0) s.lvc[wave][lane >> 3] = red;
   __syncthreads();
-  // All counts into registers at once (uniform values), then scalar math.
-  uint4 lv[WAVES][2];
-#pragma unroll
-  for (int w = 0; w < WAVES; ++w) {
-    lv[w][0] = *reinterpret_cast<const uint4*>(&s.lvc[w][0]);
-    lv[w][1] = *reinterpret_cast<const uint4*>(&s.lvc[w][4]);
-  }
-  auto word = [&](int w, int m) -> unsigned {
-    const uint4 q4 = lv[w][m >> 2];
-    const int r = m & 3;
-    return r == 0 ? q4.x : r == 1 ? q4.y : r == 2 ? q4.z : q4.w;
-  };
-  // per level: total over waves, and the count of the waves before this one
-  int tot[16], before_w[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  // Lane j (of every row of 16 lanes) owns level j: its count over all waves
+  // and over the waves before this one, then inclusive scans over the 16
+  // levels.  L = the first level whose cumulative count reaches keff (15 if
+  // none does): {lvl <= L} holds every top-k member.
+  const bool use_k = top_k > 0 && top_k < V;
+  const int keff = use_k ? min(top_k, nfin) : nfin;
+  int L, cum, wbase;
+  {
+    const int j = lane & 15;
     int t = 0, b = 0;
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      const int f = (int)((word(w, j >> 1) >> (16 * (j & 1))) & 0xffffu);
+    for (int w = 0; w < SWAVES; ++w) {
+      const int f = (int)((s.lvc[w][j >> 1] >> (16 * (j & 1))) & 0xffffu);
       t += f;
       b += (w < wave) ? f : 0;
     }
-    tot[j] = t;
-    before_w[j] = b;
-  }
-  const bool use_k = top_k > 0 && top_k < V;
-  const int keff = use_k ? min(top_k, nfin) : nfin;
-  int L = 15, cum = 0, wbase = 0;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    if (cum < keff || j == 0) {
-      L = j;
-      cum += tot[j];
-      wbase += before_w[j];
-    }
+    t += dpp_i<0x111, 0xf, true>(t);   // row_shr:1
+    t += dpp_i<0x112, 0xf, true>(t);   // row_shr:2
+    t += dpp_i<0x114, 0xf, true>(t);   // row_shr:4
+    t += dpp_i<0x118, 0xf, true>(t);   // row_shr:8
+    b += dpp_i<0x111, 0xf, true>(b);
+    b += dpp_i<0x112, 0xf, true>(b);
+    b += dpp_i<0x114, 0xf, true>(b);
+    b += dpp_i<0x118, 0xf, true>(b);
+    const unsigned long long reach = __ballot(lane < 16 && t >= keff);
+    L = reach ? min(__ffsll((long long)reach) - 1, 15) : 15;
+    cum = __builtin_amdgcn_readlane(t, L);
+    wbase = __builtin_amdgcn_readlane(b, L);
   }
 
   if (cum <= FILTER_MAX) {
-    // ---- compact {lvl <= L} as sort keys: deterministic order (wave, lane,
-    // i).  Every value is written, the rejected ones to a scratch tail of ck,
-    // so the loop has no branches.
-    int myc = 0;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) myc += (lvl[i] <= L) ? 1 : 0;
-    int pos = wave_incl_scan(myc) - myc + wbase;
-    unsigned long long* trash = ck + MAX_V - 64 + lane;
+    // ---- compact {lvl <= L} as sort keys in the deterministic order (wave,
+    // slot i, lane): a ballot per slot, the lane's offset by mbcnt.
+    int pos = wbase;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const bool in = lvl[i] <= L;
-      *(in ? ck + pos : trash) = skey(xr[i], tid + i * NT);
-      pos += in ? 1 : 0;
+      const unsigned long long bm = __ballot(in);
+      if (in)
+        ck[pos + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bm >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bm, 0u))] =
+            skey(xr[i], tid + i * SNT);
+      pos += __popcll(bm);
     }
     const int n = cum;
     const int n2 = (n + 1) & ~1;
     if (tid == n && n < n2) ck[n] = 0ull;
     __syncthreads();
     if (n <= 64) {
+      // Wave w counts, for each of the first 64 keys (one per lane), the keys
+      // of its slice [8w, 8w + 8) that sort before it; wave 0 adds the slices.
+      static_assert(SWAVES * 8 >= 64, "rank slices must cover 64 keys");
+      const unsigned long long K = (lane < n) ? ck[lane] : 0ull;
+      int part = 0;
+      if (8 * wave < n2) {
+        const ulonglong2* kp = reinterpret_cast<const ulonglong2*>(ck + 8 * wave);
+        ulonglong2 kk[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) kk[t] = kp[t];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int j = 8 * wave + 2 * t;
+          part += (j < n2 && kk[t].x > K ? 1 : 0) + (j + 1 < n2 && kk[t].y > K ? 1 : 0);
+        }
+      }
+      s.prk[wave][lane] = part;
+      __syncthreads();
       if (wave == 0) {
-        const unsigned long long K = (lane < n) ? ck[lane] : 0ull;
-        const int rank = key_rank(ck, n2, K);
+        int rank = 0;
+#pragma unroll
+        for (int w = 0; w < SWAVES; ++w) rank += s.prk[w][lane];
         if (lane < n) sk[rank] = K;
         __builtin_amdgcn_wave_barrier();
         return draw_sorted(sk, use_k ? topk_count(sk, n, top_k) : n, top_p, u, W);
@@ -1168,21 +1186,24 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
   uint32_t cut = 0u;
   if (use_k) {
     int* H = &s.hist[0][0][0];
-    int* Hw = H + (wave * 8 + (lane & 7)) * 256;
+    int* Hw = H + (wave * 4 + (lane & 3)) * 256;
     uint32_t prefix = 0u, pmask = 0u;
     int kr = top_k;
     for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = tid * 4; i < WAVES * 8 * 256; i += NT * 4)
+      for (int i = tid * 4; i < SWAVES * 4 * 256; i += SNT * 4)
         *reinterpret_cast<int4*>(&H[i]) = make_int4(0, 0, 0, 0);
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < VPT; ++i)
-        if (tid + i * NT < V && (key[i] & pmask) == prefix) atomicAdd(&Hw[(key[i] >> shift) & 255u], 1);
+        if (tid + i * SNT < V && (key[i] & pmask) == prefix) atomicAdd(&Hw[(key[i] >> shift) & 255u], 1);
       __syncthreads();
-      // bin 255 - tid summed over the private copies, then a scan over bins.
+      // bin 255 - tid (threads below 256) summed over the private copies,
+      // then a scan over bins.
       int cnt = 0;
+      if (tid < 256) {
 #pragma unroll
-      for (int j = 0; j < WAVES * 8; ++j) cnt += H[j * 256 + (255 - tid)];
+        for (int j = 0; j < SWAVES * 4; ++j) cnt += H[j * 256 + (255 - tid)];
+      }
       int incl = wave_incl_scan(cnt);
       if (lane == 63) s.scan[wave] = incl;
       __syncthreads();
@@ -1213,23 +1234,23 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
   __syncthreads();
   int base = 0, n = 0;
 #pragma unroll
-  for (int w = 0; w < WAVES; ++w) {
+  for (int w = 0; w < SWAVES; ++w) {
     if (w < wave) base += s.wcount[w];
     n += s.wcount[w];
   }
   base += wincl - myc;
 #pragma unroll
   for (int i = 0; i < VPT; ++i)
-    if (keep[i]) ck[base++] = skey(xr[i], tid + i * NT);
+    if (keep[i]) ck[base++] = skey(xr[i], tid + i * SNT);
   int P = 1;
   while (P < n) P <<= 1;
   __syncthreads();
-  for (int i = n + tid; i < P; i += NT) ck[i] = 0ull;
+  for (int i = n + tid; i < P; i += SNT) ck[i] = 0ull;
   __syncthreads();
   // Bitonic sort of the keys in LDS, largest first.
   for (int k = 2; k <= P; k <<= 1)
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < P; i += NT) {
+      for (int i = tid; i < P; i += SNT) {
         const int l = i ^ j;
         if (l > i) {
           const unsigned long long ki = ck[i], kl = ck[l];
@@ -1255,7 +1276,7 @@ __device__ __forceinline__ void merge_mask(const float* lc, const float* lu, flo
   float cvv[VPT], uvv[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int v = min((int)threadIdx.x + i * NT, V - 1);
+    const int v = min((int)threadIdx.x + i * SNT, V - 1);
     cvv[i] = lc[v];
     uvv[i] = lu ? lu[v] : 0.f;
   }
@@ -1265,10 +1286,10 @@ __device__ __forceinline__ void merge_mask(const float* lc, const float* lu, flo
   const int lo_special = min(min(bos, pad), mask_eos ? min(eos, V) : V);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int v = threadIdx.x + i * NT;
+    const int v = threadIdx.x + i * SNT;
     float m = cvv[i];
     if (lu) m = __fadd_rn(uvv[i], __fmul_rn(s, __fsub_rn(m, uvv[i])));
-    if ((i + 1) * NT > lo_special)
+    if ((i + 1) * SNT > lo_special)
       if (v == bos || v == pad || (mask_eos && v == eos) || v >= V) m = -INFINITY;
     if (dbg && v < V) dbg[v] = m;
     xr[i] = divide ? m / temp : m;
@@ -1299,9 +1320,9 @@ struct SampleArgs {
 // the next frame starts from.  Every input that does not depend on the code
 // is loaded in the first round trip (this frame's draws and flags sit at
 // fixed addresses, so nothing waits on the frame counter).  VPT = logits per
-// thread, ceil(V / NT).
+// thread, ceil(V / SNT).
 template <typename TL, int VPT>
-__global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
+__global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   extern __shared__ unsigned char raw[];
   double* W = reinterpret_cast<double*>(raw);
   unsigned long long* ck = reinterpret_cast<unsigned long long*>(W + MAX_V);
@@ -1340,7 +1361,7 @@ __global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
 
   __syncthreads();
   const size_t row_stride = (size_t)a.V * a.d;
-  for (int dd = threadIdx.x; dd < a.d; dd += NT) {
+  for (int dd = threadIdx.x; dd < a.d; dd += SNT) {
     float e = 0.f;
     for (int j0 = 0; j0 < a.Q; j0 += 16) {
       float t[16];
@@ -1363,7 +1384,7 @@ __global__ __launch_bounds__(NT) void sample_step_kernel(SampleArgs a, int q) {
 
 // Standalone sampler (operator API): one utterance, parameters by value.
 template <int VPT>
-__global__ __launch_bounds__(NT) void sample_op_kernel(const float* logits, int rows, int V, float cfg, int q,
+__global__ __launch_bounds__(SNT) void sample_op_kernel(const float* logits, int rows, int V, float cfg, int q,
                                                        int mask_eos_q0, int bos, int eos, int pad, float temp,
                                                        int top_k, float top_p, double u, int64_t* code_out) {
   extern __shared__ unsigned char raw[];

@@ -116,21 +116,22 @@ static inline GemvArgs gemv_args(const void* w, int N, int K, const float* x, in
 }
 
 // Sampler launches pick the instantiation with the fewest logits per thread
-// that covers V: 1, 2, 4, 9 or 16 (V <= MAX_V).
+// that covers V: 1, 2, 3, 5 or 8 per thread of SNT (V <= MAX_V).
+static_assert(8 * SNT >= MAX_V, "sampler instantiations must cover MAX_V");
 template <typename F>
 static hipError_t with_vpt(int V, F&& f) {
-  const int need = (V + NT - 1) / NT;
+  const int need = (V + SNT - 1) / SNT;
   if (need <= 1) return f(std::integral_constant<int, 1>{});
   if (need <= 2) return f(std::integral_constant<int, 2>{});
-  if (need <= 4) return f(std::integral_constant<int, 4>{});
-  if (need <= 9) return f(std::integral_constant<int, 9>{});
-  return f(std::integral_constant<int, 16>{});
+  if (need <= 3) return f(std::integral_constant<int, 3>{});
+  if (need <= 5) return f(std::integral_constant<int, 5>{});
+  return f(std::integral_constant<int, 8>{});
 }
 
 template <typename TL>
 static hipError_t launch_sample_step(const SampleArgs& a, int q, int n_utts, hipStream_t st) {
   return with_vpt(a.V, [&](auto vpt) {
-    hipLaunchKernelGGL((sample_step_kernel<TL, decltype(vpt)::value>), dim3(n_utts), dim3(NT), SAMPLE_SMEM, st,
+    hipLaunchKernelGGL((sample_step_kernel<TL, decltype(vpt)::value>), dim3(n_utts), dim3(SNT), SAMPLE_SMEM, st,
                        a, q);
     return hipGetLastError();
   });
@@ -144,7 +145,7 @@ static inline hipError_t prepare_sampler() {
     if (e == hipSuccess)
       e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)SAMPLE_SMEM);
   };
-  for (int V : {NT, 2 * NT, 4 * NT, 9 * NT, 16 * NT})
+  for (int V : {SNT, 2 * SNT, 3 * SNT, 5 * SNT, 8 * SNT})
     with_vpt(V, [&](auto vpt) {
       constexpr int P = decltype(vpt)::value;
       set(reinterpret_cast<const void*>(sample_step_kernel<WF32, P>));

@@ -137,7 +137,7 @@ int sk_op_sample(void* stream, int32_t rows, int32_t V, const float* logits, flo
   SK_CHECK(q >= 0, SK_EINVAL, "q must be non-negative");
   SK_HIP(prepare_sampler());
   SK_HIP(with_vpt(V, [&](auto vpt) {
-    hipLaunchKernelGGL((sample_op_kernel<decltype(vpt)::value>), dim3(1), dim3(NT), SAMPLE_SMEM,
+    hipLaunchKernelGGL((sample_op_kernel<decltype(vpt)::value>), dim3(1), dim3(SNT), SAMPLE_SMEM,
                        (hipStream_t)stream, logits, rows, V, cfg_scale, q, mask_eos_q0, bos_id, eos_id, pad_id,
                        temperature, top_k, top_p, u, code_out);
     return hipGetLastError();

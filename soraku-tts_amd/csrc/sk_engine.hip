@@ -64,6 +64,7 @@ struct sk_engine {
   char *kc = nullptr, *vc = nullptr;   // KV caches, cfg.kv_dtype elements
   float *inv_freq = nullptr;
   float *part = nullptr, *dbg = nullptr, *embeds = nullptr;
+  float2* rope = nullptr;     // [rows][hd/2] (cos, sin) at each row's position
   int *kv_len = nullptr, *pos = nullptr, *active = nullptr, *plen = nullptr;
   int *fc = nullptr, *pf_t = nullptr, *flag_ring = nullptr, *flag_cur = nullptr;
   double *u_ring = nullptr, *u_cur = nullptr;
@@ -178,9 +179,9 @@ hipError_t enqueue_trunk(sk_engine* e) {
     at.kc = e->kc + (size_t)l * kv_layer_bytes(e);
     at.vc = e->vc + (size_t)l * kv_layer_bytes(e);
     at.qn_w = w.q_norm; at.kn_w = w.k_norm; at.eps = c.trunk_eps;
-    at.inv_freq = e->inv_freq;
+    at.rope = e->rope;
     at.part = e->part; at.max_chunks = e->max_chunks;
-    at.kv_len = e->kv_len; at.pos = e->pos; at.active = e->active;
+    at.kv_len = e->kv_len; at.active = e->active;
     at.out = e->attn; at.ldo = c.n_q_heads * hd;
     at.Hq = c.n_q_heads; at.Hkv = c.n_kv_heads; at.hd = hd; at.max_ctx = c.max_ctx;
     at.scale = 1.0f / sqrtf((float)hd);
@@ -259,7 +260,8 @@ hipError_t enqueue_frame(sk_engine* e) {
   if ((err = enqueue_trunk(e)) != hipSuccess) return err;
   hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x, e->final_norm,
                      c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->fc, e->u_ring,
-                     e->flag_ring, e->u_cur, e->flag_cur, c.n_utts * c.n_codebooks, c.max_frames);
+                     e->flag_ring, e->u_cur, e->flag_cur, c.n_utts * c.n_codebooks, c.max_frames,
+                     e->inv_freq, c.head_dim / 2, e->rope);
   return hipGetLastError();
 }
 
@@ -272,7 +274,8 @@ hipError_t enqueue_prefill_step(sk_engine* e) {
   if ((err = enqueue_trunk(e)) != hipSuccess) return err;
   hipLaunchKernelGGL(final_norm_kernel, dim3(e->rows), dim3(NT), 0, e->stream, e->x, e->final_norm,
                      c.trunk_eps, c.d_model, e->hidden, e->kv_len, e->pos, e->active, e->pf_t,
-                     (const double*)nullptr, (const int*)nullptr, (double*)nullptr, (int*)nullptr, 0, 0);
+                     (const double*)nullptr, (const int*)nullptr, (double*)nullptr, (int*)nullptr, 0, 0,
+                     e->inv_freq, c.head_dim / 2, e->rope);
   return hipGetLastError();
 }
 
@@ -360,6 +363,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   ALLOC(e->kc, (size_t)c.n_layers * kv_layer_bytes(e));
   ALLOC(e->vc, (size_t)c.n_layers * kv_layer_bytes(e));
   ALLOC(e->inv_freq, (size_t)c.head_dim / 2);
+  ALLOC(e->rope, R * (size_t)c.head_dim / 2);
   ALLOC(e->part, R * c.n_q_heads * e->max_chunks * (c.head_dim + 2));
   ALLOC(e->kv_len, R); ALLOC(e->pos, R); ALLOC(e->active, R); ALLOC(e->plen, R);
   ALLOC(e->fc, 1); ALLOC(e->pf_t, 1);
@@ -407,7 +411,7 @@ int sk_destroy(sk_engine* e) {
   if (e->stream) hipStreamSynchronize(e->stream);
   drop_graphs(e);
   void* bufs[] = {e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
-                  e->kc, e->vc, e->inv_freq, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
+                  e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->pf_t, e->flag_ring, e->u_ring,
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
   for (void* p : bufs)
@@ -527,6 +531,9 @@ int sk_prefill_run(sk_engine* e) {
   SK_HIP(hipMemcpyAsync(e->plen, e->len_host.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemcpyAsync(e->kv_len, zeros.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemcpyAsync(e->pos, zeros.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  hipLaunchKernelGGL(rope_rows_kernel, dim3(R), dim3(NT), 0, e->stream, e->pos, e->inv_freq,
+                     e->c.head_dim / 2, 0, e->rope);
+  SK_HIP(hipGetLastError());
   SK_HIP(hipMemsetAsync(e->pf_t, 0, sizeof(int), e->stream));
   SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
   SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
@@ -557,6 +564,10 @@ int sk_set_row_state(sk_engine* e, int32_t row, int32_t kv_len, int32_t position
   SK_HIP(hipMemcpy(e->pos + row, &position, sizeof(int), hipMemcpyHostToDevice));
   const int one = 1;
   SK_HIP(hipMemcpy(e->active + row, &one, sizeof(int), hipMemcpyHostToDevice));
+  hipLaunchKernelGGL(rope_rows_kernel, dim3(1), dim3(NT), 0, e->stream, e->pos, e->inv_freq,
+                     e->c.head_dim / 2, row, e->rope);
+  SK_HIP(hipGetLastError());
+  SK_HIP(hipStreamSynchronize(e->stream));
   e->kv_host[row] = kv_len;
   return SK_OK;
 }

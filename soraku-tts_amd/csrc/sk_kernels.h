@@ -488,16 +488,16 @@ __global__ __launch_bounds__(NT) void rmsnorm_rows_kernel(const float* x, const 
 // token per lane).  The chunk rows are read speculatively (the cache is
 // allocated to max_ctx, so they are in bounds); tokens at or past the row's
 // length are masked once kv_len arrives.  Queries and the new key get Qwen3's
-// per-head RMSNorm then rotate-half RoPE with angle = fp32(pos * inv_freq)
-// and cos/sin evaluated in double, rounded once.  The workgroup owning the new
+// per-head RMSNorm then rotate-half RoPE with the row's (cos, sin) table
+// (rope_cs, written when the position last moved).  The workgroup owning the new
 // token appends it to the cache.  Partial (max, sum, o) per chunk go to
 // scratch, merged by attention_combine_kernel.
 struct AttnArgs {
   const float* qkv; int ldqkv;           // [rows][(Hq + 2 Hkv) hd] raw projections
   void* kc; void* vc;                    // this layer: [rows][Hkv][max_ctx][hd], FP32 or BF16
   const float* qn_w; const float* kn_w; float eps;
-  const float* inv_freq;                 // [hd/2]
-  const int* kv_len; const int* pos; const int* active;
+  const float2* rope;                    // [rows][hd/2] (cos, sin) at the row's position
+  const int* kv_len; const int* active;
   float* part;                           // [rows][Hq][max_chunks][hd+2]
   float* out; int ldo;                   // [rows][Hq hd]
   int Hq, Hkv, hd, max_ctx, max_chunks;
@@ -576,13 +576,13 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   float* vs = sm + attn_smem_floats(G, hd) - (size_t)ATT_CHUNK * hd;  // [CHUNK][hd]
 
   const int T = a.kv_len[r];
-  const int p = a.pos[r];
   const int act = a.active[r];
   // Every load goes to registers first (one element per thread: G*hd <= NT
   // and hd <= NT), then the chunk's K/V rows; LDS is written only once all of
   // them are in flight, so no load waits behind another's round trip.
   const float* row = a.qkv + (size_t)r * a.ldqkv;
-  float q_r = 0.f, kn_r = 0.f, vn_r = 0.f, qw_r = 0.f, kw_r = 0.f, fq_r = 0.f;
+  float q_r = 0.f, kn_r = 0.f, vn_r = 0.f, qw_r = 0.f, kw_r = 0.f;
+  float2 cs_r = make_float2(1.f, 0.f);
   if (tid < G * hd) q_r = row[(size_t)h * G * hd + tid];
   if (tid < hd) {
     kn_r = row[(size_t)a.Hq * hd + (size_t)h * hd + tid];
@@ -590,7 +590,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
     qw_r = a.qn_w[tid];
     kw_r = a.kn_w[tid];
   }
-  if (tid < half) fq_r = a.inv_freq[tid];
+  if (tid < half) cs_r = a.rope[(size_t)r * half + tid];
 
   const int LPT = hd / ATT_DPL;
   const int TPP = NT / LPT;              // tokens per pass
@@ -635,11 +635,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   const int n_t = min(ATT_CHUNK, ctx - t_begin);
   if (tid < G * hd) qs[tid] = q_r;
   if (tid < hd) { knew[tid] = kn_r; vnew[tid] = vn_r; qw[tid] = qw_r; kw[tid] = kw_r; }
-  if (tid < half) {
-    const float ang = (float)p * fq_r;
-    fcs[tid] = (float)cos((double)ang);
-    fsn[tid] = (float)sin((double)ang);
-  }
+  if (tid < half) { fcs[tid] = cs_r.x; fsn[tid] = cs_r.y; }
   __syncthreads();
   // Per-head RMSNorm over hd, then rotate-half RoPE; one wave per head.
   const int nheads = G + (last ? 1 : 0);
@@ -1404,6 +1400,21 @@ __global__ __launch_bounds__(SNT) void sample_op_kernel(const float* logits, int
 constexpr size_t SAMPLE_SMEM = (size_t)MAX_V * sizeof(double) + (size_t)(MAX_V + FILTER_MAX) * 8;
 
 // ------------------------------------------------------------ small kernels
+// RoPE (cos, sin) of position p for frequency fq: angle = fp32(p * fq), cos
+// and sin evaluated in double and rounded once (modeling_qwen3.py:116-122).
+__device__ __forceinline__ float2 rope_cs(int p, float fq) {
+  const float ang = (float)p * fq;
+  return make_float2((float)cos((double)ang), (float)sin((double)ang));
+}
+
+// (cos, sin) table of rows row0 + blockIdx.x at their current positions.
+__global__ __launch_bounds__(NT) void rope_rows_kernel(const int* pos, const float* inv_freq, int half, int row0,
+                                                       float2* rope) {
+  const int b = row0 + blockIdx.x;
+  const int p = pos[b];
+  for (int t = threadIdx.x; t < half; t += NT) rope[(size_t)b * half + t] = rope_cs(p, inv_freq[t]);
+}
+
 // Final trunk norm + per-row step bookkeeping.  Decode (ring != null): every
 // row advances, the frame counter moves on and the next frame's draws and
 // flags are copied from the ring to the fixed current-frame slots.  Prefill
@@ -1413,9 +1424,11 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
                                                         const int* active, int* counter,
                                                         const double* u_ring, const int* flag_ring,
                                                         double* u_cur, int* flag_cur, int nq,
-                                                        int max_frames) {
+                                                        int max_frames, const float* inv_freq, int half,
+                                                        float2* rope) {
   __shared__ float red[WAVES];
   const int b = blockIdx.x;
+  const int p0 = pos[b];                 // read by every thread before the barrier in block_sum
   if (active[b]) {
     const float* xr = x + (size_t)b * D;
     constexpr int PER = 16;              // D <= 4096 in registers, all loads issued at once
@@ -1443,7 +1456,8 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
       const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
       for (int k = threadIdx.x; k < D; k += NT) hidden[(size_t)b * D + k] = w[k] * (xr[k] * inv);
     }
-    if (threadIdx.x == 0) { kv_len[b] += 1; pos[b] += 1; }
+    if (threadIdx.x == 0) { kv_len[b] += 1; pos[b] = p0 + 1; }
+    for (int t = threadIdx.x; t < half; t += NT) rope[(size_t)b * half + t] = rope_cs(p0 + 1, inv_freq[t]);
   }
   if (b == 0) {
     const int next = *counter + 1;

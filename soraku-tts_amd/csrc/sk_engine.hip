@@ -24,6 +24,7 @@
 #include "sk_error.h"
 #include "sk_kernels.h"
 #include "sk_launch.h"
+#include "sk_prefill.h"
 #include "soraku_mi355x.h"
 
 using namespace sk;
@@ -66,7 +67,7 @@ struct sk_engine {
   float *part = nullptr, *dbg = nullptr, *embeds = nullptr;
   float2* rope = nullptr;     // [rows][hd/2] (cos, sin) at each row's position
   int *kv_len = nullptr, *pos = nullptr, *active = nullptr, *plen = nullptr;
-  int *fc = nullptr, *pf_t = nullptr, *flag_ring = nullptr, *flag_cur = nullptr;
+  int *fc = nullptr, *flag_ring = nullptr, *flag_cur = nullptr;
   double *u_ring = nullptr, *u_cur = nullptr;
   int64_t *forced_ring = nullptr, *codes_ring = nullptr, *stage_ids = nullptr, *stage_codes = nullptr;
   int* codes_cur = nullptr;
@@ -79,8 +80,14 @@ struct sk_engine {
   std::vector<char> staged;
   SkParams p_host{};
 
-  hipGraph_t graph = nullptr, pf_graph = nullptr;
-  hipGraphExec_t exec = nullptr, pf_exec = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+
+  // batched prefill scratch, sized for the largest packed prefix so far
+  int pf_cap = 0;
+  float *pX = nullptr, *pXn = nullptr, *pQKV = nullptr, *pQ = nullptr, *pATT = nullptr, *pACT = nullptr;
+  int *p_tok_row = nullptr, *p_tok_pos = nullptr, *p_row_start = nullptr;
+  float2* p_rope = nullptr;   // [max_ctx][hd/2] (cos, sin) by position
 };
 
 namespace {
@@ -95,21 +102,20 @@ size_t kv_layer_bytes(const sk_engine* e) {
 void drop_graphs(sk_engine* e) {
   if (e->exec) hipGraphExecDestroy(e->exec);
   if (e->graph) hipGraphDestroy(e->graph);
-  if (e->pf_exec) hipGraphExecDestroy(e->pf_exec);
-  if (e->pf_graph) hipGraphDestroy(e->pf_graph);
-  e->exec = nullptr; e->graph = nullptr; e->pf_exec = nullptr; e->pf_graph = nullptr;
+  e->exec = nullptr; e->graph = nullptr;
 }
 
 int validate_config(const sk_config* c) {
   SK_CHECK(c != nullptr, SK_EINVAL, "config is NULL");
-  SK_CHECK(c->d_model > 0 && c->d_model % 8 == 0, SK_EINVAL, "d_model must be a positive multiple of 8");
+  SK_CHECK(c->d_model > 0 && c->d_model % 16 == 0, SK_EINVAL, "d_model must be a positive multiple of 16");
   SK_CHECK(c->n_layers > 0, SK_EINVAL, "n_layers must be positive");
   SK_CHECK(c->n_q_heads > 0 && c->n_kv_heads > 0 && c->n_q_heads % c->n_kv_heads == 0, SK_EINVAL,
            "n_q_heads must be a positive multiple of n_kv_heads");
   const int hd = c->head_dim;
-  SK_CHECK(hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256,
-           SK_EINVAL, "head_dim must be a power of two in [16, 256]");
-  SK_CHECK(c->trunk_inter > 0 && c->trunk_inter % 8 == 0, SK_EINVAL, "trunk_inter must be a positive multiple of 8");
+  SK_CHECK(hd == 16 || hd == 32 || hd == 64 || hd == 128,
+           SK_EINVAL, "head_dim must be a power of two in [16, 128]");
+  SK_CHECK(32 % (c->n_q_heads / c->n_kv_heads) == 0, SK_EINVAL, "n_q_heads / n_kv_heads must divide 32");
+  SK_CHECK(c->trunk_inter > 0 && c->trunk_inter % 16 == 0, SK_EINVAL, "trunk_inter must be a positive multiple of 16");
   SK_CHECK(c->depth_inner > 0 && c->depth_inner % 8 == 0, SK_EINVAL, "depth_inner must be a positive multiple of 8");
   SK_CHECK(c->n_codebooks > 0 && c->n_codebooks <= 64, SK_EINVAL, "n_codebooks must be in [1, 64]");
   SK_CHECK(c->audio_vocab > 3 && c->audio_vocab <= MAX_V, SK_EINVAL, "audio_vocab must be in [4, %d]", MAX_V);
@@ -265,17 +271,107 @@ hipError_t enqueue_frame(sk_engine* e) {
   return hipGetLastError();
 }
 
-hipError_t enqueue_prefill_step(sk_engine* e) {
+// ---- batched prefill -------------------------------------------------------
+
+template <int EPI>
+hipError_t launch_gemm(int wdtype, const GemmArgs& g, hipStream_t st) {
+  const dim3 grid((g.N + GBN - 1) / GBN, (g.M + GBM - 1) / GBM);
+  if (wdtype == SK_BF16) hipLaunchKernelGGL((gemm_nt_kernel<EPI, WBF16>), grid, dim3(256), 0, st, g);
+  else hipLaunchKernelGGL((gemm_nt_kernel<EPI, WF32>), grid, dim3(256), 0, st, g);
+  return hipGetLastError();
+}
+
+GemmArgs gemm_args(const float* A, int lda, const void* B, int M, int N, int K, float* out, int ldo) {
+  GemmArgs g{};
+  g.A = A; g.lda = lda;
+  g.B[0] = B; g.B[1] = nullptr; g.B[2] = nullptr;
+  g.seg_rows[0] = N; g.seg_rows[1] = 0; g.seg_rows[2] = 0;
+  g.out = out; g.ldo = ldo;
+  g.M = M; g.N = N; g.K = K;
+  return g;
+}
+
+hipError_t ensure_prefill_bufs(sk_engine* e, int M) {
+  if (M <= e->pf_cap) return hipSuccess;
+  void* old[] = {e->pX, e->pXn, e->pQKV, e->pQ, e->pATT, e->pACT, e->p_tok_row, e->p_tok_pos};
+  for (void* p : old)
+    if (p) hipFree(p);
+  e->pX = e->pXn = e->pQKV = e->pQ = e->pATT = e->pACT = nullptr;
+  e->p_tok_row = e->p_tok_pos = nullptr;
+  e->pf_cap = 0;
   const sk_config& c = e->c;
-  hipLaunchKernelGGL(prefill_load_kernel, dim3(e->rows), dim3(NT), 0, e->stream, e->embeds,
-                     c.max_ctx, e->plen, e->pf_t, c.d_model, e->x, e->active);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  if ((err = enqueue_trunk(e)) != hipSuccess) return err;
-  hipLaunchKernelGGL(final_norm_kernel, dim3(e->rows), dim3(NT), 0, e->stream, e->x, e->final_norm,
-                     c.trunk_eps, c.d_model, e->hidden, e->kv_len, e->pos, e->active, e->pf_t,
-                     (const double*)nullptr, (const int*)nullptr, (double*)nullptr, (int*)nullptr, 0, 0,
-                     e->inv_freq, c.head_dim / 2, e->rope);
+  const size_t m = (size_t)M, hq = (size_t)c.n_q_heads * c.head_dim;
+  hipError_t err = hipSuccess;
+  if (err == hipSuccess) err = dalloc(&e->pX, m * c.d_model);
+  if (err == hipSuccess) err = dalloc(&e->pXn, m * c.d_model);
+  if (err == hipSuccess) err = dalloc(&e->pQKV, m * e->nqkv);
+  if (err == hipSuccess) err = dalloc(&e->pQ, m * hq);
+  if (err == hipSuccess) err = dalloc(&e->pATT, m * hq);
+  if (err == hipSuccess) err = dalloc(&e->pACT, m * c.trunk_inter);
+  if (err == hipSuccess) err = dalloc(&e->p_tok_row, m);
+  if (err == hipSuccess) err = dalloc(&e->p_tok_pos, m);
+  if (err == hipSuccess) e->pf_cap = M;
+  return err;
+}
+
+// All staged prefix tokens through the trunk at once (M = total tokens).
+hipError_t enqueue_batched_prefill(sk_engine* e, int M, int max_len) {
+  const sk_config& c = e->c;
+  const int d = c.d_model, hd = c.head_dim, wt = c.weight_dtype;
+  const int hq = c.n_q_heads * hd, I = c.trunk_inter;
+  const bool bf = c.kv_dtype == SK_BF16;
+  hipStream_t st = e->stream;
+  hipError_t err;
+  hipLaunchKernelGGL(pf_rope_table_kernel, dim3(max_len), dim3(NT), 0, st, e->inv_freq, hd / 2, e->p_rope);
+  hipLaunchKernelGGL(pf_gather_kernel, dim3(M), dim3(NT), 0, st, e->embeds, c.max_ctx, e->p_tok_row,
+                     e->p_tok_pos, d, e->pX);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  const size_t asmem = pf_attn_smem_floats(hd) * sizeof(float);
+  const int G = c.n_q_heads / c.n_kv_heads, QB = PF_NQ / G;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerW& w = e->L[l];
+    char* kc = e->kc + (size_t)l * kv_layer_bytes(e);
+    char* vc = e->vc + (size_t)l * kv_layer_bytes(e);
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(NT), 0, st, e->pX, (const float*)nullptr, w.in_norm,
+                       c.trunk_eps, d, e->pXn, (const int*)nullptr);
+    GemmArgs g = gemm_args(e->pXn, d, w.q, M, e->nqkv, d, e->pQKV, e->nqkv);
+    g.B[1] = w.k; g.B[2] = w.v;
+    g.seg_rows[0] = hq; g.seg_rows[1] = c.n_kv_heads * hd; g.seg_rows[2] = c.n_kv_heads * hd;
+    if ((err = launch_gemm<GEPI_STORE>(wt, g, st)) != hipSuccess) return err;
+    if (bf)
+      hipLaunchKernelGGL(pf_qkv_kernel<uint16_t>, dim3(M), dim3(NT), 0, st, e->pQKV, e->nqkv, e->p_tok_row,
+                         e->p_tok_pos, w.q_norm, w.k_norm, c.trunk_eps, e->p_rope, c.n_q_heads, c.n_kv_heads, hd,
+                         c.max_ctx, e->pQ, reinterpret_cast<uint16_t*>(kc), reinterpret_cast<uint16_t*>(vc));
+    else
+      hipLaunchKernelGGL(pf_qkv_kernel<float>, dim3(M), dim3(NT), 0, st, e->pQKV, e->nqkv, e->p_tok_row,
+                         e->p_tok_pos, w.q_norm, w.k_norm, c.trunk_eps, e->p_rope, c.n_q_heads, c.n_kv_heads, hd,
+                         c.max_ctx, e->pQ, reinterpret_cast<float*>(kc), reinterpret_cast<float*>(vc));
+    const dim3 agrid((max_len + QB - 1) / QB, c.n_kv_heads, e->rows);
+    const float scale = 1.0f / sqrtf((float)hd);
+    if (bf)
+      hipLaunchKernelGGL(pf_attention_kernel<uint16_t>, agrid, dim3(NT), asmem, st, e->pQ,
+                         reinterpret_cast<const uint16_t*>(kc), reinterpret_cast<const uint16_t*>(vc),
+                         e->p_row_start, e->plen, c.n_q_heads, c.n_kv_heads, hd, c.max_ctx, scale, e->pATT, hq);
+    else
+      hipLaunchKernelGGL(pf_attention_kernel<float>, agrid, dim3(NT), asmem, st, e->pQ,
+                         reinterpret_cast<const float*>(kc), reinterpret_cast<const float*>(vc), e->p_row_start,
+                         e->plen, c.n_q_heads, c.n_kv_heads, hd, c.max_ctx, scale, e->pATT, hq);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    g = gemm_args(e->pATT, hq, w.o, M, d, hq, e->pX, d);
+    g.res = e->pX; g.ldr = d;
+    if ((err = launch_gemm<GEPI_RESID>(wt, g, st)) != hipSuccess) return err;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(NT), 0, st, e->pX, (const float*)nullptr, w.post_norm,
+                       c.trunk_eps, d, e->pXn, (const int*)nullptr);
+    g = gemm_args(e->pXn, d, w.gate, M, I, d, e->pACT, I);
+    g.B2 = w.up;
+    if ((err = launch_gemm<GEPI_SWIGLU>(wt, g, st)) != hipSuccess) return err;
+    g = gemm_args(e->pACT, I, w.down, M, d, I, e->pX, d);
+    g.res = e->pX; g.ldr = d;
+    if ((err = launch_gemm<GEPI_RESID>(wt, g, st)) != hipSuccess) return err;
+  }
+  hipLaunchKernelGGL(pf_finish_kernel, dim3(e->rows), dim3(NT), 0, st, e->pX, e->p_row_start, e->plen,
+                     e->final_norm, c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->inv_freq, hd / 2,
+                     e->rope);
   return hipGetLastError();
 }
 
@@ -366,7 +462,9 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   ALLOC(e->rope, R * (size_t)c.head_dim / 2);
   ALLOC(e->part, R * c.n_q_heads * e->max_chunks * (c.head_dim + 2));
   ALLOC(e->kv_len, R); ALLOC(e->pos, R); ALLOC(e->active, R); ALLOC(e->plen, R);
-  ALLOC(e->fc, 1); ALLOC(e->pf_t, 1);
+  ALLOC(e->fc, 1);
+  ALLOC(e->p_rope, (size_t)c.max_ctx * (c.head_dim / 2));
+  ALLOC(e->p_row_start, R);
   ALLOC(e->u_ring, (size_t)c.max_frames * c.n_utts * Q);
   ALLOC(e->flag_ring, (size_t)c.max_frames * 2);
   ALLOC(e->u_cur, (size_t)c.n_utts * Q);
@@ -412,7 +510,9 @@ int sk_destroy(sk_engine* e) {
   drop_graphs(e);
   void* bufs[] = {e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
                   e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
-                  e->kv_len, e->pos, e->active, e->plen, e->fc, e->pf_t, e->flag_ring, e->u_ring,
+                  e->kv_len, e->pos, e->active, e->plen, e->fc, e->flag_ring, e->u_ring,
+                  e->pX, e->pXn, e->pQKV, e->pQ, e->pATT, e->pACT, e->p_tok_row, e->p_tok_pos,
+                  e->p_row_start, e->p_rope,
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
   for (void* p : bufs)
     if (p) hipFree(p);
@@ -527,27 +627,25 @@ int sk_prefill_run(sk_engine* e) {
   int rc = check_decode_weights(e);
   if (rc != SK_OK) return rc;
   const int R = e->rows;
-  std::vector<int> zeros(R, 0);
+  // Pack the rows' prefix tokens row after row.
+  std::vector<int> row_start(R), tok_row, tok_pos;
+  int M = 0, max_len = 0;
+  for (int r = 0; r < R; ++r) {
+    row_start[r] = M;
+    for (int p = 0; p < e->len_host[r]; ++p) { tok_row.push_back(r); tok_pos.push_back(p); }
+    M += e->len_host[r];
+    max_len = e->len_host[r] > max_len ? e->len_host[r] : max_len;
+  }
+  const hipError_t ae = ensure_prefill_bufs(e, M);
+  SK_CHECK(ae == hipSuccess, SK_EHIP, "prefill buffers for %d tokens: %s", M, hipGetErrorString(ae));
   SK_HIP(hipMemcpyAsync(e->plen, e->len_host.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  SK_HIP(hipMemcpyAsync(e->kv_len, zeros.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  SK_HIP(hipMemcpyAsync(e->pos, zeros.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  hipLaunchKernelGGL(rope_rows_kernel, dim3(R), dim3(NT), 0, e->stream, e->pos, e->inv_freq,
-                     e->c.head_dim / 2, 0, e->rope);
-  SK_HIP(hipGetLastError());
-  SK_HIP(hipMemsetAsync(e->pf_t, 0, sizeof(int), e->stream));
+  SK_HIP(hipMemcpyAsync(e->p_row_start, row_start.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->p_tok_row, tok_row.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->p_tok_pos, tok_pos.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
   SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
   SK_HIP(hipMemsetAsync(e->prefix2, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
-  SK_HIP(hipStreamSynchronize(e->stream));
-  if (!e->pf_exec) {
-    rc = capture(e, enqueue_prefill_step, &e->pf_graph, &e->pf_exec);
-    if (rc != SK_OK) return rc;
-  }
-  int longest = 0;
-  for (int r = 0; r < R; ++r) longest = e->len_host[r] > longest ? e->len_host[r] : longest;
-  for (int t = 0; t < longest; ++t) SK_HIP(hipGraphLaunch(e->pf_exec, e->stream));
-  std::vector<int> ones(R, 1);
-  SK_HIP(hipMemcpyAsync(e->active, ones.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(enqueue_batched_prefill(e, M, max_len));
   SK_HIP(hipStreamSynchronize(e->stream));
   for (int r = 0; r < R; ++r) { e->kv_host[r] = e->len_host[r]; e->staged[r] = 0; }
   e->fc_host = 0;

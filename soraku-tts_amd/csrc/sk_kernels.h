@@ -1415,10 +1415,10 @@ __global__ __launch_bounds__(NT) void rope_rows_kernel(const int* pos, const flo
   for (int t = threadIdx.x; t < half; t += NT) rope[(size_t)b * half + t] = rope_cs(p, inv_freq[t]);
 }
 
-// Final trunk norm + per-row step bookkeeping.  Decode (ring != null): every
-// row advances, the frame counter moves on and the next frame's draws and
-// flags are copied from the ring to the fixed current-frame slots.  Prefill
-// (ring == null): active rows only, the prefill step moves on.
+// Final trunk norm + per-row step bookkeeping after a decode trunk step: every
+// active row advances its length and position (and the RoPE table of the new
+// position), the frame counter moves on and the next frame's draws and flags
+// are copied from the ring to the fixed current-frame slots.
 __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const float* w, float eps,
                                                         int D, float* hidden, int* kv_len, int* pos,
                                                         const int* active, int* counter,
@@ -1468,18 +1468,6 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
       if (threadIdx.x < 2) flag_cur[threadIdx.x] = flag_ring[2 * next + threadIdx.x];
     }
   }
-}
-
-// Prefill token t = *step: row b takes embeds[b][t] if t < len[b].
-__global__ __launch_bounds__(NT) void prefill_load_kernel(const float* embeds, int max_len,
-                                                          const int* len, const int* step, int D,
-                                                          float* x, int* active) {
-  const int b = blockIdx.x;
-  const int t = *step;
-  const bool on = t < len[b];
-  for (int k = threadIdx.x; k < D; k += NT)
-    x[(size_t)b * D + k] = on ? embeds[((size_t)b * max_len + t) * D + k] : 0.f;
-  if (threadIdx.x == 0) active[b] = on ? 1 : 0;
 }
 
 // Prefix embeddings of one row: text rows (language rows replaced,

@@ -107,7 +107,7 @@ void drop_graphs(sk_engine* e) {
 
 int validate_config(const sk_config* c) {
   SK_CHECK(c != nullptr, SK_EINVAL, "config is NULL");
-  SK_CHECK(c->d_model > 0 && c->d_model % 16 == 0, SK_EINVAL, "d_model must be a positive multiple of 16");
+  SK_CHECK(c->d_model > 0 && c->d_model % 32 == 0, SK_EINVAL, "d_model must be a positive multiple of 32");
   SK_CHECK(c->n_layers > 0, SK_EINVAL, "n_layers must be positive");
   SK_CHECK(c->n_q_heads > 0 && c->n_kv_heads > 0 && c->n_q_heads % c->n_kv_heads == 0, SK_EINVAL,
            "n_q_heads must be a positive multiple of n_kv_heads");
@@ -115,7 +115,8 @@ int validate_config(const sk_config* c) {
   SK_CHECK(hd == 16 || hd == 32 || hd == 64 || hd == 128,
            SK_EINVAL, "head_dim must be a power of two in [16, 128]");
   SK_CHECK(32 % (c->n_q_heads / c->n_kv_heads) == 0, SK_EINVAL, "n_q_heads / n_kv_heads must divide 32");
-  SK_CHECK(c->trunk_inter > 0 && c->trunk_inter % 16 == 0, SK_EINVAL, "trunk_inter must be a positive multiple of 16");
+  SK_CHECK(c->trunk_inter > 0 && c->trunk_inter % 32 == 0, SK_EINVAL, "trunk_inter must be a positive multiple of 32");
+  SK_CHECK(c->n_q_heads * hd % 32 == 0, SK_EINVAL, "n_q_heads * head_dim must be a multiple of 32");
   SK_CHECK(c->depth_inner > 0 && c->depth_inner % 8 == 0, SK_EINVAL, "depth_inner must be a positive multiple of 8");
   SK_CHECK(c->n_codebooks > 0 && c->n_codebooks <= 64, SK_EINVAL, "n_codebooks must be in [1, 64]");
   SK_CHECK(c->audio_vocab > 3 && c->audio_vocab <= MAX_V, SK_EINVAL, "audio_vocab must be in [4, %d]", MAX_V);
@@ -273,11 +274,19 @@ hipError_t enqueue_frame(sk_engine* e) {
 
 // ---- batched prefill -------------------------------------------------------
 
+// 64-row tiles unless they leave more than half the CUs idle, then 32-row tiles.
 template <int EPI>
 hipError_t launch_gemm(int wdtype, const GemmArgs& g, hipStream_t st) {
-  const dim3 grid((g.N + GBN - 1) / GBN, (g.M + GBM - 1) / GBM);
-  if (wdtype == SK_BF16) hipLaunchKernelGGL((gemm_nt_kernel<EPI, WBF16>), grid, dim3(256), 0, st, g);
-  else hipLaunchKernelGGL((gemm_nt_kernel<EPI, WF32>), grid, dim3(256), 0, st, g);
+  const int nt = (g.N + GBN - 1) / GBN;
+  const bool small = nt * ((g.M + 63) / 64) < 128;
+  const dim3 grid(nt, small ? (g.M + 31) / 32 : (g.M + 63) / 64);
+  if (wdtype == SK_BF16) {
+    if (small) hipLaunchKernelGGL((gemm_nt_kernel<EPI, WBF16, 32>), grid, dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((gemm_nt_kernel<EPI, WBF16, 64>), grid, dim3(256), 0, st, g);
+  } else {
+    if (small) hipLaunchKernelGGL((gemm_nt_kernel<EPI, WF32, 32>), grid, dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((gemm_nt_kernel<EPI, WF32, 64>), grid, dim3(256), 0, st, g);
+  }
   return hipGetLastError();
 }
 

@@ -17,12 +17,14 @@ namespace sk {
 
 // ------------------------------------------------------------ GEMM
 // C[M][N] = A[M][K] . B[N][K]^T on the FP32 matrix cores
-// (v_mfma_f32_16x16x4f32), 64 x 64 tiles, K in steps of 16 through LDS.  B
-// (weights, FP32 or BF16 widened on load) may be split into up to three row
-// segments (q / k / v projections).  Epilogues: store, residual add
-// (out = res + C, res may alias out), SwiGLU (out = silu(A Bg^T) * (A Bu^T),
-// B2 = up weights).  M, N arbitrary (rows past the end are clamped on load and
-// not stored); K a multiple of 16.
+// (v_mfma_f32_16x16x4f32).  Workgroup tile BM x 64 (BM = 64, or 32 when
+// 64-row tiles would leave CUs idle), K in steps of 32 through LDS; the next
+// step's A / B tiles are loaded into registers while the current one is
+// multiplied.  B (weights, FP32 or BF16 widened on load) may be split into up
+// to three row segments (q / k / v projections).  Epilogues: store, residual
+// add (out = res + C, res may alias out), SwiGLU (out = silu(A Bg^T) *
+// (A Bu^T), B2 = up weights).  M, N arbitrary (rows past the end are clamped
+// on load and not stored); K a multiple of 32.
 enum { GEPI_STORE = 0, GEPI_RESID = 1, GEPI_SWIGLU = 2 };
 
 struct GemmArgs {
@@ -34,8 +36,7 @@ struct GemmArgs {
   int M, N, K;
 };
 
-constexpr int GBM = 64, GBN = 64, GBK = 16;
-constexpr int GLD = GBM + 16;   // LDS row stride (floats): lanes 16 apart in k land 16 banks apart
+constexpr int GBN = 64, GBK = 32;
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
@@ -50,66 +51,94 @@ __device__ __forceinline__ float4 load_w4(const void* base, size_t off) {
   }
 }
 
-template <int EPI, typename WL>
+template <int EPI, typename WL, int BM>
 __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmArgs a) {
   constexpr int NB = (EPI == GEPI_SWIGLU) ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) float As[GBK][GLD];
-  __shared__ __attribute__((aligned(16))) float Bs[NB][GBK][GLD];
+  // Odd k-row strides: the loader's 8 k groups x 4 rows per 32 lanes store to
+  // 32 distinct banks, and an MFMA fragment read (16 rows x 2 k per 32 lanes)
+  // shifts 17 banks per k.
+  constexpr int LDA = BM + 17, LDB = GBN + 17;
+  constexpr int AL = BM * GBK / 4 / 256;         // float4 of A per thread per step (1 or 2)
+  constexpr int BL = GBN * GBK / 4 / 256;        // float4 of B per thread per step (2)
+  constexpr int TM = BM / 32;                    // 16-row MFMA tiles per wave (wave tile (BM/2) x 32)
+  __shared__ __attribute__((aligned(16))) float As[GBK][LDA];
+  __shared__ __attribute__((aligned(16))) float Bs[NB][GBK][LDB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
-  // loader: thread -> (tile row lr, k offset lk)
-  const int lr = tid >> 2, lk = (tid & 3) * 4;
-  const int am = min(m0 + lr, a.M - 1);
-  const float* arow = a.A + (size_t)am * a.lda + lk;
-  const int bn = min(n0 + lr, a.N - 1);
-  const void* bbase;
-  int brow;
-  if (bn < a.seg_rows[0]) { bbase = a.B[0]; brow = bn; }
-  else if (bn < a.seg_rows[0] + a.seg_rows[1]) { bbase = a.B[1]; brow = bn - a.seg_rows[0]; }
-  else { bbase = a.B[2]; brow = bn - a.seg_rows[0] - a.seg_rows[1]; }
-  const size_t boff = (size_t)brow * a.K + lk;
-  const size_t b2off = (size_t)bn * a.K + lk;
-  // wave tile: 32 x 32 at (wm, wn), 2 x 2 MFMA tiles of 16 x 16
-  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
-  v4f acc[NB][2][2];
+  const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * BM;
+  // loader: float4 i of a thread covers tile row (tid >> 3) + 32 i, k offset (tid & 7) * 4
+  const int lr = tid >> 3, lk = (tid & 7) * 4;
+  const float* arow[AL];
+#pragma unroll
+  for (int i = 0; i < AL; ++i) arow[i] = a.A + (size_t)min(m0 + lr + 32 * i, a.M - 1) * a.lda + lk;
+  const void* bbase[BL];
+  size_t boff[BL], b2off[BL];
+#pragma unroll
+  for (int i = 0; i < BL; ++i) {
+    const int bn = min(n0 + lr + 32 * i, a.N - 1);
+    int brow;
+    if (bn < a.seg_rows[0]) { bbase[i] = a.B[0]; brow = bn; }
+    else if (bn < a.seg_rows[0] + a.seg_rows[1]) { bbase[i] = a.B[1]; brow = bn - a.seg_rows[0]; }
+    else { bbase[i] = a.B[2]; brow = bn - a.seg_rows[0] - a.seg_rows[1]; }
+    boff[i] = (size_t)brow * a.K + lk;
+    b2off[i] = (size_t)bn * a.K + lk;
+  }
+  float4 ra[AL], rb[BL], rb2[BL];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < AL; ++i) ra[i] = *reinterpret_cast<const float4*>(arow[i] + k0);
+#pragma unroll
+    for (int i = 0; i < BL; ++i) {
+      rb[i] = load_w4<WL>(bbase[i], boff[i] + k0);
+      if constexpr (NB == 2) rb2[i] = load_w4<WL>(a.B2, b2off[i] + k0);
+    }
+  };
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;
+  v4f acc[NB][TM][2];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[b][i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
+  fetch(0);
   for (int k0 = 0; k0 < a.K; k0 += GBK) {
-    const float4 av = *reinterpret_cast<const float4*>(arow + k0);
-    const float4 bv = load_w4<WL>(bbase, boff + k0);
-    float4 bv2 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (NB == 2) bv2 = load_w4<WL>(a.B2, b2off + k0);
-    __syncthreads();   // previous step's reads are done
-    As[lk + 0][lr] = av.x; As[lk + 1][lr] = av.y; As[lk + 2][lr] = av.z; As[lk + 3][lr] = av.w;
-    Bs[0][lk + 0][lr] = bv.x; Bs[0][lk + 1][lr] = bv.y; Bs[0][lk + 2][lr] = bv.z; Bs[0][lk + 3][lr] = bv.w;
-    if constexpr (NB == 2) {
-      Bs[1][lk + 0][lr] = bv2.x; Bs[1][lk + 1][lr] = bv2.y; Bs[1][lk + 2][lr] = bv2.z; Bs[1][lk + 3][lr] = bv2.w;
+    __syncthreads();   // the previous step's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < AL; ++i) {
+      const int rr = lr + 32 * i;
+      As[lk + 0][rr] = ra[i].x; As[lk + 1][rr] = ra[i].y; As[lk + 2][rr] = ra[i].z; As[lk + 3][rr] = ra[i].w;
+    }
+#pragma unroll
+    for (int i = 0; i < BL; ++i) {
+      const int rr = lr + 32 * i;
+      Bs[0][lk + 0][rr] = rb[i].x; Bs[0][lk + 1][rr] = rb[i].y; Bs[0][lk + 2][rr] = rb[i].z; Bs[0][lk + 3][rr] = rb[i].w;
+      if constexpr (NB == 2) {
+        Bs[1][lk + 0][rr] = rb2[i].x; Bs[1][lk + 1][rr] = rb2[i].y; Bs[1][lk + 2][rr] = rb2[i].z;
+        Bs[1][lk + 3][rr] = rb2[i].w;
+      }
     }
     __syncthreads();
+    if (k0 + GBK < a.K) fetch(k0 + GBK);   // in flight while this step multiplies
 #pragma unroll
     for (int ks = 0; ks < GBK; ks += 4) {
       const int kk = ks + (lane >> 4), ii = lane & 15;
-      float af[2];
+      float af[TM];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = As[kk][wm + i * 16 + ii];
+      for (int i = 0; i < TM; ++i) af[i] = As[kk][wm + i * 16 + ii];
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const float bf = Bs[b][kk][wn + j * 16 + ii];
 #pragma unroll
-          for (int i = 0; i < 2; ++i) acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf, acc[b][i][j], 0, 0, 0);
+          for (int i = 0; i < TM; ++i) acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf, acc[b][i][j], 0, 0, 0);
         }
     }
   }
   // lane holds C[row = 4 (lane / 16) + v][col = lane % 16] of each 16 x 16 tile
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int n = n0 + wn + j * 16 + (lane & 15);
@@ -197,12 +226,30 @@ __global__ __launch_bounds__(NT) void pf_qkv_kernel(const float* qkv, int ldqkv,
 // vectors: the G heads of kv head h for QB = 32 / G consecutive positions of
 // the row, and walks the row's keys 0 .. (last query position) in chunks of
 // 32 with an online softmax (scale hd^-1/2, keys after the query masked).
-// K / V come from the cache just written (BF16 widened), so attention sees
-// exactly what decode steps will see.
+// Per chunk: S = Q K^T on the matrix cores (one 16 x 16 tile per wave, Q
+// fragments kept in registers), softmax over each query's 32 scores by 8
+// threads (DPP all-reduce), O += P V on the matrix cores.  K / V come from
+// the cache just written (BF16 widened), so attention sees exactly what
+// decode steps will see.
 constexpr int PF_NQ = 32, PF_KC = 32;
 
+__host__ __device__ constexpr int pf_ldk(int hd) { return hd + 2; }    // lanes 0-15: 16 rows, 2 banks apart
+__host__ __device__ constexpr int pf_ldv(int hd) { return hd + 16; }   // lanes 16-31: next row, 16 banks on
+constexpr int PF_LDS = PF_KC + 1;
 __host__ __device__ constexpr size_t pf_attn_smem_floats(int hd) {
-  return (size_t)PF_NQ * (hd + 4) + 2 * (size_t)PF_KC * (hd + 4) + (size_t)PF_NQ * PF_KC + 3 * (size_t)PF_NQ;
+  return (size_t)PF_KC * pf_ldk(hd) + (size_t)PF_KC * pf_ldv(hd) + (size_t)PF_NQ * PF_LDS + 2 * (size_t)PF_NQ;
+}
+
+// all-reduce over each aligned group of 8 lanes
+__device__ __forceinline__ float grp8_max(float v) {
+  v = fmaxf(v, dpp_keep<0xb1, 0xf>(v));    // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_keep<0x4e, 0xf>(v));    // quad_perm [2,3,0,1]
+  return fmaxf(v, dpp_keep<0x141, 0xf>(v));  // row_half_mirror: lane i <-> 7 - i
+}
+__device__ __forceinline__ float grp8_sum(float v) {
+  v += dpp_keep<0xb1, 0xf>(v);
+  v += dpp_keep<0x4e, 0xf>(v);
+  return v + dpp_keep<0x141, 0xf>(v);
 }
 
 template <typename KT>
@@ -215,102 +262,147 @@ __global__ __launch_bounds__(NT) void pf_attention_kernel(const float* Q, const 
   const int n = len[r];
   const int p0 = qb * QB;
   if (p0 >= n) return;
-  const int tid = threadIdx.x;
-  const int ld = hd + 4;
-  float* Qs = psm;                              // [NQ][ld]
-  float* Ks = Qs + PF_NQ * ld;                  // [KC][ld]
-  float* Vs = Ks + PF_KC * ld;                  // [KC][ld]
-  float* S = Vs + PF_KC * ld;                   // [NQ][KC]
-  float* Msc = S + PF_NQ * PF_KC;               // [NQ] rescale of this chunk
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ldk = pf_ldk(hd), ldv = pf_ldv(hd);
+  float* Ks = psm;                              // [KC][ldk]
+  float* Vs = Ks + PF_KC * ldk;                 // [KC][ldv]
+  float* P = Vs + PF_KC * ldv;                  // [NQ][PF_LDS] scores, then probabilities
+  float* Msc = P + PF_NQ * PF_LDS;              // [NQ] rescale of this chunk
   float* Ml = Msc + PF_NQ;                      // [NQ] final sums
   const size_t head_base = ((size_t)r * Hkv + h) * max_ctx;
   const int m0 = row_start[r];
   // query vector qv = g * QB + tq: head h * G + g at position p0 + tq
-  for (int i = tid; i < PF_NQ * hd; i += NT) {
-    const int qv = i / hd, d = i - qv * hd;
-    const int g = qv / QB, tq = qv - g * QB;
-    const int p = min(p0 + tq, n - 1);
-    Qs[qv * ld + d] = Q[((size_t)(m0 + p) * Hq + h * G + g) * hd + d];
-  }
-  // scores: thread -> query tid / 8, keys (tid % 8) + 8 j
-  const int sq = tid >> 3, sj = tid & 7;
-  const int sg = sq / QB, spos = p0 + (sq - sg * QB);
-  // PV: thread -> query tid / 8, dims (tid % 8) * hd / 8 ...
-  const int dpt = hd / 8;
-  const int od0 = (tid & 7) * dpt;
-  float o[16];
+  auto qpos = [&](int qv) { return p0 + (qv - (qv / QB) * QB); };
+  auto qhead = [&](int qv) { return h * G + qv / QB; };
+  const int i16 = lane & 15, k4 = lane >> 4;
+  // S tile of this wave: queries [16 qi, +16), keys [16 ki, +16)
+  const int qi = wave >> 1, ki = wave & 1;
+  float qf[32];                                 // A fragments over hd / 4 k-steps
+  {
+    const int qv = qi * 16 + i16;
+    const int p = min(qpos(qv), n - 1);
+    const float* qrow = Q + ((size_t)(m0 + p) * Hq + qhead(qv)) * hd;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;       // threads < NQ: their query's running max / sum
+    for (int ks = 0; ks < 32; ++ks) qf[ks] = (ks * 4 < hd) ? qrow[ks * 4 + k4] : 0.f;
+  }
+  // softmax role: query tid / 8, keys (tid % 8) * 4 .. + 4
+  const int sq = tid >> 3, sk0 = (tid & 7) * 4;
+  const int sp = qpos(sq);
+  float m_run = -INFINITY, l_run = 0.f;
+  // PV tiles of this wave: (query tile, d tile) pairs t = wave, wave + 4, ...
+  const int ndt = hd / 16, ntile = 2 * ndt;
+  v4f o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
   const int last_p = min(p0 + QB, n) - 1;
+  // K / V chunk staging: groups of 4 dims, up to 4 per thread (hd <= 128),
+  // loaded one chunk ahead into registers.
+  const int q4 = hd / 4, n4 = PF_KC * q4;
+  float4 kr[4], vr[4];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(tid + u * NT, n4 - 1);
+      const int j = i / q4, d = (i - j * q4) * 4;
+      const size_t off = (head_base + min(k0 + j, n - 1)) * hd + d;
+      if constexpr (sizeof(KT) == 2) {
+        const uint2 kb = *reinterpret_cast<const uint2*>(kc + off);
+        const uint2 vb = *reinterpret_cast<const uint2*>(vc + off);
+        kr[u] = make_float4(__uint_as_float(kb.x << 16), __uint_as_float(kb.x & 0xffff0000u),
+                            __uint_as_float(kb.y << 16), __uint_as_float(kb.y & 0xffff0000u));
+        vr[u] = make_float4(__uint_as_float(vb.x << 16), __uint_as_float(vb.x & 0xffff0000u),
+                            __uint_as_float(vb.y << 16), __uint_as_float(vb.y & 0xffff0000u));
+      } else {
+        kr[u] = *reinterpret_cast<const float4*>(kc + off);
+        vr[u] = *reinterpret_cast<const float4*>(vc + off);
+      }
+    }
+  };
+  fetch(0);
   for (int k0 = 0; k0 <= last_p; k0 += PF_KC) {
     __syncthreads();
-    for (int i = tid; i < PF_KC * hd; i += NT) {
-      const int j = i / hd, d = i - j * hd;
-      const int t = min(k0 + j, n - 1);
-      const size_t off = (head_base + t) * hd + d;
-      float kv, vv;
-      if constexpr (sizeof(KT) == 2) {
-        kv = __uint_as_float((uint32_t)kc[off] << 16);
-        vv = __uint_as_float((uint32_t)vc[off] << 16);
-      } else {
-        kv = kc[off];
-        vv = vc[off];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = tid + u * NT;
+      if (i < n4) {
+        const int j = i / q4, d = (i - j * q4) * 4;
+        float2* kd = reinterpret_cast<float2*>(Ks + j * ldk + d);
+        kd[0] = make_float2(kr[u].x, kr[u].y);
+        kd[1] = make_float2(kr[u].z, kr[u].w);
+        *reinterpret_cast<float4*>(Vs + j * ldv + d) = vr[u];
       }
-      Ks[j * ld + d] = kv;
-      Vs[j * ld + d] = vv;
     }
     __syncthreads();
+    if (k0 + PF_KC <= last_p) fetch(k0 + PF_KC);
+    // S tile = Q K^T
+    {
+      v4f sacc = v4f{0.f, 0.f, 0.f, 0.f};
+      const float* kp = Ks + (ki * 16 + i16) * ldk + k4;
 #pragma unroll
-    for (int jj = 0; jj < PF_KC / 8; ++jj) {
-      const int j = sj + 8 * jj;
-      const float* qp = Qs + sq * ld;
-      const float* kp = Ks + j * ld;
-      float s = 0.f;
-      for (int d = 0; d < hd; d += 4) {
-        const float4 qa = *reinterpret_cast<const float4*>(qp + d);
-        const float4 ka = *reinterpret_cast<const float4*>(kp + d);
-        s = fmaf(qa.x, ka.x, s); s = fmaf(qa.y, ka.y, s); s = fmaf(qa.z, ka.z, s); s = fmaf(qa.w, ka.w, s);
+      for (int ks = 0; ks < 32; ++ks)
+        if (ks * 4 < hd) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[ks], kp[ks * 4], sacc, 0, 0, 0);
+      const int key = k0 + ki * 16 + i16;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int qv = qi * 16 + 4 * k4 + v;
+        const int pq = qpos(qv);
+        const bool ok = key <= pq && pq < n;
+        P[qv * PF_LDS + ki * 16 + i16] = ok ? sacc[v] * scale : -INFINITY;
       }
-      const bool ok = (k0 + j <= spos) && (spos < n);
-      S[sq * PF_KC + j] = ok ? s * scale : -INFINITY;
     }
     __syncthreads();
-    if (tid < PF_NQ) {
-      float mx = m_run;
-      for (int j = 0; j < PF_KC; ++j) mx = fmaxf(mx, S[tid * PF_KC + j]);
-      const float sc = (mx == -INFINITY) ? 1.f : expf(m_run - mx);
-      float l = l_run * sc;
-      for (int j = 0; j < PF_KC; ++j) {
-        const float e = (mx == -INFINITY) ? 0.f : expf(S[tid * PF_KC + j] - mx);
-        S[tid * PF_KC + j] = e;
-        l += e;
+    // online softmax of query sq over its 32 scores (8 threads, 4 each)
+    {
+      float sv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sv[j] = P[sq * PF_LDS + sk0 + j];
+      const float mx = grp8_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+      const float mn = fmaxf(m_run, mx);
+      const bool none = (mn == -INFINITY);
+      const float sc = none ? 1.f : expf(m_run - mn);
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e = none ? 0.f : expf(sv[j] - mn);
+        P[sq * PF_LDS + sk0 + j] = e;
+        part += e;
       }
-      m_run = mx;
-      l_run = l;
-      Msc[tid] = sc;
+      l_run = l_run * sc + grp8_sum(part);
+      m_run = mn;
+      if ((tid & 7) == 0) Msc[sq] = sc;
     }
     __syncthreads();
-    const float sc = Msc[sq];
+    // O = O * rescale + P V
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (i < dpt) o[i] *= sc;
-    for (int j = 0; j < PF_KC; ++j) {
-      const float pj = S[sq * PF_KC + j];
-      const float* vp = Vs + j * ld + od0;
+    for (int t4 = 0; t4 < 4; ++t4) {
+      const int t = wave + 4 * t4;
+      if (t < ntile) {
+        const int tq = t / ndt, td = t - tq * ndt;
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (i < dpt) o[i] = fmaf(pj, vp[i], o[i]);
+        for (int v = 0; v < 4; ++v) o[t4][v] *= Msc[tq * 16 + 4 * k4 + v];
+        const float* pp = P + (tq * 16 + i16) * PF_LDS + k4;
+        const float* vp = Vs + k4 * ldv + td * 16 + i16;
+#pragma unroll
+        for (int ks = 0; ks < PF_KC / 4; ++ks)
+          o[t4] = __builtin_amdgcn_mfma_f32_16x16x4f32(pp[ks * 4], vp[ks * 4 * ldv], o[t4], 0, 0, 0);
+      }
     }
   }
-  if (tid < PF_NQ) Ml[tid] = l_run;
+  if ((tid & 7) == 0) Ml[sq] = l_run;
   __syncthreads();
-  if (spos < n) {
-    const float inv = 1.0f / Ml[sq];
-    float* dst = out + (size_t)(m0 + spos) * ldo + (size_t)(h * G + sg) * hd + od0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (i < dpt) dst[i] = o[i] * inv;
+  for (int t4 = 0; t4 < 4; ++t4) {
+    const int t = wave + 4 * t4;
+    if (t < ntile) {
+      const int tq = t / ndt, td = t - tq * ndt;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int qv = tq * 16 + 4 * k4 + v;
+        const int pq = qpos(qv);
+        if (pq < n)
+          out[(size_t)(m0 + pq) * ldo + (size_t)qhead(qv) * hd + td * 16 + i16] = o[t4][v] / Ml[qv];
+      }
+    }
   }
 }
 

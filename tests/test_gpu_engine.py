@@ -363,3 +363,64 @@ def test_qwen3_17b_shape_bf16_weights_and_kv(hip_device):
         assert mism <= total // 200
     print(f"Qwen3-1.7B BF16 weights + BF16 KV: engine {rel:.3e}, oracle FP32 vs FP64 {spread:.3e}")
     assert rel < tol
+
+
+def _engine_kv(e, layer, kv, bf16):
+    """Layer ``layer``'s K (kv=0) or V (kv=1) cache as float32
+    ``[rows, n_kv_heads, max_ctx, head_dim]`` (BF16 widened)."""
+    import ctypes as C
+
+    from soraku_amd._lib import check, lib
+
+    p = C.c_void_p()
+    check(lib().sk_kv_ptr(e._h, layer, kv, C.byref(p)))
+    e.synchronize()
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    s = e.shape
+    out = np.empty((e.rows, s.n_kv_heads, e.max_len, s.head_dim), np.uint16 if bf16 else np.float32)
+    assert hip.hipMemcpy(out.ctypes.data, p, out.nbytes, 2) == 0  # hipMemcpyDeviceToHost
+    return (out.astype(np.uint32) << 16).view(np.float32) if bf16 else out
+
+
+@pytest.mark.parametrize("kv_bf16", [False, True])
+def test_batched_prefill_matches_oracle(hip_device, kv_bf16):
+    """The batched prefill (MFMA GEMMs over all prefix tokens, causal
+    attention per row) against the oracle's prefill at the Qwen3-0.6B shape
+    with very unequal rows (300 and 11 positions): each row's final-normed
+    hidden state, and the K/V cache of both rows in the first, middle and last
+    layer (relative to the largest entry; FP32 GEMMs differ from the oracle's
+    only in summation order).  With a BF16 cache, values that sit near a BF16
+    rounding boundary can round the other way (one ulp, 2^-8), and later
+    layers carry that on, hence the looser bounds there."""
+    from oracle.generate import start_states
+    from oracle.model import QWEN3_06B
+    from soraku_amd import GraphFrameEngine
+
+    s = QWEN3_06B
+    w = synthetic_weights(s, 4, norm_gain_std=0.1, bias_std=0.02)
+    rng = np.random.default_rng(12)
+    text, uncond = rng.integers(0, s.text_vocab, 290), np.array([9])
+    prompt = rng.integers(0, s.codebook_size, (9, s.n_codebooks))
+    m = OracleModel(s, w, np.float32, kv_bf16=kv_bf16)
+    st = start_states(m, text, prompt, uncond, 1.5, 320)
+    e = GraphFrameEngine(device=hip_device, max_cache_len=320, cfg_scale=1.5, batch=2, state_dict=w,
+                         shape=_shape(s), kv_bf16=kv_bf16)
+    e.prefill(text, uncond, prompt)
+    hid = e.hidden()
+    ref = np.stack([x.hidden for x in st])
+    rel = float((np.abs(hid - ref).max(axis=1) / np.abs(ref).max(axis=1)).max())
+    worst = 0.0
+    for layer in (0, s.n_layers // 2, s.n_layers - 1):
+        for kv, name in ((0, "k"), (1, "v")):
+            got = _engine_kv(e, layer, kv, kv_bf16)
+            for r, x in enumerate(st):
+                n = x.kv_len
+                want = getattr(x, name)[layer, :, :n]
+                err = np.abs(got[r, :, :n] - want).max() / np.abs(want).max()
+                worst = max(worst, float(err))
+    e.close()
+    print(f"prefill 300/11 rows, kv_bf16 {kv_bf16}: hidden rel {rel:.2e}, cache rel {worst:.2e}")
+    assert [x.kv_len for x in st] == [300, 11]
+    assert rel < (5e-3 if kv_bf16 else 1e-3)
+    assert worst < (1e-2 if kv_bf16 else 1e-3)

@@ -59,7 +59,7 @@ typedef struct sk_config {
   float rope_theta;       /* 1e6                                                */
   float frame_scale;      /* Q^-1/2 (model.py:99)                               */
   int32_t weight_dtype;   /* SK_F32 or SK_BF16 for every matrix                 */
-  int32_t n_utts;         /* utterances decoded together                        */
+  int32_t n_utts;         /* utterances decoded together (n_utts*cfg_rows <= 32) */
   int32_t cfg_rows;       /* rows per utterance: 2 = cond+uncond, 1 = no CFG     */
   int32_t max_ctx;        /* KV capacity per row (prefix + frames)              */
   int32_t max_frames;     /* capacity of the per-frame input/code ring          */

@@ -25,6 +25,7 @@
 #include "sk_kernels.h"
 #include "sk_launch.h"
 #include "sk_prefill.h"
+#include "sk_wide.h"
 #include "soraku_mi355x.h"
 
 using namespace sk;
@@ -47,6 +48,7 @@ hipError_t dalloc(T** p, size_t n) {
 struct sk_engine {
   sk_config c{};
   int rows = 0, G = 0, nqkv = 0, inner_max = 0, max_chunks = 0;
+  bool wide = false;          // more rows than the GEMV kernels take: skinny MFMA GEMMs
   int device = 0;
   hipStream_t stream = nullptr;
 
@@ -129,8 +131,10 @@ int validate_config(const sk_config* c) {
   SK_CHECK(c->weight_dtype == SK_F32 || c->weight_dtype == SK_BF16, SK_EINVAL, "weight_dtype must be SK_F32 or SK_BF16");
   SK_CHECK(c->kv_dtype == SK_F32 || c->kv_dtype == SK_BF16, SK_EINVAL, "kv_dtype must be SK_F32 or SK_BF16");
   SK_CHECK(c->cfg_rows == 1 || c->cfg_rows == 2, SK_EINVAL, "cfg_rows must be 1 or 2");
-  SK_CHECK(c->n_utts >= 1 && c->n_utts * c->cfg_rows <= 4, SK_EINVAL,
-           "n_utts * cfg_rows must be in [1, 4] (decode rows)");
+  SK_CHECK(c->n_utts >= 1 && c->n_utts * c->cfg_rows <= SK_ROWS, SK_EINVAL,
+           "n_utts * cfg_rows must be in [1, %d] (decode rows)", SK_ROWS);
+  SK_CHECK(c->n_utts * c->cfg_rows <= 4 || c->depth_inner % 32 == 0, SK_EINVAL,
+           "depth_inner must be a multiple of 32 for more than 4 decode rows");
   SK_CHECK(c->max_ctx >= 2 && c->max_ctx <= 65536, SK_EINVAL, "max_ctx must be in [2, 65536]");
   SK_CHECK(c->max_frames >= 1, SK_EINVAL, "max_frames must be positive");
   SK_CHECK(c->n_language == 0 || c->n_language == 4, SK_EINVAL, "n_language must be 0 or 4");
@@ -168,6 +172,33 @@ int check_decode_weights(const sk_engine* e) {
 
 // ---- graph bodies -------------------------------------------------------
 
+// ---- many-row path: skinny MFMA GEMMs ---------------------------------------
+
+// 16 waves per workgroup (K split 16 ways) when there are few workgroups
+// (N <= 1024 outputs, one weight matrix), else 8.  NORM: RMSNorm of x folded in.
+template <int EPI, bool NORM, typename WL>
+hipError_t launch_skinny_w(const SkinnyArgs& a, hipStream_t st) {
+  const dim3 grid((a.N + 15) / 16);
+  if (EPI != EPI_SWIGLU && a.N <= 1024)
+    hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WL, 16, NORM>), grid, dim3(16 * 64), 0, st, a);
+  else
+    hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WL, 8, NORM>), grid, dim3(8 * 64), 0, st, a);
+  return hipGetLastError();
+}
+template <int EPI, bool NORM = false>
+hipError_t launch_skinny(int wdtype, const SkinnyArgs& a, hipStream_t st) {
+  return wdtype == SK_BF16 ? launch_skinny_w<EPI, NORM, WBF16>(a, st) : launch_skinny_w<EPI, NORM, WF32>(a, st);
+}
+
+SkinnyArgs skinny_args(const void* w, int N, int K, const float* x, int ldx, float* out, int ldo, int R) {
+  SkinnyArgs a{};
+  a.w[0] = w; a.w[1] = nullptr; a.w[2] = nullptr;
+  a.seg_rows[0] = N; a.seg_rows[1] = 0; a.seg_rows[2] = 0;
+  a.x = x; a.ldx = ldx; a.out = out; a.ldo = ldo;
+  a.R = R; a.N = N; a.K = K;
+  return a;
+}
+
 hipError_t enqueue_trunk(sk_engine* e) {
   const sk_config& c = e->c;
   const int d = c.d_model, hd = c.head_dim, M = e->rows;
@@ -179,7 +210,15 @@ hipError_t enqueue_trunk(sk_engine* e) {
     a.w[1] = w.k; a.w[2] = w.v;
     a.seg_rows[0] = c.n_q_heads * hd; a.seg_rows[1] = c.n_kv_heads * hd; a.seg_rows[2] = c.n_kv_heads * hd;
     a.norm_w = w.in_norm; a.eps = c.trunk_eps;
-    if ((err = launch_gemv<PRO_NORM, EPI_STORE>(wt, M, a, e->stream)) != hipSuccess) return err;
+    if (e->wide) {
+      SkinnyArgs k = skinny_args(w.q, e->nqkv, d, e->x, d, e->qkv, e->nqkv, M);
+      k.w[1] = w.k; k.w[2] = w.v;
+      k.seg_rows[0] = a.seg_rows[0]; k.seg_rows[1] = a.seg_rows[1]; k.seg_rows[2] = a.seg_rows[2];
+      k.norm_w = w.in_norm; k.eps = c.trunk_eps;
+      if ((err = launch_skinny<EPI_STORE, true>(wt, k, e->stream)) != hipSuccess) return err;
+    } else if ((err = launch_gemv<PRO_NORM, EPI_STORE>(wt, M, a, e->stream)) != hipSuccess) {
+      return err;
+    }
 
     AttnArgs at{};
     at.qkv = e->qkv; at.ldqkv = e->nqkv;
@@ -203,6 +242,19 @@ hipError_t enqueue_trunk(sk_engine* e) {
     hipLaunchKernelGGL(attention_combine_kernel, dim3(c.n_q_heads, M), dim3(NT), 0, e->stream, at);
     if ((err = hipGetLastError()) != hipSuccess) return err;
 
+    if (e->wide) {
+      const int hq = c.n_q_heads * hd, I = c.trunk_inter;
+      SkinnyArgs k = skinny_args(w.o, d, hq, e->attn, hq, e->x, d, M);
+      k.res = e->x; k.ldr = d;
+      if ((err = launch_skinny<EPI_RESID>(wt, k, e->stream)) != hipSuccess) return err;
+      k = skinny_args(w.gate, I, d, e->x, d, e->act, e->inner_max, M);
+      k.w2 = w.up; k.norm_w = w.post_norm; k.eps = c.trunk_eps;
+      if ((err = launch_skinny<EPI_SWIGLU, true>(wt, k, e->stream)) != hipSuccess) return err;
+      k = skinny_args(w.down, d, I, e->act, e->inner_max, e->x, d, M);
+      k.res = e->x; k.ldr = d;
+      if ((err = launch_skinny<EPI_RESID>(wt, k, e->stream)) != hipSuccess) return err;
+      continue;
+    }
     a = gemv_args(w.o, d, c.n_q_heads * hd, e->attn, c.n_q_heads * hd, e->x, d);
     a.res = e->x; a.ldr = d;
     if ((err = launch_gemv<PRO_NONE, EPI_RESID>(wt, M, a, e->stream)) != hipSuccess) return err;
@@ -216,6 +268,34 @@ hipError_t enqueue_trunk(sk_engine* e) {
     if ((err = launch_gemv<PRO_NONE, EPI_RESID>(wt, M, a, e->stream)) != hipSuccess) return err;
   }
   return hipSuccess;
+}
+
+// Depth step q of the many-row path: prefix advance + norm_in, SwiGLU, down +
+// residual, norm_out, classifier + bias (the sampler follows).
+hipError_t enqueue_depth_wide(sk_engine* e, int q) {
+  const sk_config& c = e->c;
+  const int d = c.d_model, M = e->rows, V = c.audio_vocab, wt = c.weight_dtype;
+  const size_t tsz = (wt == SK_BF16) ? 2 : 4;
+  hipError_t err;
+  if (wt == SK_BF16)
+    hipLaunchKernelGGL(depth_in_kernel<WBF16>, dim3(M), dim3(NT), 0, e->stream, e->hidden, e->prefix, e->table,
+                       e->codes_cur, q, c.n_codebooks, V, d, c.frame_scale, c.cfg_rows, e->d_norm_in, c.depth_eps,
+                       e->abuf);
+  else
+    hipLaunchKernelGGL(depth_in_kernel<WF32>, dim3(M), dim3(NT), 0, e->stream, e->hidden, e->prefix, e->table,
+                       e->codes_cur, q, c.n_codebooks, V, d, c.frame_scale, c.cfg_rows, e->d_norm_in, c.depth_eps,
+                       e->abuf);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  SkinnyArgs k = skinny_args(e->d_gate, c.depth_inner, d, e->abuf, d, e->act, e->inner_max, M);
+  k.w2 = e->d_up;
+  if ((err = launch_skinny<EPI_SWIGLU>(wt, k, e->stream)) != hipSuccess) return err;
+  k = skinny_args(e->d_down, d, c.depth_inner, e->act, e->inner_max, e->ybuf, d, M);
+  k.res = e->abuf; k.ldr = d;
+  if ((err = launch_skinny<EPI_RESID>(wt, k, e->stream)) != hipSuccess) return err;
+  const void* tq = static_cast<const char*>(e->table) + (size_t)q * V * d * tsz;
+  k = skinny_args(tq, V, d, e->ybuf, d, e->logits, V, M);
+  k.bias = e->d_bias + (size_t)q * V; k.norm_w = e->d_norm_out; k.eps = c.depth_eps;
+  return launch_skinny<EPI_BIAS, true>(wt, k, e->stream);
 }
 
 hipError_t enqueue_frame(sk_engine* e) {
@@ -236,6 +316,13 @@ hipError_t enqueue_frame(sk_engine* e) {
   // result to the other buffer of the pair (readers of one launch never see
   // its own writes).  The last sampler launch zeroes `prefix` again.
   for (int q = 0; q < c.n_codebooks; ++q) {
+    if (e->wide) {
+      if ((err = enqueue_depth_wide(e, q)) != hipSuccess) return err;
+      err = (wt == SK_BF16) ? launch_sample_step<WBF16>(s, q, c.n_utts, e->stream)
+                            : launch_sample_step<WF32>(s, q, c.n_utts, e->stream);
+      if (err != hipSuccess) return err;
+      continue;
+    }
     GemvArgs a = gemv_args(e->d_gate, c.depth_inner, d, e->hidden, d, e->act, e->inner_max);
     a.w[1] = e->d_up; a.ldx2 = d;
     a.norm_w = e->d_norm_in; a.eps = c.depth_eps; a.norm_out = e->abuf; a.ldno = d;
@@ -434,6 +521,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   e->c = *cfg;
   const sk_config& c = e->c;
   e->rows = c.n_utts * c.cfg_rows;
+  e->wide = e->rows > 4;
   e->G = c.n_q_heads / c.n_kv_heads;
   e->nqkv = (c.n_q_heads + 2 * c.n_kv_heads) * c.head_dim;
   e->inner_max = c.trunk_inter > c.depth_inner ? c.trunk_inter : c.depth_inner;

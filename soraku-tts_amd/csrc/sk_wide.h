@@ -1,0 +1,180 @@
+// Decode kernels for many rows (more than the GEMV kernels' 4): several
+// utterances with CFG decoded together, up to 32 rows (the reference decodes
+// one utterance's two CFG rows; fast_generate.py:232-328 batches those).
+//
+// The projections run as skinny GEMMs on the FP32 matrix cores: each
+// workgroup owns 16 outputs for all rows and splits K over its 8 or 16 waves;
+// the per-wave partial tiles are summed through LDS in fixed wave order
+// (deterministic).  RMSNorms that feed a projection are folded into it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "sk_kernels.h"
+
+namespace sk {
+
+struct SkinnyArgs {
+  const void* w[3]; int seg_rows[3];   // weight segments (q / k / v), rows of each
+  const void* w2;                      // SwiGLU: up weights
+  const float* x; int ldx;             // [R][K]
+  const float* norm_w; float eps;      // optional RMSNorm of x rows (gain [K])
+  float* out; int ldo;                 // [R][N]
+  const float* res; int ldr;           // residual (may alias out)
+  const float* bias;                   // [N]
+  int R, N, K;
+};
+
+constexpr int SK_ROWS = 32;             // rows covered (two 16-row MFMA tiles)
+
+typedef float sv4f __attribute__((ext_vector_type(4)));
+
+// out[r][o] for 16 outputs o of this workgroup and all rows r < R.  Lane l of
+// a wave holds weights of output o0 + l % 16 and rows (l % 16) (+16) of x for
+// VEC consecutive k at kb + VEC (l / 16); MFMA j pairs weight and x at the
+// same k, so every k of the block enters the sum exactly once.  Wave w takes
+// blocks w, w + W, ...; the next block's loads are in flight while one is
+// multiplied.  NORM: x is taken through RMSNorm -- the gain is applied per k,
+// the row's sum of squares is gathered on the way and 1 / rms scales the sum
+// at the end (out = inv_rms * sum_k w_k g_k x_k).  EPI is one of the GEMV
+// epilogues (store, bias, residual, SwiGLU).
+template <int EPI, typename WL, int W, bool NORM>
+__global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(SkinnyArgs a) {
+  constexpr int NA = (EPI == EPI_SWIGLU) ? 2 : 1;
+  constexpr int VEC = WL::VEC;          // 4 (FP32) or 8 (BF16) k per lane per block
+  constexpr int BK = 4 * VEC;           // k per block
+  __shared__ float red[W][NA * 2 * 4][64];
+  __shared__ float ssq[NORM ? W : 1][2][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i16 = lane & 15, kq = lane >> 4;
+  const int o0 = blockIdx.x * 16;
+  const int o = min(o0 + i16, a.N - 1);
+  const void* wb;
+  int wr;
+  if (o < a.seg_rows[0]) { wb = a.w[0]; wr = o; }
+  else if (o < a.seg_rows[0] + a.seg_rows[1]) { wb = a.w[1]; wr = o - a.seg_rows[0]; }
+  else { wb = a.w[2]; wr = o - a.seg_rows[0] - a.seg_rows[1]; }
+  const size_t woff = (size_t)wr * a.K + VEC * kq;
+  const size_t w2off = (size_t)o * a.K + VEC * kq;
+  const float* xr0 = a.x + (size_t)min(i16, a.R - 1) * a.ldx + VEC * kq;
+  const float* xr1 = a.x + (size_t)min(16 + i16, a.R - 1) * a.ldx + VEC * kq;
+  const float* gp = NORM ? a.norm_w + VEC * kq : nullptr;
+  struct Stage { float w[NA][VEC], x0[VEC], x1[VEC], g[NORM ? VEC : 1]; };
+  auto load = [&](int kb, Stage& st) {
+    WL::load(wb, woff + kb, st.w[0]);
+    if constexpr (NA == 2) WL::load(a.w2, w2off + kb, st.w[NA - 1]);
+#pragma unroll
+    for (int j = 0; j < VEC; j += 4) {
+      const float4 p = *reinterpret_cast<const float4*>(xr0 + kb + j);
+      const float4 q = *reinterpret_cast<const float4*>(xr1 + kb + j);
+      st.x0[j] = p.x; st.x0[j + 1] = p.y; st.x0[j + 2] = p.z; st.x0[j + 3] = p.w;
+      st.x1[j] = q.x; st.x1[j + 1] = q.y; st.x1[j + 2] = q.z; st.x1[j + 3] = q.w;
+      if constexpr (NORM) {
+        const float4 g = *reinterpret_cast<const float4*>(gp + kb + j);
+        st.g[j] = g.x; st.g[j + 1] = g.y; st.g[j + 2] = g.z; st.g[j + 3] = g.w;
+      }
+    }
+  };
+  sv4f acc[NA][2];
+#pragma unroll
+  for (int n = 0; n < NA; ++n) acc[n][0] = acc[n][1] = sv4f{0.f, 0.f, 0.f, 0.f};
+  float ss0 = 0.f, ss1 = 0.f;
+  auto comp = [&](const Stage& st) {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      float x0 = st.x0[j], x1 = st.x1[j];
+      if constexpr (NORM) {
+        ss0 = fmaf(x0, x0, ss0);
+        ss1 = fmaf(x1, x1, ss1);
+        x0 *= st.g[j];
+        x1 *= st.g[j];
+      }
+#pragma unroll
+      for (int n = 0; n < NA; ++n) {
+        acc[n][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(st.w[n][j], x0, acc[n][0], 0, 0, 0);
+        acc[n][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(st.w[n][j], x1, acc[n][1], 0, 0, 0);
+      }
+    }
+  };
+  Stage sa, sb;
+  constexpr int STEP = W * BK;
+  int kb = wave * BK;
+  if (kb < a.K) load(kb, sa);
+  for (; kb < a.K; kb += 2 * STEP) {
+    const int k1 = kb + STEP, k2 = k1 + STEP;
+    if (k1 < a.K) load(k1, sb);
+    comp(sa);
+    if (k1 < a.K) {
+      if (k2 < a.K) load(k2, sa);
+      comp(sb);
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < NA; ++n)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][(n * 2 + t) * 4 + v][lane] = acc[n][t][v];
+  if constexpr (NORM) { ssq[wave][0][lane] = ss0; ssq[wave][1][lane] = ss1; }
+  __syncthreads();
+  if (tid >= 512) return;
+  // thread -> (row tile t, v, lane): output o0 + 4 (lane / 16) + v, row 16 t + lane % 16
+  const int t = tid >> 8, v = (tid >> 6) & 3, l = tid & 63;
+  const int oo = o0 + 4 * (l >> 4) + v, r = 16 * t + (l & 15);
+  float c[NA];
+#pragma unroll
+  for (int n = 0; n < NA; ++n) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) s += red[w][(n * 2 + t) * 4 + v][l];
+    c[n] = s;
+  }
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4) ss += ssq[w][t][k4 * 16 + (l & 15)];
+    const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+#pragma unroll
+    for (int n = 0; n < NA; ++n) c[n] *= inv;
+  }
+  if (oo < a.N && r < a.R) {
+    float y = c[0];
+    if constexpr (EPI == EPI_BIAS) y = y + a.bias[oo];
+    if constexpr (EPI == EPI_RESID) y = a.res[(size_t)r * a.ldr + oo] + y;
+    if constexpr (EPI == EPI_SWIGLU) y = y / (1.0f + expf(-y)) * c[NA - 1];
+    a.out[(size_t)r * a.ldo + oo] = y;
+  }
+}
+
+// Depth step q, row r (utterance r / rows_per_utt): for q > 0 the codebook
+// prefix advances by the previous code's table row (prefix += scale *
+// table[q-1][code], model.py:600-605) in place; then out = RMSNorm_in(hidden
+// + prefix) (eps FLT_EPSILON) -- the depth MLP input and its residual.
+template <typename TL>
+__global__ __launch_bounds__(NT) void depth_in_kernel(const float* hidden, float* prefix, const void* table,
+                                                      const int* codes_cur, int q, int Q, int V, int D,
+                                                      float scale, int rows_per_utt, const float* w, float eps,
+                                                      float* out) {
+  __shared__ float red[WAVES];
+  const int r = blockIdx.x, ut = r / rows_per_utt;
+  const size_t trow = (q > 0) ? ((size_t)(q - 1) * V + codes_cur[ut * Q + q - 1]) * D : 0;
+  float s = 0.f;
+  for (int k = threadIdx.x; k < D; k += NT) {
+    float p = prefix[(size_t)r * D + k];
+    if (q > 0) {
+      p = __fadd_rn(p, __fmul_rn(TL::get(table, trow + k), scale));
+      prefix[(size_t)r * D + k] = p;
+    }
+    const float x = __fadd_rn(hidden[(size_t)r * D + k], p);
+    s += x * x;
+  }
+  const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
+  for (int k = threadIdx.x; k < D; k += NT) {
+    const float x = __fadd_rn(hidden[(size_t)r * D + k], prefix[(size_t)r * D + k]);
+    out[(size_t)r * D + k] = w[k] * (x * inv);
+  }
+}
+
+}  // namespace sk

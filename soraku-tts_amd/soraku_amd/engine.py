@@ -181,21 +181,31 @@ class GraphFrameEngine:
 
     def prefill(self, cond_ids, uncond_ids=None, prompt_codes=None):
         """[text, BOS frame, prompt frames] per row (model.py:623-656); returns
-        the depth-input hidden ``[rows, d]`` like graph_frame.py:118-198."""
+        the depth-input hidden ``[rows, d]`` like graph_frame.py:118-198.
+        With several utterances, every utterance gets this prefix."""
+        return self.prefill_utterances([(cond_ids, uncond_ids, prompt_codes)] * self.n_utts)
+
+    def prefill_utterances(self, items):
+        """Several utterances, each with its own prefix: ``items`` holds
+        ``(cond_ids, uncond_ids, prompt_codes)`` per utterance (ragged lengths
+        are fine; each row keeps its own length and positions).  Returns the
+        depth-input hidden ``[rows, d]``."""
         import torch
 
         def ids_of(x):
             return np.asarray(x.cpu() if hasattr(x, "cpu") else x, np.int64).reshape(-1)
 
-        cond = ids_of(cond_ids)
-        rows = [cond]
-        if self.batch == 2:
-            uncond = ids_of(uncond_ids) if uncond_ids is not None else cond
-            if uncond.size > cond.size:
-                raise ValueError("uncond text is longer than cond")
-            rows.append(uncond)
-        frames = self._frames(prompt_codes)
-        for u in range(self.n_utts):
+        if len(items) != self.n_utts:
+            raise ValueError(f"{len(items)} prefixes for {self.n_utts} utterances")
+        for u, (cond_ids, uncond_ids, prompt_codes) in enumerate(items):
+            cond = ids_of(cond_ids)
+            rows = [cond]
+            if self.batch == 2:
+                uncond = ids_of(uncond_ids) if uncond_ids is not None else cond
+                if uncond.size > cond.size:
+                    raise ValueError("uncond text is longer than cond")
+                rows.append(uncond)
+            frames = self._frames(prompt_codes)
             for b, ids in enumerate(rows):
                 n = ids.size + frames.shape[0]
                 if n > self.max_len:

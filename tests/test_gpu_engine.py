@@ -424,3 +424,65 @@ def test_batched_prefill_matches_oracle(hip_device, kv_bf16):
     assert [x.kv_len for x in st] == [300, 11]
     assert rel < (5e-3 if kv_bf16 else 1e-3)
     assert worst < (1e-2 if kv_bf16 else 1e-3)
+
+
+def _many_utterance_case(s, w, n_utts, seed, hip_device, bf16=False, frames=2, max_len=64, text_len=(5, 30)):
+    """n_utts utterances with ragged prefixes, teacher-forced for `frames`
+    frames through one engine; per utterance, the engine's masked merged
+    logits and the oracle's for the same prefix and codes."""
+    from soraku_amd import GraphFrameEngine
+
+    rng = np.random.default_rng(seed)
+    items, codes = [], []
+    for _ in range(n_utts):
+        nt = int(rng.integers(*text_len))
+        items.append((rng.integers(0, s.text_vocab, nt), np.array([int(rng.integers(0, s.text_vocab))]),
+                      rng.integers(0, s.codebook_size, (int(rng.integers(0, 4)), s.n_codebooks))))
+        codes.append(rng.integers(0, s.codebook_size, (frames, s.n_codebooks)))
+    codes = np.stack(codes)                       # [utts, frames, Q]
+    cfg = 1.5
+    e = GraphFrameEngine(device=hip_device, max_cache_len=max_len, cfg_scale=cfg, batch=2, state_dict=w,
+                         shape=_shape(s), n_utts=n_utts, bf16=bf16)
+    e.set_temperature(0.0)
+    e.set_debug(True)
+    e.prefill_utterances(items)
+    e.capture()
+    got = []
+    for fi in range(frames):
+        _, lg = e.step_frame(mask_eos_q0=False, uniforms=np.zeros(n_utts * s.n_codebooks),
+                             forced_codes=codes[:, fi], return_logits=True)
+        got.append(lg)
+    e.close()
+    got = np.stack(got, axis=1)                   # [utts, frames, Q, V]
+    worst = 0.0
+    m = OracleModel(s, w, np.float64)
+    for u, (text, uncond, prompt) in enumerate(items):
+        ref = _oracle_forced_logits(m, s, text, prompt, uncond, codes[u], cfg)
+        worst = max(worst, _rowwise_rel(got[u].reshape(-1, got.shape[-1]), ref))
+    return worst
+
+
+def test_many_utterances_tiny(hip_device):
+    """Eight decode rows (4 utterances x CFG) take the skinny-GEMM path; each
+    utterance, with its own ragged prefix, matches the oracle run alone."""
+    from oracle.model import TINY
+
+    w = synthetic_weights(TINY, 31, norm_gain_std=0.1, bias_std=0.02)
+    rel = _many_utterance_case(TINY, w, 4, 3, hip_device, frames=3)
+    print(f"tiny, 4 utterances: max row-relative logit error {rel:.3e}")
+    assert rel < LOGIT_TOL
+
+
+def test_sixteen_utterances_q06b_bf16(hip_device):
+    """Batch-32 decode (16 utterances x CFG) at the Qwen3-0.6B shape with BF16
+    weights (FP32 accumulation), ragged prefixes: every utterance against the
+    oracle on the same BF16-rounded weights."""
+    import dataclasses
+
+    from oracle.model import QWEN3_06B
+
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)   # only prefix ids are embedded
+    w = _device_weights(s, 17, hip_device)
+    rel = _many_utterance_case(s, w, 16, 5, hip_device, bf16=True, frames=2)
+    print(f"q06b BF16, 16 utterances: max row-relative logit error {rel:.3e}")
+    assert rel < LOGIT_TOL

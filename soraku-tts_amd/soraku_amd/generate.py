@@ -44,8 +44,8 @@ class FastGenerator:
         self._engine: GraphFrameEngine | None = None
         self._engine_key = None
 
-    def _engine_for(self, max_len: int, batch: int, cfg_scale: float) -> GraphFrameEngine:
-        key = (batch,)
+    def _engine_for(self, max_len: int, batch: int, cfg_scale: float, n_utts: int = 1) -> GraphFrameEngine:
+        key = (batch, n_utts)
         e = self._engine
         if e is None or e.max_len < max_len or self._engine_key != key:
             if e is not None:
@@ -53,7 +53,7 @@ class FastGenerator:
             e = GraphFrameEngine(self.model, device=self.device, max_cache_len=max(max_len, 512),
                                  cfg_scale=cfg_scale, batch=batch, state_dict=self._state_dict,
                                  shape=self._shape, language_token_ids=self._language_token_ids,
-                                 bf16=self.bf16, kv_bf16=self.kv_bf16)
+                                 bf16=self.bf16, kv_bf16=self.kv_bf16, n_utts=n_utts)
             self._engine, self._engine_key = e, key
         return e
 
@@ -110,3 +110,81 @@ class FastGenerator:
             "sampled": sampled,
             "temperature": temperature,
         }
+
+    def generate_batch(self, requests, *, max_new_frames: int = 384, min_new_frames: int = 4,
+                       temperature: float = 0.9, top_k: int | None = 50, top_p: float | None = 0.95,
+                       temperature_q0: float | None = None, top_k_q0: int | None = None,
+                       top_p_q0: float | None = None, cfg_scale: float = 1.0, seeds=None, uniforms=None,
+                       on_frame: Any = None):
+        """Several utterances decoded together (one engine, ``len(requests)``
+        x CFG rows; no reference counterpart beyond one utterance's CFG pair,
+        fast_generate.py:232-328).  ``requests``: dicts with ``input_ids``
+        ``[1, L]`` and optional ``prompt_codes`` / ``uncond_input_ids``;
+        prefixes may differ in length.  Utterance u draws from
+        ``uniforms[u]`` (``[max_new_frames, Q]``) or from
+        ``default_rng(seeds[u])`` exactly as ``generate(seed=seeds[u])`` would,
+        and retires at its own EOS (q0 code == EOS once ``index >=
+        min_new_frames``): later frames of a retired utterance are dropped, and
+        the batch stops when every utterance has retired or at
+        ``max_new_frames``.  Returns a list of ``(codes [T_u, Q], info)``."""
+        import torch
+
+        U = len(requests)
+        if U < 1:
+            raise ValueError("generate_batch needs at least one request")
+        if cfg_scale != 1.0 and any(r.get("uncond_input_ids") is None for r in requests):
+            raise ValueError("classifier-free guidance requires uncond_input_ids")
+        batch = 2 if cfg_scale != 1.0 else 1
+        Qn = self._shape.n_codebooks if self._shape else 16
+        longest = 0
+        for r in requests:
+            ids = r["input_ids"]
+            shape = ids.shape if hasattr(ids, "shape") else np.asarray(ids).shape
+            if len(shape) != 2 or shape[0] != 1:
+                raise ValueError("generate_batch expects input_ids of shape [1,L]")
+            pc = r.get("prompt_codes")
+            n_prompt = 0 if pc is None else int(np.prod(pc.shape)) // Qn
+            longest = max(longest, int(shape[1]) + 1 + n_prompt)
+        engine = self._engine_for(longest + max_new_frames + 8, batch, cfg_scale, n_utts=U)
+        Q = engine.Q
+        engine.cfg.fill_(cfg_scale)
+        sampled = temperature > 0 or (temperature_q0 is not None and temperature_q0 > 0)
+        engine.set_temperature(temperature, q0=temperature_q0)
+        engine.set_sampling(sampled=sampled, top_k=top_k, top_p=top_p, top_k_q0=top_k_q0,
+                            top_p_q0=top_p_q0)
+        if uniforms is None:
+            seeds = list(seeds) if seeds is not None else [None] * U
+            uniforms = np.stack([np.random.default_rng(sd).random((max_new_frames, Q)) for sd in seeds])
+        uniforms = np.asarray(uniforms, np.float64).reshape(U, -1, Q)
+        if uniforms.shape[1] < max_new_frames:
+            raise ValueError("uniforms must cover max_new_frames rows per utterance")
+        engine.prefill_utterances([(r["input_ids"], r.get("uncond_input_ids") if batch == 2 else None,
+                                    r.get("prompt_codes")) for r in requests])
+        if engine.graph is None:
+            engine.capture()
+        eos = engine.shape.eos_id
+        frames: list[list] = [[] for _ in range(U)]
+        reason = ["max_frames"] * U
+        live = [True] * U
+        for index in range(max_new_frames):
+            codes = engine.step_frame(mask_eos_q0=index < min_new_frames,
+                                      uniforms=np.ascontiguousarray(uniforms[:, index]))
+            codes = codes.view(U, Q)
+            for u in range(U):
+                if not live[u]:
+                    continue
+                if index >= min_new_frames and int(codes[u, 0]) == eos:
+                    live[u] = False
+                    reason[u] = "eos"
+                    continue
+                frames[u].append(codes[u].clone().view(1, Q))
+                if on_frame is not None:
+                    on_frame(u, frames[u][-1])
+            if not any(live):
+                break
+        out = []
+        for u in range(U):
+            c = torch.cat(frames[u], dim=0) if frames[u] else torch.empty(0, Q, dtype=torch.long)
+            out.append((c, {"stop_reason": reason[u], "num_frames": c.shape[0], "cfg_scale": cfg_scale,
+                            "backend": "mi355x", "sampled": sampled, "temperature": temperature}))
+        return out

@@ -486,3 +486,40 @@ def test_sixteen_utterances_q06b_bf16(hip_device):
     rel = _many_utterance_case(s, w, 16, 5, hip_device, bf16=True, frames=2)
     print(f"q06b BF16, 16 utterances: max row-relative logit error {rel:.3e}")
     assert rel < LOGIT_TOL
+
+
+def test_generate_batch_per_utterance_equals_oracle(hip_device):
+    """FastGenerator.generate_batch: three utterances with ragged prefixes,
+    decoded together (six rows: the skinny-GEMM path), sampled with top-k /
+    top-p / CFG from explicit per-utterance uniforms; each utterance's codes
+    and stop reason equal the float64 oracle's run of that utterance alone
+    (including retirement at its own EOS)."""
+    import torch
+    from soraku_amd import FastGenerator
+
+    f, s, gen = load_golden("tiny_sampled")
+    w = _weights(f, s)
+    w["depth_head.bias"] = w["depth_head.bias"].copy()
+    w["depth_head.bias"][0, s.eos_id] += 0.2      # the utterances retire at frames 4, 12 and never (oracle)
+    lang = tuple(int(v) for v in f["language_ids"])
+    n_frames = 14
+    kw = {k: v for k, v in gen.items() if k not in ("seed", "max_new_frames")}
+    rng = np.random.default_rng(23)
+    reqs, us = [], []
+    for i in range(3):
+        nt = 4 + 5 * i
+        reqs.append(dict(input_ids=torch.tensor(rng.integers(0, s.text_vocab, nt)[None]),
+                         prompt_codes=torch.tensor(rng.integers(0, s.codebook_size, (i, s.n_codebooks))),
+                         uncond_input_ids=torch.tensor(f["uncond_ids"][None])))
+        us.append(rng.random((n_frames, s.n_codebooks)))
+    g = FastGenerator(device=hip_device, state_dict=w, shape=_shape(s), language_token_ids=lang)
+    out = g.generate_batch(reqs, max_new_frames=n_frames, uniforms=np.stack(us), **kw)
+    m = OracleModel(s, w, np.float64, language_token_ids=lang)
+    for r, u, (codes, info) in zip(reqs, us, out):
+        ref, rinfo = generate(m, input_ids=r["input_ids"].numpy()[0], prompt_codes=r["prompt_codes"].numpy(),
+                              uncond_input_ids=r["uncond_input_ids"].numpy()[0], uniforms=u, batched=True,
+                              max_new_frames=n_frames, **kw)
+        np.testing.assert_array_equal(codes.numpy(), ref)
+        assert info["stop_reason"] == rinfo["stop_reason"]
+    print("stop reasons", [o[1]["stop_reason"] for o in out], "frames", [o[1]["num_frames"] for o in out])
+    assert sorted(o[1]["stop_reason"] for o in out) == ["eos", "eos", "max_frames"]

@@ -87,7 +87,9 @@ int sk_destroy(sk_engine* e);
  *       trunk.layers.{i}.mlp.{gate,up,down}_proj.weight, trunk.norm.weight,
  *       trunk.embed_tokens.weight, audio_codebooks.table,
  *       depth_head.norm_in.weight, depth_head.mlp.{gate,up,down}_proj.weight,
- *       depth_head.norm_out.weight, depth_head.bias, language_embeddings.weight */
+ *       depth_head.norm_out.weight, depth_head.bias, language_embeddings.weight,
+ *       and depth_head.out_proj [Q][V][d] for an untied classifier (model.py:141-145;
+ *       when it is not bound the classifier is the tied audio_codebooks.table). */
 int sk_bind_weight(sk_engine* e, const char* key, const void* dev_ptr, int32_t dtype,
                    const int64_t* shape, int32_t ndim);
 

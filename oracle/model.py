@@ -42,6 +42,7 @@ class Shape:
     trunk_eps: float = 1e-6
     rope_theta: float = 1e6
     n_language: int = 0
+    tie_audio_head: bool = True
 
     @property
     def audio_vocab(self) -> int:  # model.py:61-63
@@ -99,6 +100,8 @@ def weight_shapes(s: Shape) -> dict[str, tuple[int, ...]]:
     out["depth_head.mlp.down_proj.weight"] = (s.d_model, s.depth_inner)
     out["depth_head.norm_out.weight"] = (s.d_model,)
     out["depth_head.bias"] = (s.n_codebooks, s.audio_vocab)
+    if not s.tie_audio_head:                     # model.py:141-145
+        out["depth_head.out_proj"] = (s.n_codebooks, s.audio_vocab, s.d_model)
     if s.n_language:
         out["language_embeddings.weight"] = (s.n_language, s.d_model)
     return out
@@ -338,14 +341,17 @@ class OracleModel:
     def depth_logits(self, hidden, prefix, q: int) -> np.ndarray:
         """``DepthHead.step``: ``a = norm_in(h + prefix)``,
         ``body = norm_out(a + mlp(a))``, ``logits = body @ table[q].T + bias[q]``
-        (model.py:147-149,163-174; eps = FLT_EPSILON, fast_generate.py:71-78)."""
+        (model.py:147-149,163-174; eps = FLT_EPSILON, fast_generate.py:71-78);
+        an untied head uses ``depth_head.out_proj[q]`` instead of the table
+        (model.py:171-174)."""
         w = self.w
         a = rms_norm(hidden + prefix, w["depth_head.norm_in.weight"], FLT_EPS)
         g = a @ w["depth_head.mlp.gate_proj.weight"].T
         u = a @ w["depth_head.mlp.up_proj.weight"].T
         y = a + (silu(g) * u) @ w["depth_head.mlp.down_proj.weight"].T
         body = rms_norm(y, w["depth_head.norm_out.weight"], FLT_EPS)
-        return body @ w["audio_codebooks.table"][q].T + w["depth_head.bias"][q]
+        head = w["audio_codebooks.table"] if self.s.tie_audio_head else w["depth_head.out_proj"]
+        return body @ head[q].T + w["depth_head.bias"][q]
 
     def prefix_step(self, q: int, code: int) -> np.ndarray:
         """``embedding(code, table[q]) * scale`` (model.py:600-603)."""

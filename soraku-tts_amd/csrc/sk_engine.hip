@@ -57,6 +57,7 @@ struct sk_engine {
   const float* final_norm = nullptr;
   const void* embed_tokens = nullptr;
   const void* table = nullptr;
+  const void* out_proj = nullptr;   // untied classifier [Q][V][d]; the table when null
   const float *d_norm_in = nullptr, *d_norm_out = nullptr, *d_bias = nullptr, *lang = nullptr;
   const void *d_gate = nullptr, *d_up = nullptr, *d_down = nullptr;
 
@@ -292,7 +293,7 @@ hipError_t enqueue_depth_wide(sk_engine* e, int q) {
   k = skinny_args(e->d_down, d, c.depth_inner, e->act, e->inner_max, e->ybuf, d, M);
   k.res = e->abuf; k.ldr = d;
   if ((err = launch_skinny<EPI_RESID>(wt, k, e->stream)) != hipSuccess) return err;
-  const void* tq = static_cast<const char*>(e->table) + (size_t)q * V * d * tsz;
+  const void* tq = static_cast<const char*>(e->out_proj ? e->out_proj : e->table) + (size_t)q * V * d * tsz;
   k = skinny_args(tq, V, d, e->ybuf, d, e->logits, V, M);
   k.bias = e->d_bias + (size_t)q * V; k.norm_w = e->d_norm_out; k.eps = c.depth_eps;
   return launch_skinny<EPI_BIAS, true>(wt, k, e->stream);
@@ -342,7 +343,7 @@ hipError_t enqueue_frame(sk_engine* e) {
     a.res = e->abuf; a.ldr = d;
     if ((err = launch_gemv<PRO_NONE, EPI_RESID>(wt, M, a, e->stream)) != hipSuccess) return err;
 
-    const void* tq = static_cast<const char*>(e->table) + (size_t)q * V * d * tsz;
+    const void* tq = static_cast<const char*>(e->out_proj ? e->out_proj : e->table) + (size_t)q * V * d * tsz;
     a = gemv_args(tq, V, d, e->ybuf, d, e->logits, V);
     a.norm_w = e->d_norm_out; a.eps = c.depth_eps; a.bias = e->d_bias + (size_t)q * V;
     if ((err = launch_gemv<PRO_NORM, EPI_BIAS>(wt, M, a, e->stream)) != hipSuccess) return err;
@@ -660,6 +661,7 @@ int sk_bind_weight(sk_engine* e, const char* key, const void* dev_ptr, int32_t d
     if (k == "trunk.norm.weight") { if (!(rc = want({d}, SK_F32))) e->final_norm = (const float*)dev_ptr; }
     else if (k == "trunk.embed_tokens.weight") { if (!(rc = want({c.text_vocab, d}, wt))) e->embed_tokens = dev_ptr; }
     else if (k == "audio_codebooks.table") { if (!(rc = want({c.n_codebooks, c.audio_vocab, d}, wt))) e->table = dev_ptr; }
+    else if (k == "depth_head.out_proj") { if (!(rc = want({c.n_codebooks, c.audio_vocab, d}, wt))) e->out_proj = dev_ptr; }
     else if (k == "depth_head.norm_in.weight") { if (!(rc = want({d}, SK_F32))) e->d_norm_in = (const float*)dev_ptr; }
     else if (k == "depth_head.norm_out.weight") { if (!(rc = want({d}, SK_F32))) e->d_norm_out = (const float*)dev_ptr; }
     else if (k == "depth_head.mlp.gate_proj.weight") { if (!(rc = want({c.depth_inner, d}, wt))) e->d_gate = dev_ptr; }

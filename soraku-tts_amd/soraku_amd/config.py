@@ -31,6 +31,7 @@ class DecodeShape:
     trunk_eps: float = 1e-6
     rope_theta: float = 1e6
     n_language: int = 0
+    tie_audio_head: bool = True
 
     @property
     def audio_vocab(self) -> int:  # model.py:61-63

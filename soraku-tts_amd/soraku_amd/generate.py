@@ -44,6 +44,16 @@ class FastGenerator:
         self._engine: GraphFrameEngine | None = None
         self._engine_key = None
 
+    @classmethod
+    def from_pretrained(cls, model_dir, *, device="cuda:0", bf16: bool = False, kv_bf16: bool = False):
+        """A generator over a release directory (runtime.py:14-44 layout):
+        config gate, decode shape and tensors from ``load_release``."""
+        from .checkpoint import load_release
+
+        rel = load_release(model_dir, bf16=bf16)
+        return cls(device=device, state_dict=rel.state_dict, shape=rel.shape,
+                   language_token_ids=rel.language_token_ids, bf16=bf16, kv_bf16=kv_bf16)
+
     def _engine_for(self, max_len: int, batch: int, cfg_scale: float, n_utts: int = 1) -> GraphFrameEngine:
         key = (batch, n_utts)
         e = self._engine

@@ -41,6 +41,8 @@ def weight_shapes(s: DecodeShape) -> dict[str, tuple[int, ...]]:
     out["depth_head.mlp.down_proj.weight"] = (s.d_model, s.depth_inner)
     out["depth_head.norm_out.weight"] = (s.d_model,)
     out["depth_head.bias"] = (s.n_codebooks, s.audio_vocab)
+    if not getattr(s, "tie_audio_head", True):   # model.py:141-145
+        out["depth_head.out_proj"] = (s.n_codebooks, s.audio_vocab, s.d_model)
     if s.n_language:
         out["language_embeddings.weight"] = (s.n_language, s.d_model)
     return out

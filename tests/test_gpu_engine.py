@@ -523,3 +523,32 @@ def test_generate_batch_per_utterance_equals_oracle(hip_device):
         assert info["stop_reason"] == rinfo["stop_reason"]
     print("stop reasons", [o[1]["stop_reason"] for o in out], "frames", [o[1]["num_frames"] for o in out])
     assert sorted(o[1]["stop_reason"] for o in out) == ["eos", "eos", "max_frames"]
+
+
+def test_from_pretrained_release_untied_head(hip_device, tmp_path):
+    """A release directory (config gate, text config, model.safetensors) with
+    an untied classifier head and four language tokens, loaded by
+    FastGenerator.from_pretrained: greedy CFG codes equal the float64
+    oracle's on the same tensors; the text includes language-token ids."""
+    import dataclasses
+
+    import torch
+    from oracle.model import TINY
+    from soraku_amd import FastGenerator
+    from test_checkpoint import write_release
+
+    s = dataclasses.replace(TINY, tie_audio_head=False, n_language=4)
+    w = synthetic_weights(s, 7, norm_gain_std=0.1, bias_std=0.02)
+    lang = (90, 91, 92, 93)
+    write_release(tmp_path, s, w, soraku_extra=dict(language_token_ids=list(lang)))
+    rng = np.random.default_rng(2)
+    text = np.concatenate([[91], rng.integers(0, 80, 9)])
+    prompt = rng.integers(0, s.codebook_size, (2, s.n_codebooks))
+    kw = dict(max_new_frames=10, min_new_frames=2, temperature=0.0, cfg_scale=1.5)
+    g = FastGenerator.from_pretrained(tmp_path, device=hip_device)
+    codes, info = g.generate(input_ids=torch.tensor(text[None]), prompt_codes=torch.tensor(prompt),
+                             uncond_input_ids=torch.tensor([[3]]), **kw)
+    ref, rinfo = generate(OracleModel(s, w, np.float64, language_token_ids=lang), input_ids=text,
+                          prompt_codes=prompt, uncond_input_ids=np.array([3]), batched=True, **kw)
+    np.testing.assert_array_equal(codes.numpy(), ref)
+    assert info["stop_reason"] == rinfo["stop_reason"]

@@ -730,6 +730,31 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   }
 }
 
+// One block of up to MERGE_CB chunks [c0, c0 + MERGE_CB) of one (row, q head,
+// dim): the running (M, L, O) are rescaled to the block's max, then the
+// block's chunks are added in chunk order.  Both merge forms use it, so they
+// round identically.
+constexpr int MERGE_CB = 16;
+__device__ __forceinline__ void merge_block(const float (&mv)[MERGE_CB], const float (&lv)[MERGE_CB],
+                                            const float (&ov)[MERGE_CB], int c0, int nch, float& M, float& L,
+                                            float& O) {
+  float Mb = M;
+#pragma unroll
+  for (int j = 0; j < MERGE_CB; ++j)
+    if (c0 + j < nch) Mb = fmaxf(Mb, mv[j]);
+  const float rescale = expf(M - Mb);   // 0 on the first block (M = -inf)
+  L *= rescale;
+  O *= rescale;
+#pragma unroll
+  for (int j = 0; j < MERGE_CB; ++j)
+    if (c0 + j < nch) {
+      const float f = expf(mv[j] - Mb);
+      L = fmaf(lv[j], f, L);
+      O = fmaf(ov[j], f, O);
+    }
+  M = Mb;
+}
+
 // Merge the chunk partials of one (row, q head) in chunk order: one thread
 // per head dim.  The partials of up to 16 chunks are loaded together with
 // kv_len (speculatively, in bounds) and masked once the chunk count is known.
@@ -739,7 +764,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   const int hd = a.hd, stride = hd + 2;
   const int dd = min(d, hd - 1);         // lanes past hd mirror the last dim, no branch
   const float* pp = a.part + ((size_t)r * a.Hq + hq) * a.max_chunks * stride;
-  constexpr int CB = 16;
+  constexpr int CB = MERGE_CB;
   float mv[CB], lv[CB], ov[CB];
   auto load_block = [&](int c0) {
 #pragma unroll
@@ -758,21 +783,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   float M = -INFINITY, L = 0.f, O = 0.f;
   for (int c0 = 0; c0 < nch; c0 += CB) {
     if (c0 > 0) load_block(c0);
-    float Mb = M;
-#pragma unroll
-    for (int j = 0; j < CB; ++j)
-      if (c0 + j < nch) Mb = fmaxf(Mb, mv[j]);
-    const float rescale = expf(M - Mb);   // 0 on the first block (M = -inf)
-    L *= rescale;
-    O *= rescale;
-#pragma unroll
-    for (int j = 0; j < CB; ++j)
-      if (c0 + j < nch) {
-        const float f = expf(mv[j] - Mb);
-        L = fmaf(lv[j], f, L);
-        O = fmaf(ov[j], f, O);
-      }
-    M = Mb;
+    merge_block(mv, lv, ov, c0, nch, M, L, O);
   }
   if (act && d < hd) a.out[(size_t)r * a.ldo + (size_t)hq * hd + d] = O / L;
 }

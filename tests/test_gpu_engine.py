@@ -552,3 +552,4 @@ def test_from_pretrained_release_untied_head(hip_device, tmp_path):
                           prompt_codes=prompt, uncond_input_ids=np.array([3]), batched=True, **kw)
     np.testing.assert_array_equal(codes.numpy(), ref)
     assert info["stop_reason"] == rinfo["stop_reason"]
+

@@ -90,7 +90,7 @@ struct sk_engine {
   int pf_cap = 0;
   float *pX = nullptr, *pXn = nullptr, *pQKV = nullptr, *pQ = nullptr, *pATT = nullptr, *pACT = nullptr;
   int *p_tok_row = nullptr, *p_tok_pos = nullptr, *p_row_start = nullptr;
-  float2* p_rope = nullptr;   // [max_ctx][hd/2] (cos, sin) by position
+  float2* p_rope = nullptr;   // [max_ctx + 1][hd/2] (cos, sin) by position, filled at creation
 };
 
 namespace {
@@ -356,7 +356,7 @@ hipError_t enqueue_frame(sk_engine* e) {
   hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x, e->final_norm,
                      c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->fc, e->u_ring,
                      e->flag_ring, e->u_cur, e->flag_cur, c.n_utts * c.n_codebooks, c.max_frames,
-                     e->inv_freq, c.head_dim / 2, e->rope);
+                     e->inv_freq, c.head_dim / 2, e->rope, (const float2*)e->p_rope, c.max_ctx + 1);
   return hipGetLastError();
 }
 
@@ -419,7 +419,6 @@ hipError_t enqueue_batched_prefill(sk_engine* e, int M, int max_len) {
   const bool bf = c.kv_dtype == SK_BF16;
   hipStream_t st = e->stream;
   hipError_t err;
-  hipLaunchKernelGGL(pf_rope_table_kernel, dim3(max_len), dim3(NT), 0, st, e->inv_freq, hd / 2, e->p_rope);
   hipLaunchKernelGGL(pf_gather_kernel, dim3(M), dim3(NT), 0, st, e->embeds, c.max_ctx, e->p_tok_row,
                      e->p_tok_pos, d, e->pX);
   if ((err = hipGetLastError()) != hipSuccess) return err;
@@ -561,7 +560,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   ALLOC(e->part, R * c.n_q_heads * e->max_chunks * (c.head_dim + 2));
   ALLOC(e->kv_len, R); ALLOC(e->pos, R); ALLOC(e->active, R); ALLOC(e->plen, R);
   ALLOC(e->fc, 1);
-  ALLOC(e->p_rope, (size_t)c.max_ctx * (c.head_dim / 2));
+  ALLOC(e->p_rope, (size_t)(c.max_ctx + 1) * (c.head_dim / 2));
   ALLOC(e->p_row_start, R);
   ALLOC(e->u_ring, (size_t)c.max_frames * c.n_utts * Q);
   ALLOC(e->flag_ring, (size_t)c.max_frames * 2);
@@ -591,6 +590,12 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   e->p_host.cfg_scale = 1.0f;
   e->p_host.temperature = 0.0f;
   if (he == hipSuccess) he = hipMemcpy(e->params, &e->p_host, sizeof(SkParams), hipMemcpyHostToDevice);
+  if (he == hipSuccess) {
+    hipLaunchKernelGGL(pf_rope_table_kernel, dim3(c.max_ctx + 1), dim3(NT), 0, e->stream, e->inv_freq,
+                       c.head_dim / 2, e->p_rope);
+    he = hipGetLastError();
+    if (he == hipSuccess) he = hipStreamSynchronize(e->stream);
+  }
   if (he == hipSuccess) he = prepare_sampler();
   if (he == hipSuccess)
     he = hipFuncSetAttribute(c.kv_dtype == SK_BF16 ? reinterpret_cast<const void*>(attention_kernel<uint16_t>)

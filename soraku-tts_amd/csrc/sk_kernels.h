@@ -1427,8 +1427,8 @@ __global__ __launch_bounds__(NT) void rope_rows_kernel(const int* pos, const flo
 }
 
 // Final trunk norm + per-row step bookkeeping after a decode trunk step: every
-// active row advances its length and position (and the RoPE table of the new
-// position), the frame counter moves on and the next frame's draws and flags
+// active row advances its length and position (and its RoPE (cos, sin) to the
+// new position), the frame counter moves on and the next frame's draws and flags
 // are copied from the ring to the fixed current-frame slots.
 __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const float* w, float eps,
                                                         int D, float* hidden, int* kv_len, int* pos,
@@ -1436,7 +1436,7 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
                                                         const double* u_ring, const int* flag_ring,
                                                         double* u_cur, int* flag_cur, int nq,
                                                         int max_frames, const float* inv_freq, int half,
-                                                        float2* rope) {
+                                                        float2* rope, const float2* rope_tab, int tab_n) {
   __shared__ float red[WAVES];
   const int b = blockIdx.x;
   const int p0 = pos[b];                 // read by every thread before the barrier in block_sum
@@ -1468,7 +1468,11 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
       for (int k = threadIdx.x; k < D; k += NT) hidden[(size_t)b * D + k] = w[k] * (xr[k] * inv);
     }
     if (threadIdx.x == 0) { kv_len[b] += 1; pos[b] = p0 + 1; }
-    for (int t = threadIdx.x; t < half; t += NT) rope[(size_t)b * half + t] = rope_cs(p0 + 1, inv_freq[t]);
+    // (cos, sin) of the new position: from the per-position table (one load),
+    // computed only for positions past it
+    const int np = p0 + 1;
+    for (int t = threadIdx.x; t < half; t += NT)
+      rope[(size_t)b * half + t] = np < tab_n ? rope_tab[(size_t)np * half + t] : rope_cs(np, inv_freq[t]);
   }
   if (b == 0) {
     const int next = *counter + 1;

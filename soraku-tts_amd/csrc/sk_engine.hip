@@ -18,6 +18,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -69,6 +70,8 @@ struct sk_engine {
   float *inv_freq = nullptr;
   float *part = nullptr, *dbg = nullptr, *embeds = nullptr;
   float2* rope = nullptr;     // [rows][hd/2] (cos, sin) at each row's position
+  float* sk_partial = nullptr;  // many-row path: split-K slice partials
+  unsigned* sk_arrive = nullptr;
   int *kv_len = nullptr, *pos = nullptr, *active = nullptr, *plen = nullptr;
   int *fc = nullptr, *flag_ring = nullptr, *flag_cur = nullptr;
   double *u_ring = nullptr, *u_cur = nullptr;
@@ -186,9 +189,27 @@ hipError_t launch_skinny_w(const SkinnyArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WL, 8, NORM>), grid, dim3(8 * 64), 0, st, a);
   return hipGetLastError();
 }
+// BF16 weights: K split over 4 or 2 workgroups per output tile when the
+// tiles alone would fill fewer than 256 CUs (tiles a multiple of 8, K slices
+// a multiple of 32); the slice partials live in `partial`, the arrival counts
+// in `arrive` (zero between launches).
+template <int EPI, bool NORM>
+hipError_t launch_skinny_bf16(SkinnyArgs a, float* partial, unsigned* arrive, hipStream_t st) {
+  const int tiles = (a.N + 15) / 16;
+  a.ksplit = 1;
+  if (tiles % 8 == 0) {
+    if (tiles <= 64 && a.K % (4 * 32) == 0) a.ksplit = 4;
+    else if (tiles <= 128 && a.K % (2 * 32) == 0) a.ksplit = 2;
+  }
+  a.partial = partial; a.arrive = arrive;
+  const dim3 grid(tiles * a.ksplit);
+  hipLaunchKernelGGL((skinny_bf16_kernel<EPI, 8, NORM>), grid, dim3(8 * 64), 0, st, a);
+  return hipGetLastError();
+}
 template <int EPI, bool NORM = false>
-hipError_t launch_skinny(int wdtype, const SkinnyArgs& a, hipStream_t st) {
-  return wdtype == SK_BF16 ? launch_skinny_w<EPI, NORM, WBF16>(a, st) : launch_skinny_w<EPI, NORM, WF32>(a, st);
+hipError_t launch_skinny(sk_engine* e, const SkinnyArgs& a) {
+  return e->c.weight_dtype == SK_BF16 ? launch_skinny_bf16<EPI, NORM>(a, e->sk_partial, e->sk_arrive, e->stream)
+                                      : launch_skinny_w<EPI, NORM, WF32>(a, e->stream);
 }
 
 SkinnyArgs skinny_args(const void* w, int N, int K, const float* x, int ldx, float* out, int ldo, int R) {
@@ -216,7 +237,7 @@ hipError_t enqueue_trunk(sk_engine* e) {
       k.w[1] = w.k; k.w[2] = w.v;
       k.seg_rows[0] = a.seg_rows[0]; k.seg_rows[1] = a.seg_rows[1]; k.seg_rows[2] = a.seg_rows[2];
       k.norm_w = w.in_norm; k.eps = c.trunk_eps;
-      if ((err = launch_skinny<EPI_STORE, true>(wt, k, e->stream)) != hipSuccess) return err;
+      if ((err = launch_skinny<EPI_STORE, true>(e, k)) != hipSuccess) return err;
     } else if ((err = launch_gemv<PRO_NORM, EPI_STORE>(wt, M, a, e->stream)) != hipSuccess) {
       return err;
     }
@@ -247,13 +268,13 @@ hipError_t enqueue_trunk(sk_engine* e) {
       const int hq = c.n_q_heads * hd, I = c.trunk_inter;
       SkinnyArgs k = skinny_args(w.o, d, hq, e->attn, hq, e->x, d, M);
       k.res = e->x; k.ldr = d;
-      if ((err = launch_skinny<EPI_RESID>(wt, k, e->stream)) != hipSuccess) return err;
+      if ((err = launch_skinny<EPI_RESID>(e, k)) != hipSuccess) return err;
       k = skinny_args(w.gate, I, d, e->x, d, e->act, e->inner_max, M);
       k.w2 = w.up; k.norm_w = w.post_norm; k.eps = c.trunk_eps;
-      if ((err = launch_skinny<EPI_SWIGLU, true>(wt, k, e->stream)) != hipSuccess) return err;
+      if ((err = launch_skinny<EPI_SWIGLU, true>(e, k)) != hipSuccess) return err;
       k = skinny_args(w.down, d, I, e->act, e->inner_max, e->x, d, M);
       k.res = e->x; k.ldr = d;
-      if ((err = launch_skinny<EPI_RESID>(wt, k, e->stream)) != hipSuccess) return err;
+      if ((err = launch_skinny<EPI_RESID>(e, k)) != hipSuccess) return err;
       continue;
     }
     a = gemv_args(w.o, d, c.n_q_heads * hd, e->attn, c.n_q_heads * hd, e->x, d);
@@ -289,14 +310,14 @@ hipError_t enqueue_depth_wide(sk_engine* e, int q) {
   if ((err = hipGetLastError()) != hipSuccess) return err;
   SkinnyArgs k = skinny_args(e->d_gate, c.depth_inner, d, e->abuf, d, e->act, e->inner_max, M);
   k.w2 = e->d_up;
-  if ((err = launch_skinny<EPI_SWIGLU>(wt, k, e->stream)) != hipSuccess) return err;
+  if ((err = launch_skinny<EPI_SWIGLU>(e, k)) != hipSuccess) return err;
   k = skinny_args(e->d_down, d, c.depth_inner, e->act, e->inner_max, e->ybuf, d, M);
   k.res = e->abuf; k.ldr = d;
-  if ((err = launch_skinny<EPI_RESID>(wt, k, e->stream)) != hipSuccess) return err;
+  if ((err = launch_skinny<EPI_RESID>(e, k)) != hipSuccess) return err;
   const void* tq = static_cast<const char*>(e->out_proj ? e->out_proj : e->table) + (size_t)q * V * d * tsz;
   k = skinny_args(tq, V, d, e->ybuf, d, e->logits, V, M);
   k.bias = e->d_bias + (size_t)q * V; k.norm_w = e->d_norm_out; k.eps = c.depth_eps;
-  return launch_skinny<EPI_BIAS, true>(wt, k, e->stream);
+  return launch_skinny<EPI_BIAS, true>(e, k);
 }
 
 hipError_t enqueue_frame(sk_engine* e) {
@@ -557,6 +578,12 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   ALLOC(e->vc, (size_t)c.n_layers * kv_layer_bytes(e));
   ALLOC(e->inv_freq, (size_t)c.head_dim / 2);
   ALLOC(e->rope, R * (size_t)c.head_dim / 2);
+  {
+    const size_t nmax = std::max({(size_t)e->nqkv, (size_t)c.trunk_inter, (size_t)c.depth_inner,
+                                  (size_t)c.audio_vocab, (size_t)c.d_model});
+    ALLOC(e->sk_partial, (nmax / 16 + 1) * 4 * SK_PSZ);
+    ALLOC(e->sk_arrive, nmax / 16 + 1);
+  }
   ALLOC(e->part, R * c.n_q_heads * e->max_chunks * (c.head_dim + 2));
   ALLOC(e->kv_len, R); ALLOC(e->pos, R); ALLOC(e->active, R); ALLOC(e->plen, R);
   ALLOC(e->fc, 1);
@@ -583,6 +610,10 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   if (he == hipSuccess) he = hipMemset(e->prefix, 0, R * d * sizeof(float));
   if (he == hipSuccess) he = hipMemset(e->prefix2, 0, R * d * sizeof(float));
   if (he == hipSuccess) he = hipMemset(e->kv_len, 0, R * sizeof(int));
+  if (he == hipSuccess)
+    he = hipMemset(e->sk_arrive, 0,
+                   (std::max({(size_t)e->nqkv, (size_t)c.trunk_inter, (size_t)c.depth_inner, (size_t)c.audio_vocab,
+                              (size_t)c.d_model}) / 16 + 1) * sizeof(unsigned));
   if (he == hipSuccess) he = hipMemset(e->pos, 0, R * sizeof(int));
   if (he == hipSuccess) he = hipMemset(e->fc, 0, sizeof(int));
   if (he == hipSuccess) he = hipMemset(e->flag_ring, 0, (size_t)c.max_frames * 2 * sizeof(int));
@@ -611,7 +642,7 @@ int sk_destroy(sk_engine* e) {
   if (!e) return SK_OK;
   if (e->stream) hipStreamSynchronize(e->stream);
   drop_graphs(e);
-  void* bufs[] = {e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
+  void* bufs[] = {e->sk_partial, e->sk_arrive, e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
                   e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->flag_ring, e->u_ring,
                   e->pX, e->pXn, e->pQKV, e->pQ, e->pATT, e->pACT, e->p_tok_row, e->p_tok_pos,

@@ -23,7 +23,14 @@ struct SkinnyArgs {
   const float* res; int ldr;           // residual (may alias out)
   const float* bias;                   // [N]
   int R, N, K;
+  int ksplit;                          // K slices per output tile (1, 2 or 4; BF16 form)
+  float* partial;                      // [tiles][ksplit][SK_PSZ] slice partials (ksplit > 1)
+  unsigned* arrive;                    // [tiles] slice arrival counts, zero between launches
 };
+
+// Floats per slice partial: two epilogue values per thread (SwiGLU) + 32 row
+// sums of squares.
+constexpr int SK_PSZ = 2 * 512 + 32;
 
 constexpr int SK_ROWS = 32;             // rows covered (two 16-row MFMA tiles)
 
@@ -135,6 +142,179 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(SkinnyArgs a) {
     for (int w = 0; w < W; ++w)
 #pragma unroll
       for (int k4 = 0; k4 < 4; ++k4) ss += ssq[w][t][k4 * 16 + (l & 15)];
+    const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+#pragma unroll
+    for (int n = 0; n < NA; ++n) c[n] *= inv;
+  }
+  if (oo < a.N && r < a.R) {
+    float y = c[0];
+    if constexpr (EPI == EPI_BIAS) y = y + a.bias[oo];
+    if constexpr (EPI == EPI_RESID) y = a.res[(size_t)r * a.ldr + oo] + y;
+    if constexpr (EPI == EPI_SWIGLU) y = y / (1.0f + expf(-y)) * c[NA - 1];
+    a.out[(size_t)r * a.ldo + oo] = y;
+  }
+}
+
+// BF16 weights: the same GEMM on the BF16 matrix cores
+// (v_mfma_f32_16x16x32_bf16).  A lane's 8 consecutive BF16 weights are the A
+// fragment as loaded; each x value (times the norm gain) is split into x_hi =
+// bf16(x) and x_lo = bf16(x - x_hi), and both halves go through the MFMA, so
+// the products are exact in FP32 and x keeps ~16 mantissa bits (relative
+// error <= 2^-16).  Sums in FP32 as in the FP32 form.
+typedef __bf16 sbf8 __attribute__((ext_vector_type(8)));
+
+//
+// Split K (ksplit S > 1, for outputs too few to fill the GPU): the S slices of
+// an output tile are workgroups tile % 8 + 8 (S (tile / 8) + s), so all run on
+// XCD tile % 8 (workgroups are dispatched to the 8 XCDs round-robin) and share
+// its L2.  Each slice stores its partial tile, waits until the stores are
+// acknowledged, and counts itself in arrive[tile] (an L2 atomic); the last
+// slice to arrive adds the S partials in slice order, applies the epilogue and
+// resets the count.  No workgroup waits for another.
+template <int EPI, int W, bool NORM>
+__global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
+  constexpr int NA = (EPI == EPI_SWIGLU) ? 2 : 1;
+  constexpr int BK = 32;                // k per block: 8 per lane
+  __shared__ float red[W][NA * 2 * 4][64];
+  __shared__ float ssq[NORM ? W : 1][2][64];
+  __shared__ int last_slice;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i16 = lane & 15, kq = lane >> 4;
+  const int S = a.ksplit;
+  int tile = blockIdx.x, slice = 0;
+  if (S > 1) {
+    const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
+    slice = q % S;
+    tile = (q / S) * 8 + xcd;
+  }
+  const int kbeg = slice * (a.K / S), kend = kbeg + a.K / S;
+  const int o0 = tile * 16;
+  const int o = min(o0 + i16, a.N - 1);
+  const void* wb;
+  int wr;
+  if (o < a.seg_rows[0]) { wb = a.w[0]; wr = o; }
+  else if (o < a.seg_rows[0] + a.seg_rows[1]) { wb = a.w[1]; wr = o - a.seg_rows[0]; }
+  else { wb = a.w[2]; wr = o - a.seg_rows[0] - a.seg_rows[1]; }
+  const uint16_t* wp = static_cast<const uint16_t*>(wb) + (size_t)wr * a.K + 8 * kq;
+  const uint16_t* w2p = NA == 2 ? static_cast<const uint16_t*>(a.w2) + (size_t)o * a.K + 8 * kq : nullptr;
+  const float* xr0 = a.x + (size_t)min(i16, a.R - 1) * a.ldx + 8 * kq;
+  const float* xr1 = a.x + (size_t)min(16 + i16, a.R - 1) * a.ldx + 8 * kq;
+  const float* gp = NORM ? a.norm_w + 8 * kq : nullptr;
+  struct Stage { uint4 w[NA]; float4 x0[2], x1[2], g[NORM ? 2 : 1]; };
+  auto load = [&](int kb, Stage& st) {
+    st.w[0] = *reinterpret_cast<const uint4*>(wp + kb);
+    if constexpr (NA == 2) st.w[NA - 1] = *reinterpret_cast<const uint4*>(w2p + kb);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      st.x0[h] = *reinterpret_cast<const float4*>(xr0 + kb + 4 * h);
+      st.x1[h] = *reinterpret_cast<const float4*>(xr1 + kb + 4 * h);
+      if constexpr (NORM) st.g[h] = *reinterpret_cast<const float4*>(gp + kb + 4 * h);
+    }
+  };
+  sv4f acc[NA][2];
+#pragma unroll
+  for (int n = 0; n < NA; ++n) acc[n][0] = acc[n][1] = sv4f{0.f, 0.f, 0.f, 0.f};
+  float ss0 = 0.f, ss1 = 0.f;
+  auto split = [&](const float4 (&xv)[2], const float4 (&gv)[NORM ? 2 : 1], float& ss, sbf8& hi, sbf8& lo) {
+    const float v[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float x = v[j];
+      if constexpr (NORM) {
+        const float g[8] = {gv[0].x, gv[0].y, gv[0].z, gv[0].w, gv[NORM ? 1 : 0].x, gv[NORM ? 1 : 0].y,
+                            gv[NORM ? 1 : 0].z, gv[NORM ? 1 : 0].w};
+        ss = fmaf(x, x, ss);
+        x *= g[j];
+      }
+      const __bf16 h = (__bf16)x;
+      hi[j] = h;
+      lo[j] = (__bf16)(x - (float)h);
+    }
+  };
+  auto comp = [&](const Stage& st) {
+    sbf8 h0, l0, h1, l1;
+    split(st.x0, st.g, ss0, h0, l0);
+    split(st.x1, st.g, ss1, h1, l1);
+#pragma unroll
+    for (int n = 0; n < NA; ++n) {
+      const sbf8 wa = __builtin_bit_cast(sbf8, st.w[n]);
+      acc[n][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, h0, acc[n][0], 0, 0, 0);
+      acc[n][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, l0, acc[n][0], 0, 0, 0);
+      acc[n][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, h1, acc[n][1], 0, 0, 0);
+      acc[n][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, l1, acc[n][1], 0, 0, 0);
+    }
+  };
+  Stage sa, sb;
+  constexpr int STEP = W * BK;
+  int kb = kbeg + wave * BK;
+  if (kb < kend) load(kb, sa);
+  for (; kb < kend; kb += 2 * STEP) {
+    const int k1 = kb + STEP, k2 = k1 + STEP;
+    if (k1 < kend) load(k1, sb);
+    comp(sa);
+    if (k1 < kend) {
+      if (k2 < kend) load(k2, sa);
+      comp(sb);
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < NA; ++n)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][(n * 2 + t) * 4 + v][lane] = acc[n][t][v];
+  if constexpr (NORM) { ssq[wave][0][lane] = ss0; ssq[wave][1][lane] = ss1; }
+  __syncthreads();
+  // Threads 0..511 own one (row tile, v, lane) each; with 16 waves the upper
+  // half only takes part in the barriers.
+  const bool et = tid < 512;
+  const int t = (tid >> 8) & 1, v = (tid >> 6) & 3, l = tid & 63;
+  const int oo = o0 + 4 * (l >> 4) + v, r = 16 * t + (l & 15);
+  float c[NA];
+#pragma unroll
+  for (int n = 0; n < NA; ++n) {
+    float sacc = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) sacc += red[w][(n * 2 + t) * 4 + v][l];
+    c[n] = sacc;
+  }
+  float ss = 0.f;
+  if constexpr (NORM) {
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4) ss += ssq[w][t][k4 * 16 + (l & 15)];
+  }
+  if (S > 1) {
+    float* mine = a.partial + ((size_t)tile * S + slice) * SK_PSZ;
+    if (et) {
+#pragma unroll
+      for (int n = 0; n < NA; ++n) mine[n * 512 + tid] = c[n];
+      if (NORM && v == 0 && (l >> 4) == 0) mine[2 * 512 + r] = ss;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's partials are in L2
+    __syncthreads();
+    if (tid == 0)
+      last_slice = __hip_atomic_fetch_add(a.arrive + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) + 1u ==
+                   (unsigned)S;
+    __syncthreads();
+    if (!last_slice) return;
+    if (tid == 0) __hip_atomic_store(a.arrive + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (!et) return;
+    const float* all = a.partial + (size_t)tile * S * SK_PSZ;
+#pragma unroll
+    for (int n = 0; n < NA; ++n) {
+      float sacc = 0.f;
+      for (int q = 0; q < S; ++q) sacc += all[(size_t)q * SK_PSZ + n * 512 + tid];
+      c[n] = sacc;
+    }
+    if constexpr (NORM) {
+      ss = 0.f;
+      for (int q = 0; q < S; ++q) ss += all[(size_t)q * SK_PSZ + 2 * 512 + r];
+    }
+  }
+  if (!et) return;
+  if constexpr (NORM) {
     const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
 #pragma unroll
     for (int n = 0; n < NA; ++n) c[n] *= inv;

@@ -50,6 +50,7 @@ struct sk_engine {
   sk_config c{};
   int rows = 0, G = 0, nqkv = 0, inner_max = 0, max_chunks = 0;
   bool wide = false;          // more rows than the GEMV kernels take: skinny MFMA GEMMs
+  int attn_splits = 0;        // > 0: attention_stream_kernel with this many splits per (row, kv head)
   int device = 0;
   hipStream_t stream = nullptr;
 
@@ -72,6 +73,10 @@ struct sk_engine {
   float2* rope = nullptr;     // [rows][hd/2] (cos, sin) at each row's position
   float* sk_partial = nullptr;  // many-row path: split-K slice partials
   unsigned* sk_arrive = nullptr;
+  // Many-row path with BF16 weights: GEMM inputs in split form (written by
+  // their producers) and per-tile sums of squares for the RMSNorms.
+  uint16_t *xs_x = nullptr, *xs_attn = nullptr, *xs_act = nullptr, *xs_abuf = nullptr, *xs_y = nullptr;
+  float *ss_x = nullptr, *ss_y = nullptr;   // [32][d_model / 16]
   int *kv_len = nullptr, *pos = nullptr, *active = nullptr, *plen = nullptr;
   int *fc = nullptr, *flag_ring = nullptr, *flag_cur = nullptr;
   double *u_ring = nullptr, *u_cur = nullptr;
@@ -139,6 +144,8 @@ int validate_config(const sk_config* c) {
            "n_utts * cfg_rows must be in [1, %d] (decode rows)", SK_ROWS);
   SK_CHECK(c->n_utts * c->cfg_rows <= 4 || c->depth_inner % 32 == 0, SK_EINVAL,
            "depth_inner must be a multiple of 32 for more than 4 decode rows");
+  SK_CHECK(c->n_utts * c->cfg_rows <= 4 || c->weight_dtype != SK_BF16 || c->d_model <= 4096, SK_EINVAL,
+           "d_model must be at most 4096 for more than 4 decode rows with BF16 weights");
   SK_CHECK(c->max_ctx >= 2 && c->max_ctx <= 65536, SK_EINVAL, "max_ctx must be in [2, 65536]");
   SK_CHECK(c->max_frames >= 1, SK_EINVAL, "max_frames must be positive");
   SK_CHECK(c->n_language == 0 || c->n_language == 4, SK_EINVAL, "n_language must be 0 or 4");
@@ -203,7 +210,10 @@ hipError_t launch_skinny_bf16(SkinnyArgs a, float* partial, unsigned* arrive, hi
   }
   a.partial = partial; a.arrive = arrive;
   const dim3 grid(tiles * a.ksplit);
-  hipLaunchKernelGGL((skinny_bf16_kernel<EPI, 8, NORM>), grid, dim3(8 * 64), 0, st, a);
+  if (a.xs)
+    hipLaunchKernelGGL((skinny_bf16_kernel<EPI, 8, NORM, true>), grid, dim3(8 * 64), 0, st, a);
+  else
+    hipLaunchKernelGGL((skinny_bf16_kernel<EPI, 8, NORM, false>), grid, dim3(8 * 64), 0, st, a);
   return hipGetLastError();
 }
 template <int EPI, bool NORM = false>
@@ -219,6 +229,53 @@ SkinnyArgs skinny_args(const void* w, int N, int K, const float* x, int ldx, flo
   a.x = x; a.ldx = ldx; a.out = out; a.ldo = ldo;
   a.R = R; a.N = N; a.K = K;
   return a;
+}
+
+// Chunked decode attention: one workgroup per 32-token chunk of each (row,
+// kv head), merged by attention_combine_kernel.  Few rows: the chunks fill
+// the chip.
+hipError_t launch_attn_chunks(sk_engine* e, const AttnArgs& at) {
+  const size_t asmem = attn_smem_floats(e->G, at.hd) * sizeof(float);
+  const dim3 grid(e->max_chunks, at.Hkv, e->rows);
+  if (e->c.kv_dtype == SK_BF16)
+    hipLaunchKernelGGL(attention_kernel<uint16_t>, grid, dim3(NT), asmem, e->stream, at);
+  else
+    hipLaunchKernelGGL(attention_kernel<float>, grid, dim3(NT), asmem, e->stream, at);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(attention_combine_kernel, dim3(at.Hq, e->rows), dim3(NT), 0, e->stream, at);
+  return hipGetLastError();
+}
+
+// Streaming decode attention (many rows): attn_splits workgroups per (row,
+// kv head); with one split the kernel writes the output itself.
+constexpr int ATTN_STREAM_NTH = 512;
+constexpr int ATTN_STREAM_DEPTH = 2;   // tokens in flight per slot
+template <typename KT, int G>
+hipError_t launch_attn_stream_g(sk_engine* e, AttnArgs at) {
+  const int S = e->attn_splits;
+  at.nparts = S > 1 ? S : 0;
+  const size_t smem = attn_stream_smem_floats(G, at.hd, ATTN_STREAM_NTH) * sizeof(float);
+  // 4 query heads: one token in flight keeps the state in registers
+  constexpr int D = G >= 4 ? 1 : ATTN_STREAM_DEPTH;
+  hipLaunchKernelGGL((attention_stream_kernel<KT, G, ATTN_STREAM_NTH, D>), dim3(S, at.Hkv, e->rows),
+                     dim3(ATTN_STREAM_NTH), smem, e->stream, at, S);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || S == 1) return err;
+  hipLaunchKernelGGL(attention_combine_kernel, dim3(at.Hq, e->rows), dim3(NT), 0, e->stream, at);
+  return hipGetLastError();
+}
+template <typename KT>
+hipError_t launch_attn_stream_kt(sk_engine* e, const AttnArgs& at) {
+  switch (e->G) {
+    case 1: return launch_attn_stream_g<KT, 1>(e, at);
+    case 2: return launch_attn_stream_g<KT, 2>(e, at);
+    case 4: return launch_attn_stream_g<KT, 4>(e, at);
+    default: return hipErrorInvalidConfiguration;   // not selected at creation
+  }
+}
+hipError_t launch_attn_stream(sk_engine* e, const AttnArgs& at) {
+  return e->c.kv_dtype == SK_BF16 ? launch_attn_stream_kt<uint16_t>(e, at) : launch_attn_stream_kt<float>(e, at);
 }
 
 hipError_t enqueue_trunk(sk_engine* e) {
@@ -237,6 +294,7 @@ hipError_t enqueue_trunk(sk_engine* e) {
       k.w[1] = w.k; k.w[2] = w.v;
       k.seg_rows[0] = a.seg_rows[0]; k.seg_rows[1] = a.seg_rows[1]; k.seg_rows[2] = a.seg_rows[2];
       k.norm_w = w.in_norm; k.eps = c.trunk_eps;
+      if (e->xs_x && l > 0) { k.xs = e->xs_x; k.ss_in = e->ss_x; k.n_ss = d / 16; }   // from the last down
       if ((err = launch_skinny<EPI_STORE, true>(e, k)) != hipSuccess) return err;
     } else if ((err = launch_gemv<PRO_NORM, EPI_STORE>(wt, M, a, e->stream)) != hipSuccess) {
       return err;
@@ -253,27 +311,27 @@ hipError_t enqueue_trunk(sk_engine* e) {
     at.out = e->attn; at.ldo = c.n_q_heads * hd;
     at.Hq = c.n_q_heads; at.Hkv = c.n_kv_heads; at.hd = hd; at.max_ctx = c.max_ctx;
     at.scale = 1.0f / sqrtf((float)hd);
-    const size_t asmem = attn_smem_floats(e->G, hd) * sizeof(float);
-    if (c.kv_dtype == SK_BF16)
-      hipLaunchKernelGGL(attention_kernel<uint16_t>, dim3(e->max_chunks, c.n_kv_heads, M), dim3(NT), asmem,
-                         e->stream, at);
-    else
-      hipLaunchKernelGGL(attention_kernel<float>, dim3(e->max_chunks, c.n_kv_heads, M), dim3(NT), asmem,
-                       e->stream, at);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(c.n_q_heads, M), dim3(NT), 0, e->stream, at);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
+    at.xs_out = e->xs_attn;
+    if ((err = e->attn_splits > 0 ? launch_attn_stream(e, at) : launch_attn_chunks(e, at)) != hipSuccess)
+      return err;
 
     if (e->wide) {
       const int hq = c.n_q_heads * hd, I = c.trunk_inter;
+      const bool xs = e->xs_x != nullptr;
       SkinnyArgs k = skinny_args(w.o, d, hq, e->attn, hq, e->x, d, M);
       k.res = e->x; k.ldr = d;
+      if (xs) { k.xs = e->xs_attn; k.xs_out = e->xs_x; k.xs_gain = w.post_norm; k.ss_out = e->ss_x; }
       if ((err = launch_skinny<EPI_RESID>(e, k)) != hipSuccess) return err;
       k = skinny_args(w.gate, I, d, e->x, d, e->act, e->inner_max, M);
       k.w2 = w.up; k.norm_w = w.post_norm; k.eps = c.trunk_eps;
+      if (xs) { k.xs = e->xs_x; k.ss_in = e->ss_x; k.n_ss = d / 16; k.xs_out = e->xs_act; }
       if ((err = launch_skinny<EPI_SWIGLU, true>(e, k)) != hipSuccess) return err;
       k = skinny_args(w.down, d, I, e->act, e->inner_max, e->x, d, M);
       k.res = e->x; k.ldr = d;
+      if (xs) {
+        k.xs = e->xs_act;
+        if (l + 1 < c.n_layers) { k.xs_out = e->xs_x; k.xs_gain = e->L[l + 1].in_norm; k.ss_out = e->ss_x; }
+      }
       if ((err = launch_skinny<EPI_RESID>(e, k)) != hipSuccess) return err;
       continue;
     }
@@ -302,21 +360,25 @@ hipError_t enqueue_depth_wide(sk_engine* e, int q) {
   if (wt == SK_BF16)
     hipLaunchKernelGGL(depth_in_kernel<WBF16>, dim3(M), dim3(NT), 0, e->stream, e->hidden, e->prefix, e->table,
                        e->codes_cur, q, c.n_codebooks, V, d, c.frame_scale, c.cfg_rows, e->d_norm_in, c.depth_eps,
-                       e->abuf);
+                       e->abuf, e->xs_abuf);
   else
     hipLaunchKernelGGL(depth_in_kernel<WF32>, dim3(M), dim3(NT), 0, e->stream, e->hidden, e->prefix, e->table,
                        e->codes_cur, q, c.n_codebooks, V, d, c.frame_scale, c.cfg_rows, e->d_norm_in, c.depth_eps,
-                       e->abuf);
+                       e->abuf, e->xs_abuf);
   if ((err = hipGetLastError()) != hipSuccess) return err;
+  const bool xs = e->xs_abuf != nullptr;
   SkinnyArgs k = skinny_args(e->d_gate, c.depth_inner, d, e->abuf, d, e->act, e->inner_max, M);
   k.w2 = e->d_up;
+  if (xs) { k.xs = e->xs_abuf; k.xs_out = e->xs_act; }
   if ((err = launch_skinny<EPI_SWIGLU>(e, k)) != hipSuccess) return err;
   k = skinny_args(e->d_down, d, c.depth_inner, e->act, e->inner_max, e->ybuf, d, M);
   k.res = e->abuf; k.ldr = d;
+  if (xs) { k.xs = e->xs_act; k.xs_out = e->xs_y; k.xs_gain = e->d_norm_out; k.ss_out = e->ss_y; }
   if ((err = launch_skinny<EPI_RESID>(e, k)) != hipSuccess) return err;
   const void* tq = static_cast<const char*>(e->out_proj ? e->out_proj : e->table) + (size_t)q * V * d * tsz;
   k = skinny_args(tq, V, d, e->ybuf, d, e->logits, V, M);
   k.bias = e->d_bias + (size_t)q * V; k.norm_w = e->d_norm_out; k.eps = c.depth_eps;
+  if (xs) { k.xs = e->xs_y; k.ss_in = e->ss_y; k.n_ss = d / 16; }
   return launch_skinny<EPI_BIAS, true>(e, k);
 }
 
@@ -547,6 +609,12 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   e->nqkv = (c.n_q_heads + 2 * c.n_kv_heads) * c.head_dim;
   e->inner_max = c.trunk_inter > c.depth_inner ? c.trunk_inter : c.depth_inner;
   e->max_chunks = (c.max_ctx + ATT_CHUNK - 1) / ATT_CHUNK;
+  // Many rows: streaming attention with enough splits per (row, kv head) for
+  // ~256 workgroups (one per CU); its partials reuse the chunk-partial buffer.
+  if (e->wide && (e->G == 1 || e->G == 2 || e->G == 4) && e->G * c.head_dim <= ATTN_STREAM_NTH) {
+    const int pairs = e->rows * c.n_kv_heads;
+    e->attn_splits = std::max(1, std::min(e->max_chunks, (256 + pairs - 1) / pairs));
+  }
   e->L.resize(c.n_layers);
   e->kv_host.assign(e->rows, 0);
   e->len_host.assign(e->rows, 0);
@@ -585,6 +653,12 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     ALLOC(e->sk_arrive, nmax / 16 + 1);
   }
   ALLOC(e->part, R * c.n_q_heads * e->max_chunks * (c.head_dim + 2));
+  const bool split_in = e->wide && c.weight_dtype == SK_BF16;
+  if (split_in) {
+    ALLOC(e->xs_x, xsplit_elems(d)); ALLOC(e->xs_attn, xsplit_elems(c.n_q_heads * c.head_dim));
+    ALLOC(e->xs_act, xsplit_elems(e->inner_max)); ALLOC(e->xs_abuf, xsplit_elems(d)); ALLOC(e->xs_y, xsplit_elems(d));
+    ALLOC(e->ss_x, (size_t)XS_ROWS * d / 16); ALLOC(e->ss_y, (size_t)XS_ROWS * d / 16);
+  }
   ALLOC(e->kv_len, R); ALLOC(e->pos, R); ALLOC(e->active, R); ALLOC(e->plen, R);
   ALLOC(e->fc, 1);
   ALLOC(e->p_rope, (size_t)(c.max_ctx + 1) * (c.head_dim / 2));
@@ -615,6 +689,13 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
                    (std::max({(size_t)e->nqkv, (size_t)c.trunk_inter, (size_t)c.depth_inner, (size_t)c.audio_vocab,
                               (size_t)c.d_model}) / 16 + 1) * sizeof(unsigned));
   if (he == hipSuccess) he = hipMemset(e->pos, 0, R * sizeof(int));
+  if (split_in) {   // rows past R are never written; keep them finite
+    uint16_t* xs[] = {e->xs_x, e->xs_attn, e->xs_act, e->xs_abuf, e->xs_y};
+    const size_t xk[] = {d, (size_t)c.n_q_heads * c.head_dim, (size_t)e->inner_max, d, d};
+    for (int i = 0; i < 5 && he == hipSuccess; ++i) he = hipMemset(xs[i], 0, xsplit_elems((int)xk[i]) * sizeof(uint16_t));
+    if (he == hipSuccess) he = hipMemset(e->ss_x, 0, (size_t)XS_ROWS * d / 16 * sizeof(float));
+    if (he == hipSuccess) he = hipMemset(e->ss_y, 0, (size_t)XS_ROWS * d / 16 * sizeof(float));
+  }
   if (he == hipSuccess) he = hipMemset(e->fc, 0, sizeof(int));
   if (he == hipSuccess) he = hipMemset(e->flag_ring, 0, (size_t)c.max_frames * 2 * sizeof(int));
   if (he == hipSuccess) he = hipMemset(e->u_ring, 0, (size_t)c.max_frames * c.n_utts * Q * sizeof(double));
@@ -642,7 +723,7 @@ int sk_destroy(sk_engine* e) {
   if (!e) return SK_OK;
   if (e->stream) hipStreamSynchronize(e->stream);
   drop_graphs(e);
-  void* bufs[] = {e->sk_partial, e->sk_arrive, e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
+  void* bufs[] = {e->sk_partial, e->sk_arrive, e->xs_x, e->xs_attn, e->xs_act, e->xs_abuf, e->xs_y, e->ss_x, e->ss_y, e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
                   e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->flag_ring, e->u_ring,
                   e->pX, e->pXn, e->pQKV, e->pQ, e->pATT, e->pACT, e->p_tok_row, e->p_tok_pos,

@@ -477,6 +477,28 @@ __global__ __launch_bounds__(NT) void rmsnorm_rows_kernel(const float* x, const 
   }
 }
 
+// ------------------------------------------------------------ split activations
+// Split form of a GEMM input x [rows <= 32][K] for the BF16 matrix cores:
+// for each 32-k block, row tile t (rows 16t .. 16t+15) and half (hi, lo), the
+// 64 lanes' B fragments of v_mfma_f32_16x16x32_bf16, 8 BF16 each (lane 16q+i:
+// row 16t+i, k = 32*block + 8q .. 8q+7), 1 KiB per (block, t, half).  x_hi =
+// bf16(x g), x_lo = bf16(x g - x_hi), with g the consumer's RMSNorm gain (1
+// without): the pair keeps ~16 mantissa bits of x g.  The kernel that produces
+// x writes it, so a consumer's workgroups load ready fragments instead of
+// each re-reading FP32 x and splitting it again.
+constexpr int XS_ROWS = 32;
+__host__ __device__ constexpr size_t xsplit_elems(int K) { return (size_t)K * XS_ROWS * 2; }
+__device__ __forceinline__ size_t xsplit_index(int r, int k) {   // hi half; lo at + 512
+  return ((size_t)(k >> 5) * 2 + (r >> 4)) * 1024 + (size_t)(16 * ((k & 31) >> 3) + (r & 15)) * 8 + (k & 7);
+}
+__device__ __forceinline__ void xsplit_store(uint16_t* xs, int r, int k, float v) {
+  const __bf16 hi = (__bf16)v;
+  const __bf16 lo = (__bf16)(v - (float)hi);
+  const size_t i = xsplit_index(r, k);
+  xs[i] = __builtin_bit_cast(uint16_t, hi);
+  xs[i + 512] = __builtin_bit_cast(uint16_t, lo);
+}
+
 // ------------------------------------------------------------ attention
 // One decode token per row against that row's own cache (per-row length and
 // RoPE position; CFG rows differ in length).  Grid (chunks, Hkv, rows); the
@@ -502,6 +524,8 @@ struct AttnArgs {
   float* out; int ldo;                   // [rows][Hq hd]
   int Hq, Hkv, hd, max_ctx, max_chunks;
   float scale;
+  int nparts;                            // > 0: partials per (row, q head) to merge (stream kernel splits)
+  uint16_t* xs_out;                      // output again in split form (null: none)
 };
 
 constexpr int ATT_DPL = 16;      // head dims per lane
@@ -778,14 +802,256 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   load_block(0);
   // Keep the first block's loads ahead of the length lookup they do not need.
   asm volatile("" ::: "memory");
-  const int nch = (a.kv_len[r] + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
+  const int nch = a.nparts > 0 ? a.nparts : (a.kv_len[r] + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
   const int act = a.active[r];
   float M = -INFINITY, L = 0.f, O = 0.f;
   for (int c0 = 0; c0 < nch; c0 += CB) {
     if (c0 > 0) load_block(c0);
     merge_block(mv, lv, ov, c0, nch, M, L, O);
   }
-  if (act && d < hd) a.out[(size_t)r * a.ldo + (size_t)hq * hd + d] = O / L;
+  if (act && d < hd) {
+    a.out[(size_t)r * a.ldo + (size_t)hq * hd + d] = O / L;
+    if (a.xs_out) xsplit_store(a.xs_out, r, hq * hd + d, O / L);
+  }
+}
+
+// ------------------------------------------------------------ many-row attention
+// All-reduce over each aligned group of n lanes (n = 1, 2, 4, 8, 16); every
+// lane of the group gets the same bits (each step adds a commutative pair).
+__device__ __forceinline__ float group_allsum(float v, int n) {
+  if (n >= 2) v += dpp_keep<0xb1, 0xf>(v);    // quad_perm [1,0,3,2]
+  if (n >= 4) v += dpp_keep<0x4e, 0xf>(v);    // quad_perm [2,3,0,1]
+  if (n >= 8) v += dpp_keep<0x141, 0xf>(v);   // row_half_mirror: lane i <-> 7 - i
+  if (n >= 16) v += dpp_keep<0x140, 0xf>(v);  // row_mirror: lane i <-> 15 - i
+  return v;
+}
+
+// Two online-softmax states (max, sum, output) of one query head -> one.
+// An empty state has max -inf and contributes nothing.
+__device__ __forceinline__ float merge_weight(float m, float M) { return m == -INFINITY ? 0.f : expf(m - M); }
+
+// smem floats of attention_stream_kernel
+__host__ __device__ constexpr size_t attn_stream_smem_floats(int G, int hd, int nth) {
+  return (size_t)G * hd + 4 * (size_t)hd + (size_t)hd + (size_t)(nth / 64) * G * (hd + 2);
+}
+
+// Decode attention for many rows.  Grid (S, Hkv, rows), NTH threads.  A group
+// of LPT = hd/16 lanes (a slot) holds one token at a time, 16 dims per lane; slot
+// `slot` of split s reads the tokens t = s*TPP + slot + j*S*TPP, j = 0, 1, ...
+// (TPP = NTH/LPT slots), so each load instruction of a workgroup covers TPP
+// consecutive cache rows.  Every slot runs its own online softmax over its
+// tokens (running max, sum and 16 output dims per query head, all in
+// registers): the loop has no LDS traffic and no barrier, and D tokens are in
+// flight per slot.  The slots are merged once at the end, across lanes by
+// shuffles and across waves in LDS.  Queries and the new key get Qwen3's
+// per-head RMSNorm then rotate-half RoPE (as attention_kernel); the split that
+// owns token T appends the new K/V and attends to it from registers.
+// S == 1 writes the attention output; S > 1 writes one partial (o, max, sum)
+// per split in the chunk-partial layout for attention_combine_kernel
+// (nparts = S).  Requires G*hd <= NTH.
+template <typename KT, int G, int NTH, int D>
+__global__ __launch_bounds__(NTH) void attention_stream_kernel(AttnArgs a, int S) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  constexpr int NW = NTH / 64;
+  const int s = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
+  const int hd = a.hd, half = hd / 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int LPT = hd / ATT_DPL, TPP = NTH / LPT;
+  const int sub = tid % LPT, slot = tid / LPT;
+  const size_t head_base = ((size_t)r * a.Hkv + h) * a.max_ctx;
+  const int t0 = s * TPP + slot, tstep = S * TPP;
+
+  float* qs = sm;                        // [G][hd]
+  float* knew = qs + G * hd;             // [hd]
+  float* vnew = knew + hd;               // [hd]
+  float* qw = vnew + hd;                 // [hd]
+  float* kw = qw + hd;                   // [hd]
+  float* fcs = kw + hd;                  // [hd/2]
+  float* fsn = fcs + half;               // [hd/2]
+  float* mo = fsn + half;                // [NW][G][hd] merged outputs
+  float* mls = mo + (size_t)NW * G * hd; // [NW][G][2] merged (max, sum)
+
+  constexpr bool KBF = sizeof(KT) == 2;
+  constexpr int EPV = 16 / (int)sizeof(KT);    // cache elements per 16-byte load
+  constexpr int NLD = ATT_DPL / EPV;           // loads per token and lane
+  // Load i of a slot covers 16-byte pieces i*LPT .. i*LPT+LPT-1 of the row, so
+  // each load instruction reads whole cache lines; the lane's register e holds
+  // head dim dim_of(e).
+  auto dim_of = [&](int e) { return ((e / EPV) * LPT + sub) * EPV + e % EPV; };
+  struct Tok { uint4 k[NLD], v[NLD]; };
+  auto load = [&](int j, Tok& b) {       // token index clamped into the cache: always in bounds
+    const int t = min(t0 + j * tstep, a.max_ctx - 1);
+    const uint4* kp = reinterpret_cast<const uint4*>(static_cast<const KT*>(a.kc) + (head_base + t) * hd) + sub;
+    const uint4* vp = reinterpret_cast<const uint4*>(static_cast<const KT*>(a.vc) + (head_base + t) * hd) + sub;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) { b.k[i] = kp[i * LPT]; b.v[i] = vp[i * LPT]; }
+  };
+  auto widen = [&](const uint4 (&raw)[NLD], float (&out)[ATT_DPL]) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (KBF) {
+          out[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+          out[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        } else {
+          out[4 * i + j] = __uint_as_float(w[j]);
+        }
+      }
+    }
+  };
+
+  // Raw q / k / v of this head, norm gains and RoPE entry to registers, then
+  // the first D tokens of every slot -- all before the row's length arrives.
+  const float* row = a.qkv + (size_t)r * a.ldqkv;
+  float q_r = 0.f, kn_r = 0.f, vn_r = 0.f, qw_r = 0.f, kw_r = 0.f;
+  float2 cs_r = make_float2(1.f, 0.f);
+  if (tid < G * hd) q_r = row[(size_t)h * G * hd + tid];
+  if (tid < hd) {
+    kn_r = row[(size_t)a.Hq * hd + (size_t)h * hd + tid];
+    vn_r = row[(size_t)(a.Hq + a.Hkv) * hd + (size_t)h * hd + tid];
+    qw_r = a.qn_w[tid];
+    kw_r = a.kn_w[tid];
+  }
+  if (tid < half) cs_r = a.rope[(size_t)r * half + tid];
+  Tok ring[D];
+#pragma unroll
+  for (int u = 0; u < D; ++u) load(u, ring[u]);
+
+  const int T = a.kv_len[r];
+  if (!a.active[r]) return;
+  const int ctx = T + 1;
+  const int n_iter = ctx > s * TPP ? (ctx - s * TPP + tstep - 1) / tstep : 0;
+  const bool owner = ((T / TPP) % S) == s;
+  if (tid < G * hd) qs[tid] = q_r;
+  if (tid < hd) { knew[tid] = kn_r; vnew[tid] = vn_r; qw[tid] = qw_r; kw[tid] = kw_r; }
+  if (tid < half) { fcs[tid] = cs_r.x; fsn[tid] = cs_r.y; }
+  __syncthreads();
+  const int nheads = G + (owner ? 1 : 0);
+  for (int j = wave; j < nheads; j += NW) {
+    float* v = (j < G) ? qs + j * hd : knew;
+    const float* w = (j < G) ? qw : kw;
+    float ss = 0.f;
+    for (int d = lane; d < hd; d += 64) ss += v[d] * v[d];
+    const float inv = 1.0f / sqrtf(wave_sum_dpp(ss) / (float)hd + a.eps);
+    for (int d = lane; d < half; d += 64) {
+      const float x1 = w[d] * (v[d] * inv);
+      const float x2 = w[d + half] * (v[d + half] * inv);
+      v[d] = x1 * fcs[d] - x2 * fsn[d];
+      v[d + half] = x2 * fcs[d] + x1 * fsn[d];
+    }
+  }
+  __syncthreads();
+  // Append the new token.  A BF16 cache stores it rounded, and this step then
+  // attends to the rounded values too, as every later step will.
+  if (owner) {
+    for (int d = tid; d < hd; d += NTH) {
+      if constexpr (KBF) {
+        static_cast<KT*>(a.kc)[(head_base + T) * hd + d] = (KT)bf16_bits(knew[d]);
+        static_cast<KT*>(a.vc)[(head_base + T) * hd + d] = (KT)bf16_bits(vnew[d]);
+      } else {
+        static_cast<KT*>(a.kc)[(head_base + T) * hd + d] = knew[d];
+        static_cast<KT*>(a.vc)[(head_base + T) * hd + d] = vnew[d];
+      }
+    }
+    if constexpr (KBF) {
+      for (int d = tid; d < hd; d += NTH) { knew[d] = bf16_round(knew[d]); vnew[d] = bf16_round(vnew[d]); }
+      __syncthreads();                   // `owner` is uniform over the workgroup
+    }
+  }
+  float q[G][ATT_DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < ATT_DPL; ++i) q[g][i] = qs[g * hd + dim_of(i)];
+
+  float m[G], l[G], o[G][ATT_DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY; l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < ATT_DPL; ++i) o[g][i] = 0.f;
+  }
+  for (int j0 = 0; j0 < n_iter; j0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const int j = j0 + u;
+      if (j < n_iter) {                  // uniform over the workgroup
+        const int t = t0 + j * tstep;
+        float kr[ATT_DPL], vr[ATT_DPL];
+        widen(ring[u].k, kr);
+        widen(ring[u].v, vr);
+        if (j + D < n_iter) load(j + D, ring[u]);
+        if (t == T) {
+#pragma unroll
+          for (int i = 0; i < ATT_DPL; ++i) { kr[i] = knew[dim_of(i)]; vr[i] = vnew[dim_of(i)]; }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float dot = 0.f;
+#pragma unroll
+          for (int i = 0; i < ATT_DPL; ++i) dot = fmaf(q[g][i], kr[i], dot);
+          const float sc = group_allsum(dot, LPT) * a.scale;
+          if (t < ctx) {
+            const float mn = fmaxf(m[g], sc);
+            const float f = expf(m[g] - mn);   // 0 while the slot is empty (m = -inf)
+            const float p = expf(sc - mn);
+            l[g] = fmaf(l[g], f, p);
+#pragma unroll
+            for (int i = 0; i < ATT_DPL; ++i) o[g][i] = fmaf(o[g][i], f, p * vr[i]);
+            m[g] = mn;
+          }
+        }
+      }
+    }
+  }
+  // Merge the slots of the wave (lanes with the same sub), then the waves.
+  for (int off = LPT; off < 64; off <<= 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float m2 = __shfl_xor(m[g], off, 64), l2 = __shfl_xor(l[g], off, 64);
+      const float M = fmaxf(m[g], m2);
+      const float f1 = merge_weight(m[g], M), f2 = merge_weight(m2, M);
+      l[g] = l[g] * f1 + l2 * f2;
+#pragma unroll
+      for (int i = 0; i < ATT_DPL; ++i) {
+        const float o2 = __shfl_xor(o[g][i], off, 64);
+        o[g][i] = o[g][i] * f1 + o2 * f2;
+      }
+      m[g] = M;
+    }
+  }
+  if (lane < LPT) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int i = 0; i < ATT_DPL; ++i) mo[((size_t)wave * G + g) * hd + dim_of(i)] = o[g][i];
+      if (lane == 0) { mls[(wave * G + g) * 2] = m[g]; mls[(wave * G + g) * 2 + 1] = l[g]; }
+    }
+  }
+  __syncthreads();
+  if (tid < G * hd) {
+    const int g = tid / hd, d = tid - g * hd;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, mls[(w * G + g) * 2]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = merge_weight(mls[(w * G + g) * 2], M);
+      L = fmaf(mls[(w * G + g) * 2 + 1], f, L);
+      O = fmaf(mo[((size_t)w * G + g) * hd + d], f, O);
+    }
+    if (S == 1) {
+      a.out[(size_t)r * a.ldo + (size_t)(h * G + g) * hd + d] = O / L;
+      if (a.xs_out) xsplit_store(a.xs_out, r, (h * G + g) * hd + d, O / L);
+    } else {
+      float* pp = a.part + (((size_t)r * a.Hq + h * G + g) * a.max_chunks + s) * (hd + 2);
+      pp[d] = O;
+      if (d == 0) { pp[hd] = M; pp[hd + 1] = L; }
+    }
+  }
 }
 
 // ------------------------------------------------------------ sampler

@@ -10,6 +10,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "sk_kernels.h"
 
 namespace sk {
@@ -26,6 +28,12 @@ struct SkinnyArgs {
   int ksplit;                          // K slices per output tile (1, 2 or 4; BF16 form)
   float* partial;                      // [tiles][ksplit][SK_PSZ] slice partials (ksplit > 1)
   unsigned* arrive;                    // [tiles] slice arrival counts, zero between launches
+  // BF16 form only:
+  const uint16_t* xs;                  // x in split form (xsplit_index), gain applied; null: FP32 x
+  const float* ss_in; int n_ss;        // NORM with xs: [32][n_ss] partial sums of x^2 per row
+  uint16_t* xs_out;                    // out again in split form for the next GEMM; null: none
+  const float* xs_gain;                // gain applied before that split (the next RMSNorm); null: 1
+  float* ss_out;                       // [32][N/16] sums of out^2 per row and output tile; null: none
 };
 
 // Floats per slice partial: two epilogue values per thread (SwiGLU) + 32 row
@@ -171,12 +179,23 @@ typedef __bf16 sbf8 __attribute__((ext_vector_type(8)));
 // acknowledged, and counts itself in arrive[tile] (an L2 atomic); the last
 // slice to arrive adds the S partials in slice order, applies the epilogue and
 // resets the count.  No workgroup waits for another.
-template <int EPI, int W, bool NORM>
+//
+// Split input (XS): x arrives in split form, written by the kernel that
+// produced it with this GEMM's norm gain applied, so a stage is four 16-byte
+// fragment loads per lane and no conversion; with NORM the row's sum of
+// squares is the sum of the producer's per-tile partials (ss_in).  Outputs
+// can be written in split form for the next GEMM (xs_out, with that GEMM's
+// gain) together with their per-tile sums of squares (ss_out).
+template <int EPI, int W, bool NORM, bool XS>
 __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
+  static_assert(!XS || W == 8, "split input: one thread per (row, 16th of the partial sums)");
   constexpr int NA = (EPI == EPI_SWIGLU) ? 2 : 1;
   constexpr int BK = 32;                // k per block: 8 per lane
+  constexpr bool XNORM = NORM && !XS;   // gain and sum of squares taken from FP32 x here
   __shared__ float red[W][NA * 2 * 4][64];
-  __shared__ float ssq[NORM ? W : 1][2][64];
+  __shared__ float ssq[XNORM ? W : 1][2][64];
+  __shared__ float ssr[XS_ROWS];
+  __shared__ float sso[2][4][64];
   __shared__ int last_slice;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i16 = lane & 15, kq = lane >> 4;
@@ -199,30 +218,38 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
   const uint16_t* w2p = NA == 2 ? static_cast<const uint16_t*>(a.w2) + (size_t)o * a.K + 8 * kq : nullptr;
   const float* xr0 = a.x + (size_t)min(i16, a.R - 1) * a.ldx + 8 * kq;
   const float* xr1 = a.x + (size_t)min(16 + i16, a.R - 1) * a.ldx + 8 * kq;
-  const float* gp = NORM ? a.norm_w + 8 * kq : nullptr;
-  struct Stage { uint4 w[NA]; float4 x0[2], x1[2], g[NORM ? 2 : 1]; };
+  const float* gp = XNORM ? a.norm_w + 8 * kq : nullptr;
+  const uint4* xsp = XS ? reinterpret_cast<const uint4*>(a.xs) + lane : nullptr;
+  struct StageF { uint4 w[NA]; float4 x0[2], x1[2], g[XNORM ? 2 : 1]; };
+  struct StageS { uint4 w[NA]; uint4 xs[4]; };   // hi/lo of row tiles 0 and 1
+  using Stage = typename std::conditional<XS, StageS, StageF>::type;
   auto load = [&](int kb, Stage& st) {
     st.w[0] = *reinterpret_cast<const uint4*>(wp + kb);
     if constexpr (NA == 2) st.w[NA - 1] = *reinterpret_cast<const uint4*>(w2p + kb);
+    if constexpr (XS) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      st.x0[h] = *reinterpret_cast<const float4*>(xr0 + kb + 4 * h);
-      st.x1[h] = *reinterpret_cast<const float4*>(xr1 + kb + 4 * h);
-      if constexpr (NORM) st.g[h] = *reinterpret_cast<const float4*>(gp + kb + 4 * h);
+      for (int j = 0; j < 4; ++j) st.xs[j] = xsp[((size_t)(kb >> 5) * 4 + j) * 64];
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        st.x0[h] = *reinterpret_cast<const float4*>(xr0 + kb + 4 * h);
+        st.x1[h] = *reinterpret_cast<const float4*>(xr1 + kb + 4 * h);
+        if constexpr (XNORM) st.g[h] = *reinterpret_cast<const float4*>(gp + kb + 4 * h);
+      }
     }
   };
   sv4f acc[NA][2];
 #pragma unroll
   for (int n = 0; n < NA; ++n) acc[n][0] = acc[n][1] = sv4f{0.f, 0.f, 0.f, 0.f};
   float ss0 = 0.f, ss1 = 0.f;
-  auto split = [&](const float4 (&xv)[2], const float4 (&gv)[NORM ? 2 : 1], float& ss, sbf8& hi, sbf8& lo) {
+  auto split = [&](const float4 (&xv)[2], const float4 (&gv)[XNORM ? 2 : 1], float& ss, sbf8& hi, sbf8& lo) {
     const float v[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float x = v[j];
-      if constexpr (NORM) {
-        const float g[8] = {gv[0].x, gv[0].y, gv[0].z, gv[0].w, gv[NORM ? 1 : 0].x, gv[NORM ? 1 : 0].y,
-                            gv[NORM ? 1 : 0].z, gv[NORM ? 1 : 0].w};
+      if constexpr (XNORM) {
+        const float g[8] = {gv[0].x, gv[0].y, gv[0].z, gv[0].w, gv[XNORM ? 1 : 0].x, gv[XNORM ? 1 : 0].y,
+                            gv[XNORM ? 1 : 0].z, gv[XNORM ? 1 : 0].w};
         ss = fmaf(x, x, ss);
         x *= g[j];
       }
@@ -233,8 +260,15 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
   };
   auto comp = [&](const Stage& st) {
     sbf8 h0, l0, h1, l1;
-    split(st.x0, st.g, ss0, h0, l0);
-    split(st.x1, st.g, ss1, h1, l1);
+    if constexpr (XS) {
+      h0 = __builtin_bit_cast(sbf8, st.xs[0]);
+      l0 = __builtin_bit_cast(sbf8, st.xs[1]);
+      h1 = __builtin_bit_cast(sbf8, st.xs[2]);
+      l1 = __builtin_bit_cast(sbf8, st.xs[3]);
+    } else {
+      split(st.x0, st.g, ss0, h0, l0);
+      split(st.x1, st.g, ss1, h1, l1);
+    }
 #pragma unroll
     for (int n = 0; n < NA; ++n) {
       const sbf8 wa = __builtin_bit_cast(sbf8, st.w[n]);
@@ -244,10 +278,38 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
       acc[n][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, l1, acc[n][1], 0, 0, 0);
     }
   };
+  // Split input with NORM: the producer's partial sums of squares of row
+  // tid / 16, 16 threads per row, loaded ahead of the first stage.
+  constexpr int SSP = 16;               // partials per thread: n_ss <= 256
+  float ssp[(XS && NORM) ? SSP : 1];
+  if constexpr (XS && NORM) {
+    const float* sp = a.ss_in + (size_t)(tid >> 4) * a.n_ss + (tid & 15);
+#pragma unroll
+    for (int i = 0; i < SSP; ++i) ssp[i] = ((tid & 15) + 16 * i < a.n_ss) ? sp[16 * i] : 0.f;
+  }
+  // Epilogue operands of this thread's output (row r, column oo), loaded at
+  // entry: they do not depend on the sums.
+  const bool et = tid < 512;            // threads 0..511 own one (row tile, v, lane) each
+  const int t = (tid >> 8) & 1, v = (tid >> 6) & 3, l = tid & 63;
+  const int oo = o0 + 4 * (l >> 4) + v, r = 16 * t + (l & 15);
+  const bool ok = et && oo < a.N && r < a.R;
+  float epi_in = 0.f;
+  if constexpr (EPI == EPI_BIAS) epi_in = ok ? a.bias[oo] : 0.f;
+  if constexpr (EPI == EPI_RESID) epi_in = ok ? a.res[(size_t)r * a.ldr + oo] : 0.f;
   Stage sa, sb;
   constexpr int STEP = W * BK;
   int kb = kbeg + wave * BK;
   if (kb < kend) load(kb, sa);
+  if constexpr (XS && NORM) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < SSP; ++i) t += ssp[i];
+    t += __shfl_xor(t, 8, 64);          // the row's 16 threads; each pair adds in both orders alike
+    t += __shfl_xor(t, 4, 64);
+    t += __shfl_xor(t, 2, 64);
+    t += __shfl_xor(t, 1, 64);
+    if ((tid & 15) == 0) ssr[tid >> 4] = t;
+  }
   for (; kb < kend; kb += 2 * STEP) {
     const int k1 = kb + STEP, k2 = k1 + STEP;
     if (k1 < kend) load(k1, sb);
@@ -263,13 +325,9 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v) red[wave][(n * 2 + t) * 4 + v][lane] = acc[n][t][v];
-  if constexpr (NORM) { ssq[wave][0][lane] = ss0; ssq[wave][1][lane] = ss1; }
+  if constexpr (XNORM) { ssq[wave][0][lane] = ss0; ssq[wave][1][lane] = ss1; }
   __syncthreads();
-  // Threads 0..511 own one (row tile, v, lane) each; with 16 waves the upper
-  // half only takes part in the barriers.
-  const bool et = tid < 512;
-  const int t = (tid >> 8) & 1, v = (tid >> 6) & 3, l = tid & 63;
-  const int oo = o0 + 4 * (l >> 4) + v, r = 16 * t + (l & 15);
+  // With 16 waves the upper half only takes part in the barriers.
   float c[NA];
 #pragma unroll
   for (int n = 0; n < NA; ++n) {
@@ -279,18 +337,19 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
     c[n] = sacc;
   }
   float ss = 0.f;
-  if constexpr (NORM) {
+  if constexpr (XNORM) {
 #pragma unroll
     for (int w = 0; w < W; ++w)
 #pragma unroll
       for (int k4 = 0; k4 < 4; ++k4) ss += ssq[w][t][k4 * 16 + (l & 15)];
   }
+  if constexpr (XS && NORM) ss = ssr[r];
   if (S > 1) {
     float* mine = a.partial + ((size_t)tile * S + slice) * SK_PSZ;
     if (et) {
 #pragma unroll
       for (int n = 0; n < NA; ++n) mine[n * 512 + tid] = c[n];
-      if (NORM && v == 0 && (l >> 4) == 0) mine[2 * 512 + r] = ss;
+      if (XNORM && v == 0 && (l >> 4) == 0) mine[2 * 512 + r] = ss;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's partials are in L2
     __syncthreads();
@@ -300,43 +359,58 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
     __syncthreads();
     if (!last_slice) return;
     if (tid == 0) __hip_atomic_store(a.arrive + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (!et) return;
-    const float* all = a.partial + (size_t)tile * S * SK_PSZ;
+    if (et) {
+      const float* all = a.partial + (size_t)tile * S * SK_PSZ;
 #pragma unroll
-    for (int n = 0; n < NA; ++n) {
-      float sacc = 0.f;
-      for (int q = 0; q < S; ++q) sacc += all[(size_t)q * SK_PSZ + n * 512 + tid];
-      c[n] = sacc;
-    }
-    if constexpr (NORM) {
-      ss = 0.f;
-      for (int q = 0; q < S; ++q) ss += all[(size_t)q * SK_PSZ + 2 * 512 + r];
+      for (int n = 0; n < NA; ++n) {
+        float sacc = 0.f;
+        for (int q = 0; q < S; ++q) sacc += all[(size_t)q * SK_PSZ + n * 512 + tid];
+        c[n] = sacc;
+      }
+      if constexpr (XNORM) {
+        ss = 0.f;
+        for (int q = 0; q < S; ++q) ss += all[(size_t)q * SK_PSZ + 2 * 512 + r];
+      }
     }
   }
-  if (!et) return;
   if constexpr (NORM) {
     const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
 #pragma unroll
     for (int n = 0; n < NA; ++n) c[n] *= inv;
   }
-  if (oo < a.N && r < a.R) {
-    float y = c[0];
-    if constexpr (EPI == EPI_BIAS) y = y + a.bias[oo];
-    if constexpr (EPI == EPI_RESID) y = a.res[(size_t)r * a.ldr + oo] + y;
+  float y = 0.f;
+  if (ok) {
+    y = c[0];
+    if constexpr (EPI == EPI_BIAS) y = y + epi_in;
+    if constexpr (EPI == EPI_RESID) y = epi_in + y;
     if constexpr (EPI == EPI_SWIGLU) y = y / (1.0f + expf(-y)) * c[NA - 1];
     a.out[(size_t)r * a.ldo + oo] = y;
+    if (a.xs_out) xsplit_store(a.xs_out, r, oo, a.xs_gain ? y * a.xs_gain[oo] : y);
+  }
+  if (a.ss_out) {                       // uniform over the workgroup
+    if (et) sso[t][v][l] = y * y;
+    __syncthreads();
+    if (et && v == 0 && (l >> 4) == 0 && r < a.R) {
+      float sq = 0.f;
+#pragma unroll
+      for (int v2 = 0; v2 < 4; ++v2)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sq += sso[t][v2][q * 16 + (l & 15)];
+      a.ss_out[(size_t)r * (a.N / 16) + tile] = sq;
+    }
   }
 }
 
 // Depth step q, row r (utterance r / rows_per_utt): for q > 0 the codebook
 // prefix advances by the previous code's table row (prefix += scale *
 // table[q-1][code], model.py:600-605) in place; then out = RMSNorm_in(hidden
-// + prefix) (eps FLT_EPSILON) -- the depth MLP input and its residual.
+// + prefix) (eps FLT_EPSILON) -- the depth MLP input and its residual -- and,
+// when xs_out is set, the same values in split form for the MLP's GEMM.
 template <typename TL>
 __global__ __launch_bounds__(NT) void depth_in_kernel(const float* hidden, float* prefix, const void* table,
                                                       const int* codes_cur, int q, int Q, int V, int D,
                                                       float scale, int rows_per_utt, const float* w, float eps,
-                                                      float* out) {
+                                                      float* out, uint16_t* xs_out) {
   __shared__ float red[WAVES];
   const int r = blockIdx.x, ut = r / rows_per_utt;
   const size_t trow = (q > 0) ? ((size_t)(q - 1) * V + codes_cur[ut * Q + q - 1]) * D : 0;
@@ -353,7 +427,9 @@ __global__ __launch_bounds__(NT) void depth_in_kernel(const float* hidden, float
   const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
   for (int k = threadIdx.x; k < D; k += NT) {
     const float x = __fadd_rn(hidden[(size_t)r * D + k], prefix[(size_t)r * D + k]);
-    out[(size_t)r * D + k] = w[k] * (x * inv);
+    const float y = w[k] * (x * inv);
+    out[(size_t)r * D + k] = y;
+    if (xs_out) xsplit_store(xs_out, r, k, y);
   }
 }
 

@@ -473,6 +473,20 @@ def test_many_utterances_tiny(hip_device):
     assert rel < LOGIT_TOL
 
 
+def test_many_utterances_tiny_bf16_ten_rows(hip_device):
+    """Ten decode rows (5 utterances x CFG) with BF16 weights: GEMM inputs
+    pass between kernels in split form (BF16 hi/lo pairs with the next norm's
+    gain, written by each producer; rows 10..31 of those buffers are never
+    written), non-unit norm gains; each utterance matches the oracle on the
+    same BF16-rounded weights."""
+    from oracle.model import TINY
+
+    w = _device_weights(TINY, 41, hip_device)
+    rel = _many_utterance_case(TINY, w, 5, 7, hip_device, bf16=True, frames=3)
+    print(f"tiny BF16, 5 utterances: max row-relative logit error {rel:.3e}")
+    assert rel < LOGIT_TOL
+
+
 def test_sixteen_utterances_q06b_bf16(hip_device):
     """Batch-32 decode (16 utterances x CFG) at the Qwen3-0.6B shape with BF16
     weights (FP32 accumulation), ragged prefixes: every utterance against the

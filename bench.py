@@ -13,6 +13,13 @@ so all K frames run (the work per frame does not depend on it).
 
 Prints one JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one
 GPU (utterances shard across GPUs with no per-frame exchange).
+
+``--utterances N`` (N > 1) runs the throughput batch instead: N synthetic
+utterances with CFG decoded together (decode batch 2N) at Qwen3-0.6B shape
+with BF16 weights (FP32 KV cache and accumulation); each prefix is 120-240
+tokens drawn uniformly (text ids + BOS frame + prompt frames, the prompt ~60%
+of it; the uncond row is [bos] + BOS frame + the same prompt); KV capacity
+512.  A step is one frame of every utterance; ``value`` is utterance-frames/s.
 """
 
 from __future__ import annotations
@@ -54,15 +61,17 @@ def algorithmic_bytes(shape, kv_lens, w_bytes=4, kv_bytes=4):
     """Bytes one frame must move at minimum: every weight tensor read once
     (depth MLP counted once although applied Q times), K/V of every cached
     token of every row read once, the new token's K/V written, Q table rows
-    gathered.  ``kv_lens``: cached tokens per row at the frame's start."""
+    gathered.  ``kv_lens``: cached tokens per row at the frame's start.
+    ``w_bytes``: bytes per matrix element (norm gains and biases stay FP32)."""
     s = shape
     per_layer = (2 * s.n_q_heads * s.head_dim * s.d_model + 2 * s.n_kv_heads * s.head_dim * s.d_model
-                 + 3 * s.trunk_inter * s.d_model + 2 * s.d_model + 2 * s.head_dim)
-    trunk = s.n_layers * per_layer + s.d_model
-    depth = 3 * s.depth_inner * s.d_model + 2 * s.d_model
+                 + 3 * s.trunk_inter * s.d_model)
+    vectors = s.n_layers * (2 * s.d_model + 2 * s.head_dim) + s.d_model + 2 * s.d_model
+    trunk = s.n_layers * per_layer
+    depth = 3 * s.depth_inner * s.d_model
     table = s.n_codebooks * s.audio_vocab * s.d_model
     bias = s.n_codebooks * s.audio_vocab
-    weights = (trunk + depth + table) * w_bytes + bias * 4
+    weights = (trunk + depth + table) * w_bytes + (vectors + bias) * 4
     kv_token = s.n_layers * 2 * s.n_kv_heads * s.head_dim * kv_bytes
     kv = sum(kv_lens) * kv_token + len(kv_lens) * kv_token
     gather = s.n_codebooks * s.d_model * 4
@@ -139,6 +148,78 @@ def copy_probe(mib):
     print(json.dumps({"copy_probe_bytes_each_way": n * 4, "copies": 4}))
 
 
+def many_utterances(args):
+    """The throughput batch (see the module docstring); prints one JSON line."""
+    import torch
+
+    from soraku_amd import GraphFrameEngine
+    from soraku_amd.config import QWEN3_06B
+    from soraku_amd.synthetic import synthetic_weights
+
+    shape, n = QWEN3_06B, args.utterances
+    t_setup = time.perf_counter()
+    weights = synthetic_weights(shape, args.seed)
+    rng = np.random.default_rng(args.seed + 7)
+    items, kv0 = [], []
+    for _ in range(n):
+        p_len = int(rng.integers(120, 241))
+        n_prompt = int(round(0.6 * p_len))
+        text = rng.integers(0, shape.text_vocab, p_len - 1 - n_prompt)
+        text[0] = TEXT_BOS
+        prompt = rng.integers(0, shape.codebook_size, (n_prompt, shape.n_codebooks))
+        items.append((text, np.array([TEXT_BOS], np.int64), prompt))
+        kv0 += [p_len, n_prompt + 2]
+    u = rng.random((N_FRAMES, n * shape.n_codebooks))
+    dev = torch.device("cuda:0")
+    e = GraphFrameEngine(device=dev, max_cache_len=512, cfg_scale=CFG, batch=2, state_dict=weights, shape=shape,
+                         n_utts=n, bf16=True, max_frames=N_FRAMES)
+    del weights
+    e.set_temperature(TEMP)
+    e.set_sampling(sampled=True, top_k=TOP_K, top_p=TOP_P)
+    t0 = time.perf_counter()
+    e.prefill_utterances(items)
+    t_prefill = time.perf_counter() - t0
+    e.capture()
+    total = args.warmup + args.steps
+    e.queue_frames(u[:total], np.ones(total, np.int32))
+    print(f"# setup {time.perf_counter() - t_setup:.1f}s, prefill of {n} utterances {t_prefill * 1e3:.1f} ms",
+          file=sys.stderr, flush=True)
+    stream = torch.cuda.ExternalStream(e.stream_handle, device=dev)
+    e.replay(args.warmup)
+    e.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    e.replay(args.steps)
+    b.record(stream)
+    e.synchronize()
+    torch.cuda.synchronize(dev)
+    us = a.elapsed_time(b) * 1e3 / args.steps
+    codes = e.read_codes(args.steps)
+    assert codes.min() >= 0 and codes.max() < shape.codebook_size, "decoded a special id"
+    e.close()
+    kv_mid = [k + args.warmup + (args.steps - 1) / 2 for k in kv0]
+    alg = algorithmic_bytes(shape, kv_mid, w_bytes=2)
+    achieved = alg / (us * 1e-6) / 1e9
+    out = {
+        "metric": f"codec frames/sec summed over {n} utterances (CFG, decode batch {2 * n}) + % HBM roofline, "
+                  "1 MI355X",
+        "value": n * 1e6 / us, "unit": "utterance-frames/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": us / 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": (f"throughput batch: {n} synthetic utterances x CFG, Qwen3-0.6B shape, BF16 "
+                                "weights, FP32 KV, ragged prefixes 120-240, KV capacity 512, CFG 1.5, T 0.9, "
+                                "top-k 50, top-p 0.95, seeded uniforms, one hipGraph per frame"),
+                   "global_batch": 2 * n, "seq_len": 512, "parallelism": "none",
+                   "prefill_ms": t_prefill * 1e3},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "unit_of_work": "one frame of every utterance = one hipGraph launch",
+                     "algorithmic_bytes_per_launch": alg},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,6 +227,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--utterances", type=int, default=1,
+                    help="N > 1: the throughput batch of N utterances x CFG (BF16 weights) instead")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 4 device copies of MIB MiB each (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -158,6 +241,9 @@ def main():
         sys.exit(2)
     if args.steps + args.warmup > N_FRAMES:
         sys.exit(f"steps + warmup must be <= {N_FRAMES} (the workload's decoded frames)")
+    if args.utterances > 1:
+        many_utterances(args)
+        return
 
     import torch
 

@@ -97,8 +97,25 @@ int sk_bind_weight(sk_engine* e, const char* key, const void* dev_ptr, int32_t d
  * (the caller includes the BOS frame first, model.py:633-642).  Resets the row. */
 int sk_prefill_row(sk_engine* e, int32_t row, const int64_t* text_ids, int32_t n_text,
                    const int64_t* frame_codes, int32_t n_frames);
-/* Run every staged row through the trunk; leaves per-row hidden and KV length. */
+/* Run every staged row through the trunk; leaves per-row hidden and KV length.
+ * Every row must be staged; the frame counter starts over. */
 int sk_prefill_run(sk_engine* e);
+/* Continuous batching (no counterpart in the reference, which decodes one
+ * utterance's CFG pair, fast_generate.py:232-328): between frames, run only
+ * the rows staged since the last prefill (at least one) through the trunk.
+ * Every other row keeps its cache, length, position and hidden state, and the
+ * frame counter is unchanged, so an utterance slot whose utterance retired
+ * takes the next utterance while the others keep decoding.  The staged rows
+ * become active.  Requires a completed sk_prefill_run. */
+int sk_prefill_refill(sk_engine* e);
+/* Stop decoding one row (no reference counterpart; continuous batching): it
+ * no longer advances its length or position, attention skips it and the
+ * cache-capacity checks ignore it.  Its codes are meaningless until a refill. */
+int sk_retire_row(sk_engine* e, int32_t row);
+/* Restart the frame ring (no reference counterpart): the next frame uses slot
+ * 0 again, so codes of earlier frames can no longer be read with
+ * sk_read_codes.  Lets one engine decode more than max_frames frames in all. */
+int sk_reset_frames(sk_engine* e);
 
 /* Override one row's KV length and RoPE position (after an external prefill). */
 int sk_set_row_state(sk_engine* e, int32_t row, int32_t kv_len, int32_t position);
@@ -123,7 +140,9 @@ int sk_set_debug(sk_engine* e, int32_t record_logits);
  * trunk step) as one hipGraph. */
 int sk_capture(sk_engine* e);
 
-/* Replay one frame.  uniforms: [n_utts][Q] draws in [0,1) (NULL => 0).
+/* Replay one frame.  mask_eos_q0: bit u masks EOS at codebook 0 for
+ * utterance u (the min_new_frames rule, model.py:583-584); with one utterance
+ * 0 or 1.  uniforms: [n_utts][Q] draws in [0,1) (NULL => 0).
  * forced_codes: NULL, or [n_utts][Q] codes to use instead of the sampled ones
  * (teacher forcing).  codes_out: host [n_utts][Q].  logits_dbg: NULL or host
  * [n_utts][Q][V] masked merged logits (needs sk_set_debug(e, 1)).
@@ -132,7 +151,8 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
                   const int64_t* forced_codes, int64_t* codes_out, float* logits_dbg);
 
 /* Throughput path: upload per-frame inputs for the next `n` frames
- * (uniforms [n][n_utts][Q], mask_eos_q0 [n]), then replay `n` frames back to
+ * (uniforms [n][n_utts][Q], mask_eos_q0 [n] utterance bit masks as in
+ * sk_step_frame), then replay `n` frames back to
  * back with no host synchronisation.  sk_read_codes copies codes of the
  * `n` most recent frames ([n][n_utts][Q]). */
 int sk_queue_frames(sk_engine* e, int32_t n, const double* uniforms, const int32_t* mask_eos_q0);

@@ -86,7 +86,9 @@ struct sk_engine {
 
   // host mirrors
   int fc_host = 0;
-  bool prefilled = false;
+  std::vector<int> active_host;   // rows decoding (advance each frame); retired rows do not
+  bool prefilled = false;      // every row holds a prefix; cleared while a row is staged
+  bool ran_full = false;       // an sk_prefill_run has completed (refills may follow)
   std::vector<int> kv_host, len_host;
   std::vector<char> staged;
   SkParams p_host{};
@@ -617,6 +619,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   }
   e->L.resize(c.n_layers);
   e->kv_host.assign(e->rows, 0);
+  e->active_host.assign(e->rows, 0);
   e->len_host.assign(e->rows, 0);
   e->staged.assign(e->rows, 0);
   auto bail = [&](int code) { sk_destroy(e); return code; };
@@ -837,35 +840,77 @@ int sk_prefill_row(sk_engine* e, int32_t row, const int64_t* text_ids, int32_t n
   return SK_OK;
 }
 
-int sk_prefill_run(sk_engine* e) {
-  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
-  for (int r = 0; r < e->rows; ++r) SK_CHECK(e->staged[r], SK_ESTATE, "row %d has no staged prefix", r);
+// Prefill the staged rows.  all: every row must be staged and the frame
+// counter and codebook prefixes start over; otherwise (refill) only the staged
+// rows are touched -- the other rows' caches, lengths and hidden states and
+// the frame counter stay as they are (unstaged rows get length 0 here, which
+// every prefill kernel skips).
+static int prefill_staged(sk_engine* e, bool all) {
+  const int R = e->rows;
+  int n_staged = 0;
+  for (int r = 0; r < R; ++r) {
+    if (all) SK_CHECK(e->staged[r], SK_ESTATE, "row %d has no staged prefix", r);
+    n_staged += e->staged[r] ? 1 : 0;
+  }
+  SK_CHECK(n_staged > 0, SK_ESTATE, "no row has a staged prefix");
   int rc = check_decode_weights(e);
   if (rc != SK_OK) return rc;
-  const int R = e->rows;
-  // Pack the rows' prefix tokens row after row.
-  std::vector<int> row_start(R), tok_row, tok_pos;
+  // Pack the staged rows' prefix tokens row after row.
+  std::vector<int> row_start(R), row_len(R), tok_row, tok_pos;
   int M = 0, max_len = 0;
   for (int r = 0; r < R; ++r) {
     row_start[r] = M;
-    for (int p = 0; p < e->len_host[r]; ++p) { tok_row.push_back(r); tok_pos.push_back(p); }
-    M += e->len_host[r];
-    max_len = e->len_host[r] > max_len ? e->len_host[r] : max_len;
+    row_len[r] = e->staged[r] ? e->len_host[r] : 0;
+    for (int p = 0; p < row_len[r]; ++p) { tok_row.push_back(r); tok_pos.push_back(p); }
+    M += row_len[r];
+    max_len = row_len[r] > max_len ? row_len[r] : max_len;
   }
   const hipError_t ae = ensure_prefill_bufs(e, M);
   SK_CHECK(ae == hipSuccess, SK_EHIP, "prefill buffers for %d tokens: %s", M, hipGetErrorString(ae));
-  SK_HIP(hipMemcpyAsync(e->plen, e->len_host.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->plen, row_len.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemcpyAsync(e->p_row_start, row_start.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemcpyAsync(e->p_tok_row, tok_row.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemcpyAsync(e->p_tok_pos, tok_pos.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
-  SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
-  SK_HIP(hipMemsetAsync(e->prefix2, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
+  if (all) {
+    SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
+    SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
+    SK_HIP(hipMemsetAsync(e->prefix2, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
+  }
   SK_HIP(enqueue_batched_prefill(e, M, max_len));
   SK_HIP(hipStreamSynchronize(e->stream));
-  for (int r = 0; r < R; ++r) { e->kv_host[r] = e->len_host[r]; e->staged[r] = 0; }
-  e->fc_host = 0;
+  for (int r = 0; r < R; ++r)
+    if (e->staged[r]) { e->kv_host[r] = e->len_host[r]; e->active_host[r] = 1; e->staged[r] = 0; }
+  if (all) { e->fc_host = 0; e->ran_full = true; }
   e->prefilled = true;
+  return SK_OK;
+}
+
+int sk_prefill_run(sk_engine* e) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  return prefill_staged(e, true);
+}
+
+int sk_prefill_refill(sk_engine* e) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  SK_CHECK(e->ran_full, SK_ESTATE, "refill before the first sk_prefill_run");
+  return prefill_staged(e, false);
+}
+
+int sk_retire_row(sk_engine* e, int32_t row) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  SK_CHECK(row >= 0 && row < e->rows, SK_EINVAL, "row %d out of range", row);
+  const int zero = 0;
+  SK_HIP(hipMemcpyAsync(e->active + row, &zero, sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipStreamSynchronize(e->stream));
+  e->active_host[row] = 0;
+  return SK_OK;
+}
+
+int sk_reset_frames(sk_engine* e) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
+  SK_HIP(hipStreamSynchronize(e->stream));
+  e->fc_host = 0;
   return SK_OK;
 }
 
@@ -883,6 +928,7 @@ int sk_set_row_state(sk_engine* e, int32_t row, int32_t kv_len, int32_t position
   SK_HIP(hipGetLastError());
   SK_HIP(hipStreamSynchronize(e->stream));
   e->kv_host[row] = kv_len;
+  e->active_host[row] = 1;
   return SK_OK;
 }
 
@@ -946,7 +992,8 @@ static int check_step(sk_engine* e, int n) {
   SK_CHECK(n >= 1, SK_EINVAL, "frame count must be positive");
   SK_CHECK(e->fc_host + n <= e->c.max_frames, SK_EKVFULL, "frame ring full (max_frames=%d)", e->c.max_frames);
   for (int r = 0; r < e->rows; ++r)
-    SK_CHECK(e->kv_host[r] + n <= e->c.max_ctx, SK_EKVFULL, "KV cache full on row %d (max_ctx=%d)", r, e->c.max_ctx);
+    SK_CHECK(!e->active_host[r] || e->kv_host[r] + n <= e->c.max_ctx, SK_EKVFULL,
+             "KV cache full on row %d (max_ctx=%d)", r, e->c.max_ctx);
   return SK_OK;
 }
 
@@ -967,7 +1014,7 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
   const int slot = e->fc_host;
   std::vector<double> u(nq, 0.0);
   if (uniforms) memcpy(u.data(), uniforms, nq * sizeof(double));
-  const int flags[2] = {mask_eos_q0 ? 1 : 0, forced_codes ? 1 : 0};
+  const int flags[2] = {mask_eos_q0, forced_codes ? 1 : 0};
   SK_HIP(hipMemcpyAsync(e->u_ring + slot * nq, u.data(), nq * sizeof(double), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemcpyAsync(e->flag_ring + 2 * slot, flags, sizeof(flags), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemcpyAsync(e->u_cur, u.data(), nq * sizeof(double), hipMemcpyHostToDevice, e->stream));
@@ -981,7 +1028,7 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
     SK_HIP(hipMemcpyAsync(logits_dbg, e->dbg, nq * c.audio_vocab * sizeof(float), hipMemcpyDeviceToHost, e->stream));
   SK_HIP(hipStreamSynchronize(e->stream));
   e->fc_host += 1;
-  for (int r = 0; r < e->rows; ++r) e->kv_host[r] += 1;
+  for (int r = 0; r < e->rows; ++r) e->kv_host[r] += e->active_host[r];
   return SK_OK;
 }
 
@@ -997,7 +1044,7 @@ int sk_queue_frames(sk_engine* e, int32_t n, const double* uniforms, const int32
     memcpy(u.data(), uniforms, u.size() * sizeof(double));
   }
   std::vector<int> flags((size_t)2 * n, 0);
-  for (int i = 0; i < n; ++i) flags[2 * i] = mask_eos_q0 ? (mask_eos_q0[i] ? 1 : 0) : 0;
+  for (int i = 0; i < n; ++i) flags[2 * i] = mask_eos_q0 ? mask_eos_q0[i] : 0;
   SK_HIP(hipStreamSynchronize(e->stream));
   SK_HIP(hipMemcpy(e->u_ring + (size_t)e->fc_host * nq, u.data(), u.size() * sizeof(double), hipMemcpyHostToDevice));
   SK_HIP(hipMemcpy(e->flag_ring + 2 * (size_t)e->fc_host, flags.data(), flags.size() * sizeof(int),
@@ -1012,7 +1059,7 @@ int sk_replay(sk_engine* e, int32_t n) {
   if (rc != SK_OK) return rc;
   for (int i = 0; i < n; ++i) SK_HIP(hipGraphLaunch(e->exec, e->stream));
   e->fc_host += n;
-  for (int r = 0; r < e->rows; ++r) e->kv_host[r] += n;
+  for (int r = 0; r < e->rows; ++r) e->kv_host[r] += n * e->active_host[r];
   return SK_OK;
 }
 

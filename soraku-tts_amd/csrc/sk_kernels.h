@@ -1538,13 +1538,14 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
 }
 
 // CFG merge u + s (c - u) without contraction, then BOS/PAD (and EOS) -> -inf
-// (model.py:579-584); the merged row is optionally recorded, then kept in
+// (model.py:579-584).  EOS is masked when force_mask is set or bit mask_bit
+// (the utterance) of *mask_flag is set.  The merged row is optionally recorded, then kept in
 // registers divided by the temperature when sampling (model.py:696).  Loads
 // are clamped into the row and entries past V become -inf afterwards, so no
 // load sits behind a branch.
 template <int VPT>
 __device__ __forceinline__ void merge_mask(const float* lc, const float* lu, float s, int V, int bos, int eos,
-                                           int pad, const int* mask_flag, bool force_mask, float temp,
+                                           int pad, const int* mask_flag, int mask_bit, bool force_mask, float temp,
                                            float* dbg, float (&xr)[VPT]) {
   float cvv[VPT], uvv[VPT];
 #pragma unroll
@@ -1553,7 +1554,7 @@ __device__ __forceinline__ void merge_mask(const float* lc, const float* lu, flo
     cvv[i] = lc[v];
     uvv[i] = lu ? lu[v] : 0.f;
   }
-  const bool mask_eos = force_mask || (mask_flag && *mask_flag != 0);
+  const bool mask_eos = force_mask || (mask_flag && ((*mask_flag >> mask_bit) & 1));
   const bool divide = temp > 0.f;
   // Chunks below the lowest special id need no mask compares (uniform test).
   const int lo_special = min(min(bos, pad), mask_eos ? min(eos, V) : V);
@@ -1619,7 +1620,7 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   const int topk = q0 ? P.top_k_q0 : P.top_k;
   const float topp = q0 ? P.top_p_q0 : P.top_p;
   float xr[VPT];
-  merge_mask<VPT>(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, a.flag_cur, q != 0, temp,
+  merge_mask<VPT>(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, a.flag_cur, ut, q != 0, temp,
                   P.record_logits ? a.dbg + ((size_t)ut * a.Q + q) * a.V : nullptr, xr);
   int code = sample_core<VPT>(xr, a.V, temp, topk, topp, u, ck, sk, W, s);
   const size_t uoff = ((size_t)slot * a.n_utts + ut) * a.Q + q;
@@ -1666,7 +1667,7 @@ __global__ __launch_bounds__(SNT) void sample_op_kernel(const float* logits, int
   unsigned long long* sk = ck + MAX_V;
   __shared__ SampleSmem s;
   float xr[VPT];
-  merge_mask<VPT>(logits, rows == 2 ? logits + V : nullptr, cfg, V, bos, eos, pad, nullptr,
+  merge_mask<VPT>(logits, rows == 2 ? logits + V : nullptr, cfg, V, bos, eos, pad, nullptr, 0,
                   (q != 0) || mask_eos_q0 != 0, temp, nullptr, xr);
   const int code = sample_core<VPT>(xr, V, temp, top_k, top_p, u, ck, sk, W, s);
   if (threadIdx.x == 0) *code_out = code;

@@ -415,6 +415,7 @@ __global__ __launch_bounds__(NT) void pf_finish_kernel(const float* X, const int
   __shared__ float red[WAVES];
   const int r = blockIdx.x;
   const int n = len[r];
+  if (n == 0) return;                    // not in this prefill: the row keeps its state
   const float* xr = X + (size_t)(row_start[r] + n - 1) * D;
   float s = 0.f;
   for (int k = threadIdx.x; k < D; k += NT) s += xr[k] * xr[k];

@@ -185,6 +185,26 @@ class GraphFrameEngine:
         With several utterances, every utterance gets this prefix."""
         return self.prefill_utterances([(cond_ids, uncond_ids, prompt_codes)] * self.n_utts)
 
+    def _stage(self, u, cond_ids, uncond_ids, prompt_codes):
+        """Stage utterance slot ``u``'s rows (cond, and uncond with CFG)."""
+        def ids_of(x):
+            return np.asarray(x.cpu() if hasattr(x, "cpu") else x, np.int64).reshape(-1)
+
+        cond = ids_of(cond_ids)
+        rows = [cond]
+        if self.batch == 2:
+            uncond = ids_of(uncond_ids) if uncond_ids is not None else cond
+            if uncond.size > cond.size:
+                raise ValueError("uncond text is longer than cond")
+            rows.append(uncond)
+        frames = self._frames(prompt_codes)
+        for b, ids in enumerate(rows):
+            n = ids.size + frames.shape[0]
+            if n > self.max_len:
+                raise ValueError(f"prefill {n} exceeds max_cache_len={self.max_len}")
+            check(lib().sk_prefill_row(self._h, u * self.batch + b, _i64(ids), ids.size,
+                                       _i64(np.ascontiguousarray(frames)), frames.shape[0]))
+
     def prefill_utterances(self, items):
         """Several utterances, each with its own prefix: ``items`` holds
         ``(cond_ids, uncond_ids, prompt_codes)`` per utterance (ragged lengths
@@ -192,28 +212,48 @@ class GraphFrameEngine:
         depth-input hidden ``[rows, d]``."""
         import torch
 
-        def ids_of(x):
-            return np.asarray(x.cpu() if hasattr(x, "cpu") else x, np.int64).reshape(-1)
-
         if len(items) != self.n_utts:
             raise ValueError(f"{len(items)} prefixes for {self.n_utts} utterances")
         for u, (cond_ids, uncond_ids, prompt_codes) in enumerate(items):
-            cond = ids_of(cond_ids)
-            rows = [cond]
-            if self.batch == 2:
-                uncond = ids_of(uncond_ids) if uncond_ids is not None else cond
-                if uncond.size > cond.size:
-                    raise ValueError("uncond text is longer than cond")
-                rows.append(uncond)
-            frames = self._frames(prompt_codes)
-            for b, ids in enumerate(rows):
-                n = ids.size + frames.shape[0]
-                if n > self.max_len:
-                    raise ValueError(f"prefill {n} exceeds max_cache_len={self.max_len}")
-                check(lib().sk_prefill_row(self._h, u * self.batch + b, _i64(ids), ids.size,
-                                           _i64(np.ascontiguousarray(frames)), frames.shape[0]))
+            self._stage(u, cond_ids, uncond_ids, prompt_codes)
         check(lib().sk_prefill_run(self._h))
         return torch.from_numpy(self.hidden()).to(self.device)
+
+    # ---- continuous batching (no reference counterpart beyond one CFG pair) ----
+    def refill(self, items: dict) -> None:
+        """Between frames, give utterance slots new utterances: ``items`` maps
+        slot -> ``(cond_ids, uncond_ids, prompt_codes)``.  Only those slots'
+        rows are prefilled; every other slot keeps decoding where it was."""
+        if not items:
+            return
+        for u, (cond_ids, uncond_ids, prompt_codes) in items.items():
+            if not 0 <= u < self.n_utts:
+                raise ValueError(f"slot {u} outside [0, {self.n_utts})")
+            self._stage(u, cond_ids, uncond_ids, prompt_codes)
+        check(lib().sk_prefill_refill(self._h))
+
+    def retire(self, u: int) -> None:
+        """Stop decoding utterance slot ``u`` (its rows no longer advance)."""
+        if not 0 <= u < self.n_utts:
+            raise ValueError(f"slot {u} outside [0, {self.n_utts})")
+        for b in range(self.batch):
+            check(lib().sk_retire_row(self._h, u * self.batch + b))
+
+    def reset_frames(self) -> None:
+        """Restart the frame ring (codes of earlier frames become unreadable)."""
+        check(lib().sk_reset_frames(self._h))
+
+    def eos_mask_bits(self, mask) -> int:
+        """EOS-at-q0 mask as the engine's per-utterance bits: a bool applies to
+        every utterance, a sequence of n_utts bools gives one per utterance."""
+        if np.ndim(mask) == 0:
+            bits = (1 << self.n_utts) - 1 if bool(mask) else 0
+        else:
+            m = np.asarray(mask, bool).reshape(-1)
+            if m.size != self.n_utts:
+                raise ValueError(f"EOS mask of {m.size} utterances for {self.n_utts}")
+            bits = sum(1 << i for i in range(self.n_utts) if m[i])
+        return int(np.array(bits, np.uint32).view(np.int32))
 
     def hidden(self) -> np.ndarray:
         out = np.empty((self.rows, self.d_model), np.float32)
@@ -227,10 +267,11 @@ class GraphFrameEngine:
         check(lib().sk_capture(self._h))
         self.graph = True
 
-    def step_frame(self, *, mask_eos_q0: bool, uniforms=None, forced_codes=None,
+    def step_frame(self, *, mask_eos_q0, uniforms=None, forced_codes=None,
                    return_logits: bool = False):
         """One replay; returns this frame's codes as a CPU LongTensor ``[Q]``
-        (``[n_utts, Q]`` for several utterances), graph_frame.py:298-305."""
+        (``[n_utts, Q]`` for several utterances), graph_frame.py:298-305.
+        ``mask_eos_q0``: a bool (every utterance) or one bool per utterance."""
         import torch
 
         if self.graph is None:
@@ -245,7 +286,7 @@ class GraphFrameEngine:
         codes = np.empty(nq, np.int64)
         logits = np.empty((self.n_utts, self.Q, self.V), np.float32) if return_logits else None
         check(lib().sk_step_frame(
-            self._h, int(bool(mask_eos_q0)), u.ctypes.data_as(C.POINTER(C.c_double)),
+            self._h, self.eos_mask_bits(mask_eos_q0), u.ctypes.data_as(C.POINTER(C.c_double)),
             _i64(fc) if fc is not None else None, _i64(codes),
             logits.ctypes.data_as(C.POINTER(C.c_float)) if logits is not None else None))
         out = torch.from_numpy(codes.reshape(self.n_utts, self.Q))
@@ -255,9 +296,16 @@ class GraphFrameEngine:
 
     # ---- throughput path: many frames without host synchronisation -------
     def queue_frames(self, uniforms: np.ndarray, mask_eos_q0: np.ndarray) -> None:
-        n = int(np.asarray(mask_eos_q0).size)
+        """``mask_eos_q0``: ``[n]`` (one flag per frame, for every utterance)
+        or ``[n, n_utts]`` (per utterance)."""
+        mk = np.asarray(mask_eos_q0)
+        if mk.ndim == 2:
+            bits = [self.eos_mask_bits(row) for row in mk]
+        else:
+            bits = [self.eos_mask_bits(bool(x)) for x in mk.reshape(-1)]
+        n = len(bits)
         u = np.ascontiguousarray(np.asarray(uniforms, np.float64).reshape(n, self.n_utts * self.Q))
-        m = np.ascontiguousarray(np.asarray(mask_eos_q0, np.int32).reshape(n))
+        m = np.ascontiguousarray(np.array(bits, np.int32))
         check(lib().sk_queue_frames(self._h, n, u.ctypes.data_as(C.POINTER(C.c_double)),
                                     m.ctypes.data_as(C.POINTER(C.c_int32))))
 

@@ -125,18 +125,20 @@ class FastGenerator:
                        temperature: float = 0.9, top_k: int | None = 50, top_p: float | None = 0.95,
                        temperature_q0: float | None = None, top_k_q0: int | None = None,
                        top_p_q0: float | None = None, cfg_scale: float = 1.0, seeds=None, uniforms=None,
-                       on_frame: Any = None):
-        """Several utterances decoded together (one engine, ``len(requests)``
-        x CFG rows; no reference counterpart beyond one utterance's CFG pair,
-        fast_generate.py:232-328).  ``requests``: dicts with ``input_ids``
-        ``[1, L]`` and optional ``prompt_codes`` / ``uncond_input_ids``;
-        prefixes may differ in length.  Utterance u draws from
-        ``uniforms[u]`` (``[max_new_frames, Q]``) or from
-        ``default_rng(seeds[u])`` exactly as ``generate(seed=seeds[u])`` would,
-        and retires at its own EOS (q0 code == EOS once ``index >=
-        min_new_frames``): later frames of a retired utterance are dropped, and
-        the batch stops when every utterance has retired or at
-        ``max_new_frames``.  Returns a list of ``(codes [T_u, Q], info)``."""
+                       on_frame: Any = None, max_batch: int | None = None):
+        """Several utterances decoded together (one engine, up to 16 utterance
+        slots with CFG, 32 without; no reference counterpart beyond one
+        utterance's CFG pair, fast_generate.py:232-328).  ``requests``: dicts
+        with ``input_ids`` ``[1, L]`` and optional ``prompt_codes`` /
+        ``uncond_input_ids``; prefixes may differ in length.  Request i draws
+        from ``uniforms[i]`` (``[max_new_frames, Q]``) or from
+        ``default_rng(seeds[i])`` exactly as ``generate(seed=seeds[i])``
+        would, is decoded with its own frame index (EOS masked at q0 for its
+        first ``min_new_frames`` frames) and retires at its own EOS or at
+        ``max_new_frames``.  ``max_batch`` caps the slots; with more requests
+        than slots, a slot whose request retires takes the next request
+        between frames (continuous batching: only that slot is prefilled).
+        Returns a list of ``(codes [T_i, Q], info)`` in request order."""
         import torch
 
         U = len(requests)
@@ -145,6 +147,10 @@ class FastGenerator:
         if cfg_scale != 1.0 and any(r.get("uncond_input_ids") is None for r in requests):
             raise ValueError("classifier-free guidance requires uncond_input_ids")
         batch = 2 if cfg_scale != 1.0 else 1
+        cap = 32 // batch
+        slots = min(U, max_batch if max_batch is not None else cap)
+        if not 1 <= slots <= cap:
+            raise ValueError(f"max_batch must be in [1, {cap}]")
         Qn = self._shape.n_codebooks if self._shape else 16
         longest = 0
         for r in requests:
@@ -155,7 +161,7 @@ class FastGenerator:
             pc = r.get("prompt_codes")
             n_prompt = 0 if pc is None else int(np.prod(pc.shape)) // Qn
             longest = max(longest, int(shape[1]) + 1 + n_prompt)
-        engine = self._engine_for(longest + max_new_frames + 8, batch, cfg_scale, n_utts=U)
+        engine = self._engine_for(longest + max_new_frames + 8, batch, cfg_scale, n_utts=slots)
         Q = engine.Q
         engine.cfg.fill_(cfg_scale)
         sampled = temperature > 0 or (temperature_q0 is not None and temperature_q0 > 0)
@@ -168,33 +174,54 @@ class FastGenerator:
         uniforms = np.asarray(uniforms, np.float64).reshape(U, -1, Q)
         if uniforms.shape[1] < max_new_frames:
             raise ValueError("uniforms must cover max_new_frames rows per utterance")
-        engine.prefill_utterances([(r["input_ids"], r.get("uncond_input_ids") if batch == 2 else None,
-                                    r.get("prompt_codes")) for r in requests])
+
+        def item(i):
+            r = requests[i]
+            return (r["input_ids"], r.get("uncond_input_ids") if batch == 2 else None, r.get("prompt_codes"))
+
+        engine.prefill_utterances([item(i) for i in range(slots)])
         if engine.graph is None:
             engine.capture()
         eos = engine.shape.eos_id
+        slot_req = list(range(slots))          # request decoded in each slot (None: idle)
+        slot_idx = [0] * slots                 # that request's frame index
+        next_req = slots
         frames: list[list] = [[] for _ in range(U)]
         reason = ["max_frames"] * U
-        live = [True] * U
-        for index in range(max_new_frames):
-            codes = engine.step_frame(mask_eos_q0=index < min_new_frames,
-                                      uniforms=np.ascontiguousarray(uniforms[:, index]))
-            codes = codes.view(U, Q)
-            for u in range(U):
-                if not live[u]:
+        while any(i is not None for i in slot_req):
+            if engine.frames_done + 1 > engine.max_frames:
+                engine.reset_frames()
+            mask = [i is not None and slot_idx[s] < min_new_frames for s, i in enumerate(slot_req)]
+            u = np.zeros((slots, Q))
+            for s, i in enumerate(slot_req):
+                if i is not None:
+                    u[s] = uniforms[i, slot_idx[s]]
+            codes = engine.step_frame(mask_eos_q0=mask, uniforms=u).view(slots, Q)
+            refill = {}
+            for s, i in enumerate(slot_req):
+                if i is None:
                     continue
-                if index >= min_new_frames and int(codes[u, 0]) == eos:
-                    live[u] = False
-                    reason[u] = "eos"
-                    continue
-                frames[u].append(codes[u].clone().view(1, Q))
-                if on_frame is not None:
-                    on_frame(u, frames[u][-1])
-            if not any(live):
-                break
+                if slot_idx[s] >= min_new_frames and int(codes[s, 0]) == eos:
+                    reason[i] = "eos"
+                    done = True
+                else:
+                    frames[i].append(codes[s].clone().view(1, Q))
+                    if on_frame is not None:
+                        on_frame(i, frames[i][-1])
+                    slot_idx[s] += 1
+                    done = slot_idx[s] >= max_new_frames
+                if done:
+                    if next_req < U:
+                        refill[s] = item(next_req)
+                        slot_req[s], slot_idx[s] = next_req, 0
+                        next_req += 1
+                    else:
+                        slot_req[s] = None
+                        engine.retire(s)
+            engine.refill(refill)
         out = []
-        for u in range(U):
-            c = torch.cat(frames[u], dim=0) if frames[u] else torch.empty(0, Q, dtype=torch.long)
-            out.append((c, {"stop_reason": reason[u], "num_frames": c.shape[0], "cfg_scale": cfg_scale,
+        for i in range(U):
+            c = torch.cat(frames[i], dim=0) if frames[i] else torch.empty(0, Q, dtype=torch.long)
+            out.append((c, {"stop_reason": reason[i], "num_frames": c.shape[0], "cfg_scale": cfg_scale,
                             "backend": "mi355x", "sampled": sampled, "temperature": temperature}))
         return out

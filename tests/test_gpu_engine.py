@@ -539,6 +539,47 @@ def test_generate_batch_per_utterance_equals_oracle(hip_device):
     assert sorted(o[1]["stop_reason"] for o in out) == ["eos", "eos", "max_frames"]
 
 
+@pytest.mark.parametrize("max_batch", [2, 3])
+def test_generate_batch_continuous_refill(hip_device, max_batch):
+    """Continuous batching: seven requests through 2 or 3 utterance slots (4
+    rows: GEMV path; 6 rows: skinny-GEMM path).  A slot whose request retires
+    (EOS or max_new_frames) is prefilled with the next request between frames
+    while the other slots keep decoding; a refilled request starts at its own
+    frame 0, so EOS is masked for it alone during its first min_new_frames.
+    Every request's codes and stop reason equal the float64 oracle's run of
+    that request alone."""
+    import torch
+    from soraku_amd import FastGenerator
+
+    f, s, gen = load_golden("tiny_sampled")
+    w = _weights(f, s)
+    w["depth_head.bias"] = w["depth_head.bias"].copy()
+    w["depth_head.bias"][0, s.eos_id] += 0.2      # staggered retirement: EOS or max_new_frames
+    lang = tuple(int(v) for v in f["language_ids"])
+    n_frames = 5
+    kw = {k: v for k, v in gen.items() if k not in ("seed", "max_new_frames")}
+    rng = np.random.default_rng(41)
+    reqs, us = [], []
+    for i in range(7):
+        nt = 3 + 3 * (i % 4)
+        reqs.append(dict(input_ids=torch.tensor(rng.integers(0, s.text_vocab, nt)[None]),
+                         prompt_codes=torch.tensor(rng.integers(0, s.codebook_size, (i % 3, s.n_codebooks))),
+                         uncond_input_ids=torch.tensor(f["uncond_ids"][None])))
+        us.append(rng.random((n_frames, s.n_codebooks)))
+    g = FastGenerator(device=hip_device, state_dict=w, shape=_shape(s), language_token_ids=lang)
+    out = g.generate_batch(reqs, max_new_frames=n_frames, uniforms=np.stack(us), max_batch=max_batch, **kw)
+    m = OracleModel(s, w, np.float64, language_token_ids=lang)
+    for r, u, (codes, info) in zip(reqs, us, out):
+        ref, rinfo = generate(m, input_ids=r["input_ids"].numpy()[0], prompt_codes=r["prompt_codes"].numpy(),
+                              uncond_input_ids=r["uncond_input_ids"].numpy()[0], uniforms=u, batched=True,
+                              max_new_frames=n_frames, **kw)
+        np.testing.assert_array_equal(codes.numpy(), ref)
+        assert info["stop_reason"] == rinfo["stop_reason"]
+    reasons = [o[1]["stop_reason"] for o in out]
+    print(f"max_batch {max_batch}: stop reasons {reasons}, frames {[o[1]['num_frames'] for o in out]}")
+    assert "eos" in reasons and "max_frames" in reasons
+
+
 def test_from_pretrained_release_untied_head(hip_device, tmp_path):
     """A release directory (config gate, text config, model.safetensors) with
     an untied classifier head and four language tokens, loaded by

@@ -14,6 +14,11 @@ so all K frames run (the work per frame does not depend on it).
 Prints one JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one
 GPU (utterances shard across GPUs with no per-frame exchange).
 
+``--model q17b`` runs the larger-backbone workload instead: Qwen3-1.7B shape
+(hidden 2048, SwiGLU 6144) with BF16 weights (FP32 KV and accumulation), 95
+text ids + BOS frame + 144 prompt frames (240 positions), 480 decoded frames,
+same sampling.
+
 ``--utterances N`` (N > 1) runs the throughput batch instead: N synthetic
 utterances with CFG decoded together (decode batch 2N) at Qwen3-0.6B shape
 with BF16 weights (FP32 KV cache and accumulation); each prefix is 120-240
@@ -47,13 +52,13 @@ CFG, TEMP, TOP_K, TOP_P = 1.5, 0.9, 50, 0.95
 TEXT_BOS = 151643
 
 
-def workload_inputs(shape, seed=0):
+def workload_inputs(shape, seed=0, n_text=N_TEXT, n_prompt=N_PROMPT, n_frames=N_FRAMES):
     from soraku_amd.synthetic import utterance
 
-    text, prompt = utterance(shape, seed + 100, n_text=N_TEXT, n_prompt=N_PROMPT)
+    text, prompt = utterance(shape, seed + 100, n_text=n_text, n_prompt=n_prompt)
     text[0] = TEXT_BOS
     uncond = np.array([TEXT_BOS], np.int64)
-    u = np.random.default_rng(seed + 1).random((N_FRAMES, shape.n_codebooks))
+    u = np.random.default_rng(seed + 1).random((n_frames, shape.n_codebooks))
     return text, prompt, uncond, u
 
 
@@ -227,6 +232,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--model", choices=("q06b", "q17b"), default="q06b",
+                    help="q17b: Qwen3-1.7B shape with BF16 weights, 240-position prefix, 480 frames")
     ap.add_argument("--utterances", type=int, default=1,
                     help="N > 1: the throughput batch of N utterances x CFG (BF16 weights) instead")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -239,8 +246,10 @@ def main():
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): utterances shard across GPUs "
               "with no per-frame exchange, so the per-GPU figure is the N=1 line.", file=sys.stderr)
         sys.exit(2)
-    if args.steps + args.warmup > N_FRAMES:
-        sys.exit(f"steps + warmup must be <= {N_FRAMES} (the workload's decoded frames)")
+    big = args.model == "q17b"
+    n_text, n_prompt, n_frames = (95, 144, 480) if big else (N_TEXT, N_PROMPT, N_FRAMES)
+    if args.steps + args.warmup > n_frames:
+        sys.exit(f"steps + warmup must be <= {n_frames} (the workload's decoded frames)")
     if args.utterances > 1:
         many_utterances(args)
         return
@@ -248,17 +257,17 @@ def main():
     import torch
 
     from soraku_amd import GraphFrameEngine
-    from soraku_amd.config import QWEN3_06B
+    from soraku_amd.config import QWEN3_06B, QWEN3_17B
     from soraku_amd.synthetic import synthetic_weights
 
-    shape = QWEN3_06B
+    shape = QWEN3_17B if big else QWEN3_06B
     t_setup = time.perf_counter()
     weights = synthetic_weights(shape, args.seed)
-    text, prompt, uncond, u = workload_inputs(shape, args.seed)
+    text, prompt, uncond, u = workload_inputs(shape, args.seed, n_text, n_prompt, n_frames)
     dev = torch.device("cuda:0")
-    max_ctx = text.size + 1 + prompt.shape[0] + N_FRAMES + 8
+    max_ctx = text.size + 1 + prompt.shape[0] + n_frames + 8
     e = GraphFrameEngine(device=dev, max_cache_len=max_ctx, cfg_scale=CFG, batch=2,
-                         state_dict=weights, shape=shape, max_frames=N_FRAMES)
+                         state_dict=weights, shape=shape, max_frames=n_frames, bf16=big)
     e.set_temperature(TEMP)
     e.set_sampling(sampled=True, top_k=TOP_K, top_p=TOP_P)
     t0 = time.perf_counter()
@@ -289,29 +298,34 @@ def main():
 
     us = total_ms * 1e3 / args.steps
     kv_mid = [k + args.warmup + (args.steps - 1) / 2 for k in kv0]
-    alg = algorithmic_bytes(shape, kv_mid)
+    alg = algorithmic_bytes(shape, kv_mid, w_bytes=2 if big else 4)
     achieved = alg / (us * 1e-6) / 1e9
+    workload = ("larger backbone, Qwen3-1.7B shape, BF16 weights (FP32 KV and accumulation): 95 text ids + "
+                "144 prompt frames (240 positions), 480 frames, CFG 1.5, T 0.9, top-k 50, top-p 0.95, "
+                "seeded uniforms, one hipGraph per frame") if big else (
+                "full synthetic utterance, Qwen3-0.6B shape FP32: 96 text ids + "
+                "144 prompt frames, CFG 1.5, T 0.9, top-k 50, top-p 0.95, seeded "
+                "uniforms, one hipGraph per frame")
     out = {
         "metric": METRIC, "value": 1e6 / us, "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": us / 1e3, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": ("full synthetic utterance, Qwen3-0.6B shape FP32: 96 text ids + "
-                                "144 prompt frames, CFG 1.5, T 0.9, top-k 50, top-p 0.95, seeded "
-                                "uniforms, one hipGraph per frame"),
-                   "global_batch": 2, "seq_len": int(kv0[0] + N_FRAMES), "parallelism": "none",
+        "vs_baseline": None, "dtype": "bf16" if big else "f32", "data": "synthetic",
+        "config": {"workload": workload,
+                   "global_batch": 2, "seq_len": int(kv0[0] + n_frames), "parallelism": "none",
                    "us_per_frame_median": float(np.median(per)),
                    "us_per_frame_p90": float(np.percentile(per, 90)),
                    "prefill_ms": t_prefill * 1e3},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(),
-                     "traffic_source": "profiles/hbm_traffic_decode_frame_q06b_f32.md (rocprofv3 "
-                                       "FETCH_SIZE + WRITE_SIZE, copy-calibrated, bytes per frame)",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None if big else measured_traffic(),
+                     "traffic_source": None if big else (
+                         "profiles/hbm_traffic_decode_frame_q06b_f32.md (rocprofv3 "
+                         "FETCH_SIZE + WRITE_SIZE, copy-calibrated, bytes per frame)"),
                      "unit_of_work": "one frame = one hipGraph launch",
                      "algorithmic_bytes_per_launch": alg},
     }
     e.close()
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(shape, weights, text, prompt, uncond, u)
+        out["cpu_baseline"] = cpu_baseline(shape, weights, text, prompt, uncond, u, n_frames=3 if big else 6)
         out["cpu_baseline"]["speedup"] = out["value"] / out["cpu_baseline"]["value"]
     print(json.dumps(out))
 

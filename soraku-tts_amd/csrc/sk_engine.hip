@@ -359,15 +359,6 @@ hipError_t enqueue_depth_wide(sk_engine* e, int q) {
   const int d = c.d_model, M = e->rows, V = c.audio_vocab, wt = c.weight_dtype;
   const size_t tsz = (wt == SK_BF16) ? 2 : 4;
   hipError_t err;
-  if (wt == SK_BF16)
-    hipLaunchKernelGGL(depth_in_kernel<WBF16>, dim3(M), dim3(NT), 0, e->stream, e->hidden, e->prefix, e->table,
-                       e->codes_cur, q, c.n_codebooks, V, d, c.frame_scale, c.cfg_rows, e->d_norm_in, c.depth_eps,
-                       e->abuf, e->xs_abuf);
-  else
-    hipLaunchKernelGGL(depth_in_kernel<WF32>, dim3(M), dim3(NT), 0, e->stream, e->hidden, e->prefix, e->table,
-                       e->codes_cur, q, c.n_codebooks, V, d, c.frame_scale, c.cfg_rows, e->d_norm_in, c.depth_eps,
-                       e->abuf, e->xs_abuf);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
   const bool xs = e->xs_abuf != nullptr;
   SkinnyArgs k = skinny_args(e->d_gate, c.depth_inner, d, e->abuf, d, e->act, e->inner_max, M);
   k.w2 = e->d_up;
@@ -397,10 +388,18 @@ hipError_t enqueue_frame(sk_engine* e) {
   s.codes_ring = e->codes_ring; s.codes_cur = e->codes_cur; s.dbg = e->dbg; s.table = e->table;
   s.prefix = e->prefix; s.xnext = e->x; s.d = d; s.Q = c.n_codebooks; s.scale = c.frame_scale;
   s.bos = c.bos_id; s.eos = c.eos_id; s.pad = c.pad_id; s.n_utts = c.n_utts;
-  // Codebook prefix: step 0 reads `prefix` (all zero); step q >= 1 reads the
-  // previous step's prefix, adds the embedding of code q-1 and writes the
-  // result to the other buffer of the pair (readers of one launch never see
-  // its own writes).  The last sampler launch zeroes `prefix` again.
+  // Depth step inputs.  Many rows: step 0's abuf = RMSNorm_in(hidden) comes
+  // from the trunk's final norm (or the prefill), and the sampler launch of
+  // step q advances its rows' codebook prefix with code q and writes step
+  // q+1's abuf -- no separate launch.  Few rows: the gate/up GEMV's prologue
+  // forms it; step q >= 1 reads the previous step's prefix, adds the embedding
+  // of code q-1 and writes the result to the other buffer of the pair (readers
+  // of one launch never see its own writes).  Either way the last sampler
+  // launch writes the frame embedding and zeroes `prefix` again.
+  if (e->wide) {
+    s.hidden = e->hidden; s.w_in = e->d_norm_in; s.eps_in = c.depth_eps;
+    s.abuf = e->abuf; s.xs_abuf = e->xs_abuf;
+  }
   for (int q = 0; q < c.n_codebooks; ++q) {
     if (e->wide) {
       if ((err = enqueue_depth_wide(e, q)) != hipSuccess) return err;
@@ -409,6 +408,8 @@ hipError_t enqueue_frame(sk_engine* e) {
       if (err != hipSuccess) return err;
       continue;
     }
+    // The depth input is formed in the gate/up GEMV's prologue, which loads
+    // the gathered table row of code q-1 behind its own weight stream.
     GemvArgs a = gemv_args(e->d_gate, c.depth_inner, d, e->hidden, d, e->act, e->inner_max);
     a.w[1] = e->d_up; a.ldx2 = d;
     a.norm_w = e->d_norm_in; a.eps = c.depth_eps; a.norm_out = e->abuf; a.ldno = d;
@@ -441,7 +442,8 @@ hipError_t enqueue_frame(sk_engine* e) {
   hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x, e->final_norm,
                      c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->fc, e->u_ring,
                      e->flag_ring, e->u_cur, e->flag_cur, c.n_utts * c.n_codebooks, c.max_frames,
-                     e->inv_freq, c.head_dim / 2, e->rope, (const float2*)e->p_rope, c.max_ctx + 1);
+                     e->inv_freq, c.head_dim / 2, e->rope, (const float2*)e->p_rope, c.max_ctx + 1,
+                     e->d_norm_in, c.depth_eps, e->wide ? e->abuf : nullptr, e->xs_abuf);
   return hipGetLastError();
 }
 
@@ -552,7 +554,7 @@ hipError_t enqueue_batched_prefill(sk_engine* e, int M, int max_len) {
   }
   hipLaunchKernelGGL(pf_finish_kernel, dim3(e->rows), dim3(NT), 0, st, e->pX, e->p_row_start, e->plen,
                      e->final_norm, c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->inv_freq, hd / 2,
-                     e->rope);
+                     e->rope, e->d_norm_in, c.depth_eps, e->abuf, e->xs_abuf);
   return hipGetLastError();
 }
 

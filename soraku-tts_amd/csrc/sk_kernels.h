@@ -1585,13 +1585,68 @@ struct SampleArgs {
   int d, Q; float scale;
   int bos, eos, pad;
   int n_utts;
+  // Next depth step's input (q < Q-1): abuf = RMSNorm_in(hidden + prefix) per
+  // row, and its split form for the many-row GEMMs (xs_abuf, may be null).
+  const float* hidden; const float* w_in; float eps_in;
+  float* abuf; uint16_t* xs_abuf;
 };
 
+// The depth input rows of one utterance after its code q (sample_step_kernel,
+// SNT threads): prefix += table[q][code] * scale, x = hidden + prefix,
+// abuf = w_in * (x * inv_rms(x)); the loads are issued together once the code
+// is known (all threads hold it).
+constexpr int DEPTH_DPT = 8;             // d <= SNT * DEPTH_DPT
+template <typename TL>
+__device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, int q, int code) {
+  __shared__ float red[2][SWAVES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t trow = ((size_t)q * a.V + code) * a.d;
+  float xv[2][DEPTH_DPT];
+  for (int rr = 0; rr < a.rows_per_utt; ++rr) {
+    const size_t ro = (size_t)(r0 + rr) * a.d;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < DEPTH_DPT; ++i) {
+      const int k = tid + i * SNT;
+      xv[rr][i] = 0.f;
+      if (k < a.d) {
+        const float p = __fadd_rn(a.prefix[ro + k], __fmul_rn(TL::get(a.table, trow + k), a.scale));
+        a.prefix[ro + k] = p;
+        const float x = __fadd_rn(a.hidden[ro + k], p);
+        xv[rr][i] = x;
+        ss = fmaf(x, x, ss);
+      }
+    }
+    ss = wave_sum_dpp(ss);
+    if (lane == 0) red[rr][wave] = ss;
+  }
+  __syncthreads();
+  for (int rr = 0; rr < a.rows_per_utt; ++rr) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < SWAVES; ++w) t += red[rr][w];
+    const float inv = 1.0f / sqrtf(t / (float)a.d + a.eps_in);
+    const size_t ro = (size_t)(r0 + rr) * a.d;
+#pragma unroll
+    for (int i = 0; i < DEPTH_DPT; ++i) {
+      const int k = tid + i * SNT;
+      if (k < a.d) {
+        const float y = a.w_in[k] * (xv[rr][i] * inv);
+        a.abuf[ro + k] = y;
+        if (a.xs_abuf) xsplit_store(a.xs_abuf, r0 + rr, k, y);
+      }
+    }
+  }
+}
+
 // One workgroup per utterance, launched once per codebook q.  Samples the
-// code and records it; the next depth step's first GEMV advances the prefix
-// with it (model.py:600-605).  After the last codebook it writes the frame
-// embedding (model.py:105-114) as the next trunk input and clears the prefix
-// the next frame starts from.  Every input that does not depend on the code
+// code and records it.  Before the last codebook it advances the rows' prefix
+// with it (prefix += table[q][code] / sqrt(Q), model.py:600-605) and writes the
+// next depth step's input, abuf = RMSNorm_in(hidden + prefix) (eps
+// FLT_EPSILON) -- the depth MLP input and its residual -- so the depth GEMVs
+// take it ready-made.  After the last codebook it writes the frame embedding
+// (model.py:105-114) as the next trunk input and clears the prefix the next
+// frame starts from.  Every input that does not depend on the code
 // is loaded in the first round trip (this frame's draws and flags sit at
 // fixed addresses, so nothing waits on the frame counter).  VPT = logits per
 // thread, ceil(V / SNT).
@@ -1631,7 +1686,13 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
     a.codes_cur[(size_t)ut * a.Q + q] = code;
     codes_l[q] = code;
   }
-  if (!last) return;
+  if (!last) {
+    if (a.abuf) {
+      __syncthreads();                   // codes_l[q] from thread 0
+      depth_input_rows<TL>(a, r0, q, codes_l[q]);
+    }
+    return;
+  }
 
   __syncthreads();
   const size_t row_stride = (size_t)a.V * a.d;
@@ -1696,43 +1757,80 @@ __global__ __launch_bounds__(NT) void rope_rows_kernel(const int* pos, const flo
 // Final trunk norm + per-row step bookkeeping after a decode trunk step: every
 // active row advances its length and position (and its RoPE (cos, sin) to the
 // new position), the frame counter moves on and the next frame's draws and flags
-// are copied from the ring to the fixed current-frame slots.
+// are copied from the ring to the fixed current-frame slots.  With abuf set it
+// also writes depth step 0's input, RMSNorm_in(hidden) (the codebook prefix is
+// zero when a frame starts), and its split form when xs_abuf is set.
 __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const float* w, float eps,
                                                         int D, float* hidden, int* kv_len, int* pos,
                                                         const int* active, int* counter,
                                                         const double* u_ring, const int* flag_ring,
                                                         double* u_cur, int* flag_cur, int nq,
                                                         int max_frames, const float* inv_freq, int half,
-                                                        float2* rope, const float2* rope_tab, int tab_n) {
+                                                        float2* rope, const float2* rope_tab, int tab_n,
+                                                        const float* w_in, float eps_in, float* abuf,
+                                                        uint16_t* xs_abuf) {
   __shared__ float red[WAVES];
   const int b = blockIdx.x;
   const int p0 = pos[b];                 // read by every thread before the barrier in block_sum
   if (active[b]) {
     const float* xr = x + (size_t)b * D;
+    const size_t ro = (size_t)b * D;
     constexpr int PER = 16;              // D <= 4096 in registers, all loads issued at once
     if (D <= NT * PER) {
-      float xv[PER], wv[PER];
+      float xv[PER], wv[PER], gv[PER];
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int k = min((int)threadIdx.x + i * NT, D - 1);
         xv[i] = xr[k];
         wv[i] = w[k];
+        gv[i] = abuf ? w_in[k] : 0.f;
       }
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < PER; ++i)
         if ((int)threadIdx.x + i * NT < D) s += xv[i] * xv[i];
       const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
+      float s2 = 0.f;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int k = threadIdx.x + i * NT;
-        if (k < D) hidden[(size_t)b * D + k] = wv[i] * (xv[i] * inv);
+        xv[i] = wv[i] * (xv[i] * inv);
+        if (k < D) {
+          hidden[ro + k] = xv[i];
+          s2 = fmaf(xv[i], xv[i], s2);
+        }
+      }
+      // Depth step 0's input: the prefix is zero at the start of a frame.
+      if (abuf) {
+        const float inv2 = 1.0f / sqrtf(block_sum(s2, red) / (float)D + eps_in);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int k = threadIdx.x + i * NT;
+          if (k < D) {
+            const float y = gv[i] * (xv[i] * inv2);
+            abuf[ro + k] = y;
+            if (xs_abuf) xsplit_store(xs_abuf, b, k, y);
+          }
+        }
       }
     } else {
       float s = 0.f;
       for (int k = threadIdx.x; k < D; k += NT) s += xr[k] * xr[k];
       const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
-      for (int k = threadIdx.x; k < D; k += NT) hidden[(size_t)b * D + k] = w[k] * (xr[k] * inv);
+      float s2 = 0.f;
+      for (int k = threadIdx.x; k < D; k += NT) {
+        const float h = w[k] * (xr[k] * inv);
+        hidden[ro + k] = h;
+        s2 = fmaf(h, h, s2);
+      }
+      if (abuf) {
+        const float inv2 = 1.0f / sqrtf(block_sum(s2, red) / (float)D + eps_in);
+        for (int k = threadIdx.x; k < D; k += NT) {
+          const float y = w_in[k] * (hidden[ro + k] * inv2);
+          abuf[ro + k] = y;
+          if (xs_abuf) xsplit_store(xs_abuf, b, k, y);
+        }
+      }
     }
     if (threadIdx.x == 0) { kv_len[b] += 1; pos[b] = p0 + 1; }
     // (cos, sin) of the new position: from the per-position table (one load),

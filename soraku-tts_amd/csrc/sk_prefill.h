@@ -407,20 +407,36 @@ __global__ __launch_bounds__(NT) void pf_attention_kernel(const float* Q, const 
 }
 
 // Row r after its prefix: hidden = RMSNorm_final(X[last token]); kv_len and
-// position = prefix length, RoPE (cos, sin) at that position, row active.
+// position = prefix length, RoPE (cos, sin) at that position, row active; the
+// first depth step's input abuf = RMSNorm_in(hidden) (and its split form).
+// Rows with no tokens in this prefill keep their state.
 __global__ __launch_bounds__(NT) void pf_finish_kernel(const float* X, const int* row_start, const int* len,
                                                        const float* w, float eps, int D, float* hidden,
                                                        int* kv_len, int* pos, int* active, const float* inv_freq,
-                                                       int half, float2* rope) {
+                                                       int half, float2* rope, const float* w_in, float eps_in,
+                                                       float* abuf, uint16_t* xs_abuf) {
   __shared__ float red[WAVES];
   const int r = blockIdx.x;
   const int n = len[r];
   if (n == 0) return;                    // not in this prefill: the row keeps its state
   const float* xr = X + (size_t)(row_start[r] + n - 1) * D;
+  const size_t ro = (size_t)r * D;
   float s = 0.f;
   for (int k = threadIdx.x; k < D; k += NT) s += xr[k] * xr[k];
   const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
-  for (int k = threadIdx.x; k < D; k += NT) hidden[(size_t)r * D + k] = w[k] * (xr[k] * inv);
+  float s2 = 0.f;
+  for (int k = threadIdx.x; k < D; k += NT) {
+    const float h = w[k] * (xr[k] * inv);
+    hidden[ro + k] = h;
+    s2 = fmaf(h, h, s2);
+  }
+  // The first frame's depth step 0 input, RMSNorm_in(hidden) (zero prefix).
+  const float inv2 = 1.0f / sqrtf(block_sum(s2, red) / (float)D + eps_in);
+  for (int k = threadIdx.x; k < D; k += NT) {
+    const float y = w_in[k] * (hidden[ro + k] * inv2);
+    abuf[ro + k] = y;
+    if (xs_abuf) xsplit_store(xs_abuf, r, k, y);
+  }
   for (int t = threadIdx.x; t < half; t += NT) rope[(size_t)r * half + t] = rope_cs(n, inv_freq[t]);
   if (threadIdx.x == 0) { kv_len[r] = n; pos[r] = n; active[r] = 1; }
 }

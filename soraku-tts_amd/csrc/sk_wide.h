@@ -401,36 +401,4 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
   }
 }
 
-// Depth step q, row r (utterance r / rows_per_utt): for q > 0 the codebook
-// prefix advances by the previous code's table row (prefix += scale *
-// table[q-1][code], model.py:600-605) in place; then out = RMSNorm_in(hidden
-// + prefix) (eps FLT_EPSILON) -- the depth MLP input and its residual -- and,
-// when xs_out is set, the same values in split form for the MLP's GEMM.
-template <typename TL>
-__global__ __launch_bounds__(NT) void depth_in_kernel(const float* hidden, float* prefix, const void* table,
-                                                      const int* codes_cur, int q, int Q, int V, int D,
-                                                      float scale, int rows_per_utt, const float* w, float eps,
-                                                      float* out, uint16_t* xs_out) {
-  __shared__ float red[WAVES];
-  const int r = blockIdx.x, ut = r / rows_per_utt;
-  const size_t trow = (q > 0) ? ((size_t)(q - 1) * V + codes_cur[ut * Q + q - 1]) * D : 0;
-  float s = 0.f;
-  for (int k = threadIdx.x; k < D; k += NT) {
-    float p = prefix[(size_t)r * D + k];
-    if (q > 0) {
-      p = __fadd_rn(p, __fmul_rn(TL::get(table, trow + k), scale));
-      prefix[(size_t)r * D + k] = p;
-    }
-    const float x = __fadd_rn(hidden[(size_t)r * D + k], p);
-    s += x * x;
-  }
-  const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
-  for (int k = threadIdx.x; k < D; k += NT) {
-    const float x = __fadd_rn(hidden[(size_t)r * D + k], prefix[(size_t)r * D + k]);
-    const float y = w[k] * (x * inv);
-    out[(size_t)r * D + k] = y;
-    if (xs_out) xsplit_store(xs_out, r, k, y);
-  }
-}
-
 }  // namespace sk

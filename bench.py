@@ -19,6 +19,13 @@ GPU (utterances shard across GPUs with no per-frame exchange).
 text ids + BOS frame + 144 prompt frames (240 positions), 480 decoded frames,
 same sampling.
 
+``--kernels`` times the isolated fused kernels at decode shape M = 2 instead
+(RMSNorm over 1024, SwiGLU gate/up GEMV 1024 -> 2 x 3072, down GEMV
+3072 -> 1024 + residual, the 16 classifier heads 1024 -> 2051 + bias; FP32 and
+BF16 weights): each is captured as a chain of launches over distinct weight
+copies totalling more than the 256 MB last-level cache (so every launch reads
+HBM), replayed, and reported per launch with its bytes and HBM fraction.
+
 ``--utterances N`` (N > 1) runs the throughput batch instead: N synthetic
 utterances with CFG decoded together (decode batch 2N) at Qwen3-0.6B shape
 with BF16 weights (FP32 KV cache and accumulation); each prefix is 120-240
@@ -225,6 +232,79 @@ def many_utterances(args):
     print(json.dumps(out))
 
 
+def isolated_kernels(args):
+    """The isolated-kernel measurement (see the module docstring); one JSON line."""
+    import torch
+
+    from soraku_amd import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    B, D, I, V, Q = 2, 1024, 3072, 2051, 16
+    mall = 256 << 20
+
+    def rnd(*shape, std=1.0, dtype=torch.float32):
+        return (torch.randn(*shape, generator=gen, device=dev) * std).to(dtype)
+
+    def timed(name, wname, calls, nbytes, reps=20):
+        ref = [c().clone() for c in calls[:2]]           # eager results (and warm-up)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        outs = []
+        with torch.cuda.graph(graph):
+            for c in calls:
+                outs.append(c())
+        for _ in range(3):                                # every replay equals eager
+            graph.replay()
+            torch.cuda.synchronize()
+            for r, o in zip(ref, outs[:2]):
+                assert torch.equal(r, o), f"{name}: graph replay differs from the eager launch"
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (reps * len(calls))
+        gbs = nbytes / us / 1e3
+        return {"kernel": name, "weights": wname, "us_per_launch": us, "bytes_per_launch": nbytes,
+                "achieved_gbs": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "launches_captured": len(calls)}
+
+    out = []
+    x, g = rnd(B, D), 1.0 + 0.1 * rnd(D)
+    k = ops.rmsnorm(B, D, 1e-6)
+    out.append(timed("rmsnorm hidden 1024", "f32 gain", [lambda: k(x, g)] * 64, 2 * B * D * 4 + D * 4))
+    for wname, dt, wb in (("f32", torch.float32, 4), ("bf16", torch.bfloat16, 2)):
+        gu_bytes = 2 * I * D * wb
+        n = mall // gu_bytes + 2
+        wg = [rnd(I, D, std=0.02, dtype=dt) for _ in range(n)]
+        wu = [rnd(I, D, std=0.02, dtype=dt) for _ in range(n)]
+        k = ops.swiglu_gemv(B, I, D)
+        calls = [lambda i=i: k(x, wg[i], wu[i]) for i in range(n)]
+        out.append(timed("swiglu gate/up GEMV 1024 -> 2x3072", wname, calls, gu_bytes + B * D * 4 + B * I * 4))
+        del wg, wu
+        act = rnd(B, I)
+        n = mall // (D * I * wb) + 2
+        wd = [rnd(D, I, std=0.02, dtype=dt) for _ in range(n)]
+        k = ops.down_residual_gemv(B, D, I)
+        calls = [lambda i=i: k(act, wd[i], x) for i in range(n)]
+        out.append(timed("down GEMV 3072 -> 1024 + residual", wname, calls, D * I * wb + B * I * 4 + 2 * B * D * 4))
+        del wd
+        n = max(2, mall // (Q * V * D * wb) + 1)
+        tables = [rnd(Q, V, D, std=0.02, dtype=dt) for _ in range(n)]
+        bias = rnd(Q, V, std=0.02)
+        k = ops.classifier_gemv(B, V, D)
+        calls = [lambda i=i, q=q: k(x, tables[i][q], bias[q]) for i in range(n) for q in range(Q)]
+        out.append(timed("classifier GEMV 1024 -> 2051 + bias (one of 16 heads)", wname, calls,
+                         V * D * wb + V * 4 + B * D * 4 + B * V * 4))
+        del tables
+    print(json.dumps({"metric": "isolated decode kernels at M=2: us per launch and HBM fraction, 1 MI355X",
+                      "n_gpus": 1, "data": "synthetic", "unit": "us/launch",
+                      "note": "per launch inside a captured chain (includes the ~1.6 us per-kernel graph floor)",
+                      "kernels": out}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -234,6 +314,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--model", choices=("q06b", "q17b"), default="q06b",
                     help="q17b: Qwen3-1.7B shape with BF16 weights, 240-position prefix, 480 frames")
+    ap.add_argument("--kernels", action="store_true",
+                    help="time the isolated fused kernels at M=2 (FP32 and BF16 weights) instead")
     ap.add_argument("--utterances", type=int, default=1,
                     help="N > 1: the throughput batch of N utterances x CFG (BF16 weights) instead")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -250,6 +332,9 @@ def main():
     n_text, n_prompt, n_frames = (95, 144, 480) if big else (N_TEXT, N_PROMPT, N_FRAMES)
     if args.steps + args.warmup > n_frames:
         sys.exit(f"steps + warmup must be <= {n_frames} (the workload's decoded frames)")
+    if args.kernels:
+        isolated_kernels(args)
+        return
     if args.utterances > 1:
         many_utterances(args)
         return

@@ -148,9 +148,9 @@ class FastGenerator:
             raise ValueError("classifier-free guidance requires uncond_input_ids")
         batch = 2 if cfg_scale != 1.0 else 1
         cap = 32 // batch
-        slots = min(U, max_batch if max_batch is not None else cap)
-        if not 1 <= slots <= cap:
+        if max_batch is not None and not 1 <= max_batch <= cap:
             raise ValueError(f"max_batch must be in [1, {cap}]")
+        slots = min(U, max_batch if max_batch is not None else cap)
         Qn = self._shape.n_codebooks if self._shape else 16
         longest = 0
         for r in requests:

@@ -89,6 +89,9 @@ def test_null_handles_are_rejected(L):
     assert L.sk_step_frame(None, 0, None, None, None, None) == SK_EINVAL
     assert L.sk_bind_weight(None, b"trunk.norm.weight", None, 0, None, 0) == SK_EINVAL
     assert L.sk_frames_done(None) == -1
+    assert L.sk_prefill_refill(None) == SK_EINVAL
+    assert L.sk_retire_row(None, 0) == SK_EINVAL
+    assert L.sk_reset_frames(None) == SK_EINVAL
 
 
 def test_ops_reject_bad_arguments(L):
@@ -114,6 +117,44 @@ def test_generate_argument_errors_before_gpu():
         FastGenerator.generate(g, input_ids=np.zeros((2, 3), np.int64))
     with pytest.raises(ValueError):
         FastGenerator.generate(g, input_ids=np.zeros((1, 3), np.int64), cfg_scale=1.5)
+
+
+def test_eos_mask_bits():
+    """The per-utterance EOS mask passed to sk_step_frame / sk_queue_frames:
+    bit u is utterance u; a bool covers every utterance; 32 utterances use
+    all 32 bits of the signed argument."""
+    from soraku_amd import GraphFrameEngine
+
+    e = GraphFrameEngine.__new__(GraphFrameEngine)
+    e.n_utts = 3
+    assert e.eos_mask_bits(True) == 0b111 and e.eos_mask_bits(False) == 0
+    assert e.eos_mask_bits([True, False, True]) == 0b101
+    assert e.eos_mask_bits(np.array([0, 1, 0])) == 0b010
+    with pytest.raises(ValueError):
+        e.eos_mask_bits([True, False])
+    e.n_utts = 1
+    assert e.eos_mask_bits(1) == 1
+    e.n_utts = 32
+    assert e.eos_mask_bits(True) == -1
+    assert e.eos_mask_bits([False] * 31 + [True]) == -(1 << 31)
+    assert e.eos_mask_bits([True] + [False] * 31) == 1
+
+
+def test_generate_batch_argument_errors_before_gpu():
+    """generate_batch checks its requests and max_batch before any engine."""
+    from soraku_amd import FastGenerator
+
+    g = FastGenerator.__new__(FastGenerator)
+    g._shape = None
+    ok = dict(input_ids=np.zeros((1, 3), np.int64), uncond_input_ids=np.zeros((1, 1), np.int64))
+    with pytest.raises(ValueError):
+        FastGenerator.generate_batch(g, [])
+    with pytest.raises(ValueError):
+        FastGenerator.generate_batch(g, [dict(input_ids=np.zeros((1, 3), np.int64))], cfg_scale=1.5)
+    with pytest.raises(ValueError):
+        FastGenerator.generate_batch(g, [ok] * 3, cfg_scale=1.5, max_batch=17)
+    with pytest.raises(ValueError):
+        FastGenerator.generate_batch(g, [ok] * 3, cfg_scale=1.5, max_batch=0)
 
 
 def test_synthetic_weights_match_oracle():

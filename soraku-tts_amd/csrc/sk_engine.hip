@@ -456,9 +456,9 @@ hipError_t launch_gemm(int wdtype, const GemmArgs& g, hipStream_t st) {
   const bool small = nt * ((g.M + 63) / 64) < 128;
   const dim3 grid(nt, small ? (g.M + 31) / 32 : (g.M + 63) / 64);
   if (wdtype == SK_BF16) {
-    if (small) hipLaunchKernelGGL((gemm_nt_kernel<EPI, WBF16, 32>), grid, dim3(256), 0, st, g);
-    else hipLaunchKernelGGL((gemm_nt_kernel<EPI, WBF16, 64>), grid, dim3(256), 0, st, g);
-  } else {
+    if (small) hipLaunchKernelGGL((gemm_bf16_kernel<EPI, 32>), grid, dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((gemm_bf16_kernel<EPI, 64>), grid, dim3(256), 0, st, g);
+  } else {   // FP32 weights stay on the FP32 matrix cores: exact FP32 products
     if (small) hipLaunchKernelGGL((gemm_nt_kernel<EPI, WF32, 32>), grid, dim3(256), 0, st, g);
     else hipLaunchKernelGGL((gemm_nt_kernel<EPI, WF32, 64>), grid, dim3(256), 0, st, g);
   }

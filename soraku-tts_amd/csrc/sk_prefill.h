@@ -158,6 +158,135 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmArgs a) {
     }
 }
 
+typedef __bf16 pbf8 __attribute__((ext_vector_type(8)));
+
+// FP32 -> (hi, lo) BF16 pair of 4 values, packed 4 x 16 bits each.
+__device__ __forceinline__ void split4(const float4 v, uint2& hi, uint2& lo) {
+  const float x[4] = {v.x, v.y, v.z, v.w};
+  uint16_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const __bf16 b = (__bf16)x[i];
+    h[i] = __builtin_bit_cast(uint16_t, b);
+    l[i] = __builtin_bit_cast(uint16_t, (__bf16)(x[i] - (float)b));
+  }
+  hi = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+  lo = make_uint2((uint32_t)l[0] | ((uint32_t)l[1] << 16), (uint32_t)l[2] | ((uint32_t)l[3] << 16));
+}
+
+// The same GEMM for BF16 weights on the BF16 matrix cores
+// (v_mfma_f32_16x16x32_bf16).  Each 32-k step stores the A tile to LDS
+// already split into x_hi = bf16(x) and x_lo = bf16(x - x_hi), in MFMA
+// fragment order (per 16-row tile and half: 64 lanes x 8 BF16, lane 16q + i =
+// row i, k 8q .. 8q+7), so a wave reads a fragment with one 16-byte LDS load;
+// the weights are stored as fragments unchanged.  Two MFMAs per product
+// (A_hi W, A_lo W): the products are exact in FP32 and A keeps ~16 mantissa
+// bits.  The output layout is the FP32 form's, and so is the epilogue.
+template <int EPI, int BM>
+__global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs a) {
+  constexpr int NB = (EPI == GEPI_SWIGLU) ? 2 : 1;
+  constexpr int TA = BM / 16, TB = GBN / 16;     // 16-row tiles of A, 16-column tiles of B
+  constexpr int TM = BM / 32;                    // A tiles per wave (wave tile (BM/2) x 32)
+  constexpr int AL = BM * 8 / 256;               // float4 of A per thread per step (1 or 2)
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][TA * 512];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[NB][TB * 512];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * BM;
+  // fragment slot (in BF16 elements) of element k of row r within a 32-k step
+  auto slot = [](int r, int k) { return ((r >> 4) * 64 + (k >> 3) * 16 + (r & 15)) * 8 + (k & 7); };
+
+  const float* arow[AL];
+  int adst[AL];
+#pragma unroll
+  for (int i = 0; i < AL; ++i) {
+    const int idx = tid + 256 * i, r = idx >> 3, k4 = (idx & 7) * 4;
+    arow[i] = a.A + (size_t)min(m0 + r, a.M - 1) * a.lda + k4;
+    adst[i] = slot(r, k4);
+  }
+  // weights: 64 rows x 32 k = 256 pieces of 8 BF16, one per thread
+  const int bn_l = tid >> 2, bk = (tid & 3) * 8;
+  const int bn = min(n0 + bn_l, a.N - 1);
+  const void* bbase;
+  int brow;
+  if (bn < a.seg_rows[0]) { bbase = a.B[0]; brow = bn; }
+  else if (bn < a.seg_rows[0] + a.seg_rows[1]) { bbase = a.B[1]; brow = bn - a.seg_rows[0]; }
+  else { bbase = a.B[2]; brow = bn - a.seg_rows[0] - a.seg_rows[1]; }
+  const uint16_t* bp = static_cast<const uint16_t*>(bbase) + (size_t)brow * a.K + bk;
+  const uint16_t* b2p = NB == 2 ? static_cast<const uint16_t*>(a.B2) + (size_t)bn * a.K + bk : nullptr;
+  const int bdst = slot(bn_l, bk);
+  float4 ra[AL];
+  uint4 rb[NB];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < AL; ++i) ra[i] = *reinterpret_cast<const float4*>(arow[i] + k0);
+    rb[0] = *reinterpret_cast<const uint4*>(bp + k0);
+    if constexpr (NB == 2) rb[NB - 1] = *reinterpret_cast<const uint4*>(b2p + k0);
+  };
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;
+  v4f acc[NB][TM][2];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[b][i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  fetch(0);
+  for (int k0 = 0; k0 < a.K; k0 += GBK) {
+    __syncthreads();   // the previous step's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < AL; ++i) {
+      uint2 hi, lo;
+      split4(ra[i], hi, lo);
+      *reinterpret_cast<uint2*>(&As[0][adst[i]]) = hi;
+      *reinterpret_cast<uint2*>(&As[1][adst[i]]) = lo;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) *reinterpret_cast<uint4*>(&Bs[b][bdst]) = rb[b];
+    __syncthreads();
+    if (k0 + GBK < a.K) fetch(k0 + GBK);   // in flight while this step multiplies
+    pbf8 ah[TM], al[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int t = wm / 16 + i;
+      ah[i] = __builtin_bit_cast(pbf8, *reinterpret_cast<const uint4*>(&As[0][(t * 64 + lane) * 8]));
+      al[i] = __builtin_bit_cast(pbf8, *reinterpret_cast<const uint4*>(&As[1][(t * 64 + lane) * 8]));
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int t = wn / 16 + j;
+        const pbf8 bw = __builtin_bit_cast(pbf8, *reinterpret_cast<const uint4*>(&Bs[b][(t * 64 + lane) * 8]));
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bw, acc[b][i][j], 0, 0, 0);
+          acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bw, acc[b][i][j], 0, 0, 0);
+        }
+      }
+  }
+  // lane holds C[row = 4 (lane / 16) + v][col = lane % 16] of each 16 x 16 tile
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn + j * 16 + (lane & 15);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = m0 + wm + i * 16 + 4 * (lane >> 4) + v;
+        if (m < a.M && n < a.N) {
+          float c = acc[0][i][j][v];
+          if constexpr (EPI == GEPI_RESID) c = a.res[(size_t)m * a.ldr + n] + c;
+          if constexpr (EPI == GEPI_SWIGLU) {
+            const float u = acc[NB - 1][i][j][v];
+            c = c / (1.0f + expf(-c)) * u;
+          }
+          a.out[(size_t)m * a.ldo + n] = c;
+        }
+      }
+    }
+}
+
 // ------------------------------------------------------------ per-token kernels
 // X[m] = embeds[tok_row[m]][tok_pos[m]].
 __global__ __launch_bounds__(NT) void pf_gather_kernel(const float* embeds, int max_ctx, const int* tok_row,

@@ -32,6 +32,11 @@ with BF16 weights (FP32 KV cache and accumulation); each prefix is 120-240
 tokens drawn uniformly (text ids + BOS frame + prompt frames, the prompt ~60%
 of it; the uncond row is [bos] + BOS frame + the same prompt); KV capacity
 512.  A step is one frame of every utterance; ``value`` is utterance-frames/s.
+With ``--requests R`` (R > N) it decodes R such requests through N slots with
+``FastGenerator.generate_batch`` instead: a slot whose request retires is
+prefilled with the next one between frames (continuous batching), and
+``value`` is decoded frames per second of wall clock, prefills, refills and
+the per-frame host synchronisation included.
 """
 
 from __future__ import annotations
@@ -232,6 +237,50 @@ def many_utterances(args):
     print(json.dumps(out))
 
 
+def continuous_batch(args):
+    """R requests through N utterance slots with refills; one JSON line."""
+    import torch
+
+    from soraku_amd import FastGenerator
+    from soraku_amd.config import QWEN3_06B
+    from soraku_amd.synthetic import synthetic_weights
+
+    shape, n, R = QWEN3_06B, args.utterances, args.requests
+    weights = synthetic_weights(shape, args.seed)
+    rng = np.random.default_rng(args.seed + 7)
+    reqs = []
+    for _ in range(R):
+        p_len = int(rng.integers(120, 241))
+        n_prompt = int(round(0.6 * p_len))
+        text = rng.integers(0, shape.text_vocab, p_len - 1 - n_prompt)
+        text[0] = TEXT_BOS
+        reqs.append(dict(input_ids=torch.tensor(text[None]),
+                         prompt_codes=torch.tensor(rng.integers(0, shape.codebook_size, (n_prompt, shape.n_codebooks))),
+                         uncond_input_ids=torch.tensor([[TEXT_BOS]])))
+    g = FastGenerator(device=torch.device("cuda:0"), state_dict=weights, shape=shape, bf16=True)
+    del weights
+    kw = dict(max_new_frames=N_FRAMES, min_new_frames=4, temperature=TEMP, top_k=TOP_K, top_p=TOP_P,
+              cfg_scale=CFG, max_batch=n)
+    g.generate_batch(reqs[:n], seeds=list(range(n)), **dict(kw, max_new_frames=8))   # engine + capture
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = g.generate_batch(reqs, seeds=list(range(R)), **kw)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    frames = sum(o[1]["num_frames"] for o in out)
+    stops = sum(o[1]["stop_reason"] == "eos" for o in out)
+    print(json.dumps({
+        "metric": f"codec frames/sec over {R} requests through {n} CFG slots (continuous batching), 1 MI355X",
+        "value": frames / dt, "unit": "utterance-frames/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": (f"{R} synthetic requests x CFG, Qwen3-0.6B shape, BF16 weights, FP32 KV, ragged "
+                                f"prefixes 120-240, up to {N_FRAMES} frames each, CFG 1.5, T 0.9, top-k 50, "
+                                "top-p 0.95; a retired slot is refilled between frames"),
+                   "slots": n, "requests": R, "frames_decoded": frames, "stopped_at_eos": stops,
+                   "wall_s": dt, "timing": "wall clock of generate_batch (prefills, refills, host sync per frame)"},
+    }))
+
+
 def isolated_kernels(args):
     """The isolated-kernel measurement (see the module docstring); one JSON line."""
     import torch
@@ -318,6 +367,8 @@ def main():
                     help="time the isolated fused kernels at M=2 (FP32 and BF16 weights) instead")
     ap.add_argument("--utterances", type=int, default=1,
                     help="N > 1: the throughput batch of N utterances x CFG (BF16 weights) instead")
+    ap.add_argument("--requests", type=int, default=0,
+                    help="with --utterances N: decode this many requests through the N slots (refills)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 4 device copies of MIB MiB each (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -334,6 +385,9 @@ def main():
         sys.exit(f"steps + warmup must be <= {n_frames} (the workload's decoded frames)")
     if args.kernels:
         isolated_kernels(args)
+        return
+    if args.utterances > 1 and args.requests > args.utterances:
+        continuous_batch(args)
         return
     if args.utterances > 1:
         many_utterances(args)

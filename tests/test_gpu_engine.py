@@ -152,6 +152,43 @@ def test_queued_replay_equals_stepwise(hip_device):
     e.close()
 
 
+def test_frame_ring_reset(hip_device):
+    """sk_reset_frames: an engine whose frame ring holds 3 frames decodes 7
+    (restarting the ring whenever it is full) with the same codes and logits
+    as an engine whose ring holds them all; a full ring refuses the next frame."""
+    from soraku_amd import GraphFrameEngine, SkError
+    from soraku_amd._lib import SK_EKVFULL
+
+    f, s, gen = load_golden("tiny_sampled")
+    w = _weights(f, s)
+    n = 7
+    u = np.random.default_rng(9).random((n, s.n_codebooks))
+    runs = []
+    for ring in (n, 3):
+        e = GraphFrameEngine(device=hip_device, max_cache_len=64, cfg_scale=1.5, batch=2, state_dict=w,
+                             shape=_shape(s), language_token_ids=tuple(int(v) for v in f["language_ids"]),
+                             max_frames=ring)
+        e.set_temperature(gen["temperature"])
+        e.set_sampling(sampled=True, top_k=gen.get("top_k"), top_p=gen.get("top_p"))
+        e.set_debug(True)
+        e.prefill(f["text_ids"], f["uncond_ids"], f["prompt_codes"])
+        e.capture()
+        got = []
+        for i in range(n):
+            if e.frames_done == ring:
+                with pytest.raises(SkError) as ei:
+                    e.step_frame(mask_eos_q0=i < 2, uniforms=u[i])
+                assert ei.value.code == SK_EKVFULL
+                e.reset_frames()
+            c, lg = e.step_frame(mask_eos_q0=i < 2, uniforms=u[i], return_logits=True)
+            got.append((c.numpy(), lg))
+        e.close()
+        runs.append(got)
+    for (c0, l0), (c1, l1) in zip(*runs):
+        np.testing.assert_array_equal(c0, c1)
+        np.testing.assert_array_equal(l0, l1)
+
+
 def test_engine_error_paths(hip_device):
     from soraku_amd import GraphFrameEngine, SkError
     from soraku_amd._lib import SK_EKVFULL, SK_ENOCAPTURE

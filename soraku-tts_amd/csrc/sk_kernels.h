@@ -295,6 +295,47 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
   const int row0 = (blockIdx.x * WAVES + wave) * RW;
 
   constexpr bool ADD = (PRO == PRO_ADDNORM || PRO == PRO_ADDGATHER);
+  // The workgroup's waves share the activations: each thread loads CH
+  // consecutive elements of x per chunk (1/NT of it, plus its share of the norm
+  // gain, and of x2 for an add prologue) before the weight stream, finishes its
+  // chunks once its own loads are in (x2 + table row * scale, then x + x2, the
+  // per-element order of the unshared path), stores them to LDS, and after one
+  // barrier -- with the weights still in flight -- every wave reads the whole
+  // vectors from LDS.  The cache serves x once per workgroup instead of once per
+  // wave, and no wave holds x2 or the table rows for the whole K in registers.
+  // Capped at 32 KB of LDS: a 48 KB buffer (M = 2, K = 6144) leaves too few
+  // workgroups per CU and is slower than per-wave loads.
+  constexpr int CH = ADD ? VEC : 4;                                         // elements per chunk
+  constexpr bool SHARE = M * KT * 4 <= 32768 && (M * KT) % (NT * CH) == 0;
+  constexpr int XQ = SHARE ? (M * KT) / (NT * CH) : 1;                      // chunks of x per thread
+  // The gain is loaded up front unless a gathered table row follows the
+  // weights anyway (then it is loaded with that row, straight into LDS).
+  constexpr bool GEARLY = SHARE && PRO != PRO_NONE && PRO != PRO_ADDGATHER;
+  constexpr int GQ = GEARLY ? KT / (NT * 4) : 1;                            // float4 of the gain
+  static_assert(!SHARE || PRO == PRO_NONE || KT % (NT * 4) == 0, "shared gain: K a multiple of 1024");
+  __shared__ __attribute__((aligned(16))) float xsh[SHARE ? M * KT : 4];
+  __shared__ __attribute__((aligned(16))) float gsh[(SHARE && PRO != PRO_NONE) ? KT : 4];
+  float xq[XQ][CH], x2q[(SHARE && ADD) ? XQ : 1][CH];
+  float4 gq[GQ];
+  if constexpr (SHARE) {
+#pragma unroll
+    for (int q = 0; q < XQ; ++q) {
+      const int f = (tid + NT * q) * CH, m = f / KT, k = f % KT;
+#pragma unroll
+      for (int i = 0; i < CH; i += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + k + i);
+        xq[q][i] = t.x; xq[q][i + 1] = t.y; xq[q][i + 2] = t.z; xq[q][i + 3] = t.w;
+        if constexpr (ADD) {
+          const float4 w = *reinterpret_cast<const float4*>(a.x2 + (size_t)m * a.ldx2 + k + i);
+          x2q[q][i] = w.x; x2q[q][i + 1] = w.y; x2q[q][i + 2] = w.z; x2q[q][i + 3] = w.w;
+        }
+      }
+    }
+    if constexpr (GEARLY) {
+#pragma unroll
+      for (int q = 0; q < GQ; ++q) gq[q] = *reinterpret_cast<const float4*>(a.norm_w + (tid + NT * q) * 4);
+    }
+  }
   // Codes of the gathered table rows first, as vector loads (an opaque zero
   // lane offset keeps them off the scalar path): waiting on them later then
   // never waits on the weight stream issued after them.
@@ -306,26 +347,28 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
     for (int m = 0; m < M; ++m) gc[m] = a.gcode[(m / a.g_rpu) * a.gstride + zero];
   }
   float xv[M][NV][VEC];
-  float x2v[ADD ? M : 1][ADD ? NV : 1][VEC];
+  float x2v[(ADD && !SHARE) ? M : 1][(ADD && !SHARE) ? NV : 1][VEC];
+  if constexpr (!SHARE) {
 #pragma unroll
-  for (int m = 0; m < M; ++m)
+    for (int m = 0; m < M; ++m)
 #pragma unroll
-    for (int j = 0; j < NV; ++j)
+      for (int j = 0; j < NV; ++j)
 #pragma unroll
-      for (int i = 0; i < VEC; i += 4) {
-        const size_t k = (size_t)(j * 64 + lane) * VEC + i;
-        const float4 t = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + k);
-        xv[m][j][i] = t.x; xv[m][j][i + 1] = t.y; xv[m][j][i + 2] = t.z; xv[m][j][i + 3] = t.w;
-        if (ADD) {
-          const float4 w = *reinterpret_cast<const float4*>(a.x2 + (size_t)m * a.ldx2 + k);
-          x2v[m][j][i] = w.x; x2v[m][j][i + 1] = w.y; x2v[m][j][i + 2] = w.z; x2v[m][j][i + 3] = w.w;
+        for (int i = 0; i < VEC; i += 4) {
+          const size_t k = (size_t)(j * 64 + lane) * VEC + i;
+          const float4 t = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + k);
+          xv[m][j][i] = t.x; xv[m][j][i + 1] = t.y; xv[m][j][i + 2] = t.z; xv[m][j][i + 3] = t.w;
+          if (ADD) {
+            const float4 w = *reinterpret_cast<const float4*>(a.x2 + (size_t)m * a.ldx2 + k);
+            x2v[m][j][i] = w.x; x2v[m][j][i + 1] = w.y; x2v[m][j][i + 2] = w.z; x2v[m][j][i + 3] = w.w;
+          }
         }
-      }
+  }
 
   // Small operands next (norm gains, residual / bias for this lane's
   // outputs), so waiting on them never waits on the weight stream.
   float gw[(PRO != PRO_NONE) ? NV : 1][VEC];
-  if (PRO != PRO_NONE) {
+  if (PRO != PRO_NONE && !SHARE) {
 #pragma unroll
     for (int j = 0; j < NV; ++j)
 #pragma unroll
@@ -363,10 +406,76 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
       for (int j = 0; j < NV; ++j) WL::load(base[s], off + (size_t)(j * 64 + lane) * VEC, wv[r][s][j]);
   }
 
-  // The gathered rows are loaded after the weights (their address waits on
-  // the code), and x + x2 is formed only now, so neither holds the weight
-  // stream back.
-  if (PRO == PRO_ADDGATHER) {
+  if constexpr (SHARE) {
+    // nothing issued below may be scheduled above the weight stream
+    if constexpr (PRO == PRO_ADDGATHER) __builtin_amdgcn_sched_barrier(0);
+    // gathered table rows and the gain: every load before the first store
+    // (a store may alias them), so they take one round trip together
+    constexpr int TQ = (PRO == PRO_ADDGATHER) ? XQ : 1;
+    float tq[TQ][CH];
+    if constexpr (PRO == PRO_ADDGATHER) {
+#pragma unroll
+      for (int q = 0; q < XQ; ++q) {
+        const int f = (tid + NT * q) * CH, m = f / KT, k = f % KT;
+        int code = gc[0];
+#pragma unroll
+        for (int mm = 1; mm < M; ++mm) code = (m == mm) ? gc[mm] : code;
+        WL::load(a.gtable, (size_t)code * KT + k, tq[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < KT / (NT * 4); ++q)   // LDS cannot alias the global stores below
+        *reinterpret_cast<float4*>(&gsh[(tid + NT * q) * 4]) =
+            *reinterpret_cast<const float4*>(a.norm_w + (tid + NT * q) * 4);
+    }
+#pragma unroll
+    for (int q = 0; q < XQ; ++q) {
+      const int f = (tid + NT * q) * CH, m = f / KT, k = f % KT;
+      if constexpr (PRO == PRO_ADDGATHER) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) x2q[q][i] = __fadd_rn(x2q[q][i], __fmul_rn(tq[q][i], a.gscale));
+        if (blockIdx.x == 0)
+#pragma unroll
+          for (int i = 0; i < CH; i += 4)
+            *reinterpret_cast<float4*>(a.gout + (size_t)m * a.ldgo + k + i) =
+                make_float4(x2q[q][i], x2q[q][i + 1], x2q[q][i + 2], x2q[q][i + 3]);
+      }
+      if constexpr (ADD) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) xq[q][i] = __fadd_rn(xq[q][i], x2q[q][i]);
+      }
+#pragma unroll
+      for (int i = 0; i < CH; i += 4)
+        *reinterpret_cast<float4*>(&xsh[f + i]) = make_float4(xq[q][i], xq[q][i + 1], xq[q][i + 2], xq[q][i + 3]);
+    }
+    if constexpr (GEARLY) {
+#pragma unroll
+      for (int q = 0; q < GQ; ++q) *reinterpret_cast<float4*>(&gsh[(tid + NT * q) * 4]) = gq[q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; i += 4) {
+          const float4 t = *reinterpret_cast<const float4*>(&xsh[m * KT + (j * 64 + lane) * VEC + i]);
+          xv[m][j][i] = t.x; xv[m][j][i + 1] = t.y; xv[m][j][i + 2] = t.z; xv[m][j][i + 3] = t.w;
+        }
+    if constexpr (PRO != PRO_NONE) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; i += 4) {
+          const float4 g = *reinterpret_cast<const float4*>(&gsh[(j * 64 + lane) * VEC + i]);
+          gw[j][i] = g.x; gw[j][i + 1] = g.y; gw[j][i + 2] = g.z; gw[j][i + 3] = g.w;
+        }
+    }
+  }
+
+  // Unshared: the gathered rows are loaded after the weights (their address
+  // waits on the code), and x + x2 is formed only now, so neither holds the
+  // weight stream back.
+  if constexpr (PRO == PRO_ADDGATHER && !SHARE) {
     float tv[M][NV][VEC];
 #pragma unroll
     for (int m = 0; m < M; ++m)
@@ -385,7 +494,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
                 make_float4(x2v[m][j][i], x2v[m][j][i + 1], x2v[m][j][i + 2], x2v[m][j][i + 3]);
       }
   }
-  if (ADD) {
+  if constexpr (ADD && !SHARE) {
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll

@@ -214,14 +214,15 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs a) {
   const uint16_t* bp = static_cast<const uint16_t*>(bbase) + (size_t)brow * a.K + bk;
   const uint16_t* b2p = NB == 2 ? static_cast<const uint16_t*>(a.B2) + (size_t)bn * a.K + bk : nullptr;
   const int bdst = slot(bn_l, bk);
+  // next step's A and B pieces.  The two B pieces are named registers: as a
+  // two-element array the compiler kept them in memory, which put a wait on
+  // each prefetch in front of the step's MFMAs.
   float4 ra[AL];
-  uint4 rb[NB];
-  auto fetch = [&](int k0) {
+  uint4 rb0, rb1 = make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < AL; ++i) ra[i] = *reinterpret_cast<const float4*>(arow[i] + k0);
-    rb[0] = *reinterpret_cast<const uint4*>(bp + k0);
-    if constexpr (NB == 2) rb[NB - 1] = *reinterpret_cast<const uint4*>(b2p + k0);
-  };
+  for (int i = 0; i < AL; ++i) ra[i] = *reinterpret_cast<const float4*>(arow[i]);
+  rb0 = *reinterpret_cast<const uint4*>(bp);
+  if constexpr (NB == 2) rb1 = *reinterpret_cast<const uint4*>(b2p);
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;
   v4f acc[NB][TM][2];
 #pragma unroll
@@ -231,7 +232,6 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[b][i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  fetch(0);
   for (int k0 = 0; k0 < a.K; k0 += GBK) {
     __syncthreads();   // the previous step's LDS reads are done
 #pragma unroll
@@ -241,10 +241,16 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs a) {
       *reinterpret_cast<uint2*>(&As[0][adst[i]]) = hi;
       *reinterpret_cast<uint2*>(&As[1][adst[i]]) = lo;
     }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) *reinterpret_cast<uint4*>(&Bs[b][bdst]) = rb[b];
+    *reinterpret_cast<uint4*>(&Bs[0][bdst]) = rb0;
+    if constexpr (NB == 2) *reinterpret_cast<uint4*>(&Bs[NB - 1][bdst]) = rb1;
     __syncthreads();
-    if (k0 + GBK < a.K) fetch(k0 + GBK);   // in flight while this step multiplies
+    if (k0 + GBK < a.K) {   // in flight while this step multiplies
+      const int kn = k0 + GBK;
+#pragma unroll
+      for (int i = 0; i < AL; ++i) ra[i] = *reinterpret_cast<const float4*>(arow[i] + kn);
+      rb0 = *reinterpret_cast<const uint4*>(bp + kn);
+      if constexpr (NB == 2) rb1 = *reinterpret_cast<const uint4*>(b2p + kn);
+    }
     pbf8 ah[TM], al[TM];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -441,9 +447,11 @@ __global__ __launch_bounds__(NT) void pf_attention_kernel(const float* Q, const 
                             __uint_as_float(kb.y << 16), __uint_as_float(kb.y & 0xffff0000u));
         vr[u] = make_float4(__uint_as_float(vb.x << 16), __uint_as_float(vb.x & 0xffff0000u),
                             __uint_as_float(vb.y << 16), __uint_as_float(vb.y & 0xffff0000u));
-      } else {
-        kr[u] = *reinterpret_cast<const float4*>(kc + off);
-        vr[u] = *reinterpret_cast<const float4*>(vc + off);
+      } else {   // built element-wise like the BF16 form, which keeps kr / vr in registers
+        const float4 kb = *reinterpret_cast<const float4*>(kc + off);
+        const float4 vb = *reinterpret_cast<const float4*>(vc + off);
+        kr[u] = make_float4(kb.x, kb.y, kb.z, kb.w);
+        vr[u] = make_float4(vb.x, vb.y, vb.z, vb.w);
       }
     }
   };

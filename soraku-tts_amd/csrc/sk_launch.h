@@ -61,6 +61,13 @@ static hipError_t launch_fast_k(const GemvArgs& a, hipStream_t st) {
   constexpr int NV = KT / (64 * WL::VEC);
   int rw = 4;
   while (rw > 1 && (rw * NS * NV > 16 || a.N / (WAVES * rw) < 256)) rw /= 2;
+  // Prefer a grid that spreads evenly over the 256 CUs: N = 3072 with SwiGLU
+  // is 384 workgroups at 2 rows per wave (half the CUs stream twice the
+  // bytes) but 768 at 1 row (3 per CU).
+  if (rw > 1) {
+    const int g = (a.N + WAVES * rw - 1) / (WAVES * rw), g2 = (a.N + WAVES * (rw / 2) - 1) / (WAVES * (rw / 2));
+    if (g % 256 != 0 && g2 % 256 == 0) rw /= 2;
+  }
   switch (rw) {
     case 4: return launch_fast_t<M, KT, 4, PRO, EPI, WL>(a, st);
     case 2: return launch_fast_t<M, KT, 2, PRO, EPI, WL>(a, st);

@@ -714,16 +714,15 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
   // and hd <= NT), then the chunk's K/V rows; LDS is written only once all of
   // them are in flight, so no load waits behind another's round trip.
   const float* row = a.qkv + (size_t)r * a.ldqkv;
-  float q_r = 0.f, kn_r = 0.f, vn_r = 0.f, qw_r = 0.f, kw_r = 0.f;
-  float2 cs_r = make_float2(1.f, 0.f);
-  if (tid < G * hd) q_r = row[(size_t)h * G * hd + tid];
-  if (tid < hd) {
-    kn_r = row[(size_t)a.Hq * hd + (size_t)h * hd + tid];
-    vn_r = row[(size_t)(a.Hq + a.Hkv) * hd + (size_t)h * hd + tid];
-    qw_r = a.qn_w[tid];
-    kw_r = a.kn_w[tid];
-  }
-  if (tid < half) cs_r = a.rope[(size_t)r * half + tid];
+  // Indices clamped instead of branched: with no branch around them the
+  // compiler issues these loads, and the argument loads they need, together.
+  const int tq = min(tid, G * hd - 1), th = min(tid, hd - 1), tr = min(tid, half - 1);
+  const float q_r = row[(size_t)h * G * hd + tq];
+  const float kn_r = row[(size_t)a.Hq * hd + (size_t)h * hd + th];
+  const float vn_r = row[(size_t)(a.Hq + a.Hkv) * hd + (size_t)h * hd + th];
+  const float qw_r = a.qn_w[th];
+  const float kw_r = a.kn_w[th];
+  const float2 cs_r = a.rope[(size_t)r * half + tr];
 
   const int LPT = hd / ATT_DPL;
   const int TPP = NT / LPT;              // tokens per pass
@@ -761,6 +760,9 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
     }
   };
   load_tok(0);
+  // Keep the chunk's K/V loads above the exit test below: sunk past it, they
+  // waited for kv_len and active to arrive first.
+  asm volatile("" ::: "memory");
   const int ctx = T + 1;
   const int nch = (ctx + ATT_CHUNK - 1) / ATT_CHUNK;
   if (!act || c >= nch) return;
@@ -908,11 +910,13 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
       ov[j] = pp[cc * stride + dd];
     }
   };
-  load_block(0);
-  // Keep the first block's loads ahead of the length lookup they do not need.
-  asm volatile("" ::: "memory");
-  const int nch = a.nparts > 0 ? a.nparts : (a.kv_len[r] + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
+  // Row length and state first: issued ahead of the partials, they arrive
+  // with them instead of costing a round trip of their own afterwards.
+  const int kvl = a.kv_len[r];
   const int act = a.active[r];
+  load_block(0);
+  asm volatile("" ::: "memory");
+  const int nch = a.nparts > 0 ? a.nparts : (kvl + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
   float M = -INFINITY, L = 0.f, O = 0.f;
   for (int c0 = 0; c0 < nch; c0 += CB) {
     if (c0 > 0) load_block(c0);

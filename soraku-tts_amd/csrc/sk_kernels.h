@@ -1018,22 +1018,25 @@ __global__ __launch_bounds__(NTH) void attention_stream_kernel(AttnArgs a, int S
   // Raw q / k / v of this head, norm gains and RoPE entry to registers, then
   // the first D tokens of every slot -- all before the row's length arrives.
   const float* row = a.qkv + (size_t)r * a.ldqkv;
-  float q_r = 0.f, kn_r = 0.f, vn_r = 0.f, qw_r = 0.f, kw_r = 0.f;
-  float2 cs_r = make_float2(1.f, 0.f);
-  if (tid < G * hd) q_r = row[(size_t)h * G * hd + tid];
-  if (tid < hd) {
-    kn_r = row[(size_t)a.Hq * hd + (size_t)h * hd + tid];
-    vn_r = row[(size_t)(a.Hq + a.Hkv) * hd + (size_t)h * hd + tid];
-    qw_r = a.qn_w[tid];
-    kw_r = a.kn_w[tid];
-  }
-  if (tid < half) cs_r = a.rope[(size_t)r * half + tid];
+  // The row's length and state first (uniform, scalar loads: waiting for them
+  // does not wait for the vector loads below).  Indices clamped instead of
+  // branched, so these loads and the argument loads they need go together.
+  const int T = a.kv_len[r];
+  const int act = a.active[r];
+  const int tq = min(tid, G * hd - 1), th = min(tid, hd - 1), tr = min(tid, half - 1);
+  const float q_r = row[(size_t)h * G * hd + tq];
+  const float kn_r = row[(size_t)a.Hq * hd + (size_t)h * hd + th];
+  const float vn_r = row[(size_t)(a.Hq + a.Hkv) * hd + (size_t)h * hd + th];
+  const float qw_r = a.qn_w[th];
+  const float kw_r = a.kn_w[th];
+  const float2 cs_r = a.rope[(size_t)r * half + tr];
   Tok ring[D];
 #pragma unroll
   for (int u = 0; u < D; ++u) load(u, ring[u]);
-
-  const int T = a.kv_len[r];
-  if (!a.active[r]) return;
+  // The exit test below must not move above these loads: hoisted, it put the
+  // row's state and a second round of argument loads in front of the stream.
+  asm volatile("" ::: "memory");
+  if (!act) return;
   const int ctx = T + 1;
   const int n_iter = ctx > s * TPP ? (ctx - s * TPP + tstep - 1) / tstep : 0;
   const bool owner = ((T / TPP) % S) == s;

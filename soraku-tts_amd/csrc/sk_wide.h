@@ -283,9 +283,14 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
   constexpr int SSP = 16;               // partials per thread: n_ss <= 256
   float ssp[(XS && NORM) ? SSP : 1];
   if constexpr (XS && NORM) {
-    const float* sp = a.ss_in + (size_t)(tid >> 4) * a.n_ss + (tid & 15);
+    // index clamped in bounds, value masked: no branch between the loads
+    const float* sp = a.ss_in + (size_t)(tid >> 4) * a.n_ss;
 #pragma unroll
-    for (int i = 0; i < SSP; ++i) ssp[i] = ((tid & 15) + 16 * i < a.n_ss) ? sp[16 * i] : 0.f;
+    for (int i = 0; i < SSP; ++i) {
+      const int j = (tid & 15) + 16 * i;
+      const float v = sp[min(j, a.n_ss - 1)];
+      ssp[i] = j < a.n_ss ? v : 0.f;
+    }
   }
   // Epilogue operands of this thread's output (row r, column oo), loaded at
   // entry: they do not depend on the sums.
@@ -296,10 +301,48 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
   float epi_in = 0.f;
   if constexpr (EPI == EPI_BIAS) epi_in = ok ? a.bias[oo] : 0.f;
   if constexpr (EPI == EPI_RESID) epi_in = ok ? a.res[(size_t)r * a.ldr + oo] : 0.f;
-  Stage sa, sb;
   constexpr int STEP = W * BK;
-  int kb = kbeg + wave * BK;
-  if (kb < kend) load(kb, sa);
+  // This wave's stages: k = kw0 + i * STEP for i < nst.  Up to 4 stages
+  // (every K / split of the 0.6B shapes) the wave issues all of its loads up
+  // front, in straight-line code for its exact stage count, then multiplies
+  // the stages in order: each multiply waits for its own stage only.  (In a
+  // loop with conditional loads the compiler cannot count the loads in flight
+  // and waited for all of them.)  Longer slices use the two-stage ring.
+  const int kw0 = kbeg + wave * BK;
+  const int nst = kw0 < kend ? (kend - kw0 + STEP - 1) / STEP : 0;
+  auto upfront = [&](auto nc) {
+    constexpr int NC = decltype(nc)::value;
+    Stage st[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) load(kw0 + i * STEP, st[i]);
+    asm volatile("" ::: "memory");   // not sunk towards the multiplies
+#pragma unroll
+    for (int i = 0; i < NC; ++i) comp(st[i]);
+  };
+  if (nst == 1) {
+    upfront(std::integral_constant<int, 1>{});
+  } else if (nst == 2) {
+    upfront(std::integral_constant<int, 2>{});
+  } else if (nst == 3) {
+    upfront(std::integral_constant<int, 3>{});
+  } else if (nst == 4) {
+    upfront(std::integral_constant<int, 4>{});
+  } else if (nst > 4) {
+    Stage sa, sb;
+    int kb = kw0;
+    load(kb, sa);
+    for (; kb < kend; kb += 2 * STEP) {
+      const int k1 = kb + STEP, k2 = k1 + STEP;
+      if (k1 < kend) load(k1, sb);
+      comp(sa);
+      if (k1 < kend) {
+        if (k2 < kend) load(k2, sa);
+        comp(sb);
+      }
+    }
+  }
+  // The row's sum of squares is needed only by the epilogue: summed after the
+  // stream, so waiting for the partials never holds back a stage's loads.
   if constexpr (XS && NORM) {
     float t = 0.f;
 #pragma unroll
@@ -309,15 +352,6 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
     t += __shfl_xor(t, 2, 64);
     t += __shfl_xor(t, 1, 64);
     if ((tid & 15) == 0) ssr[tid >> 4] = t;
-  }
-  for (; kb < kend; kb += 2 * STEP) {
-    const int k1 = kb + STEP, k2 = k1 + STEP;
-    if (k1 < kend) load(k1, sb);
-    comp(sa);
-    if (k1 < kend) {
-      if (k2 < kend) load(k2, sa);
-      comp(sb);
-    }
   }
 #pragma unroll
   for (int n = 0; n < NA; ++n)

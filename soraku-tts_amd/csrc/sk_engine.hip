@@ -210,6 +210,7 @@ hipError_t launch_skinny_bf16(SkinnyArgs a, float* partial, unsigned* arrive, hi
     if (tiles <= 64 && a.K % (4 * 32) == 0) a.ksplit = 4;
     else if (tiles <= 128 && a.K % (2 * 32) == 0) a.ksplit = 2;
   }
+  static_assert(SK_MAX_SPLIT >= 4, "the kernel's split-K merge covers the splits chosen here");
   a.partial = partial; a.arrive = arrive;
   const dim3 grid(tiles * a.ksplit);
   if (a.xs)

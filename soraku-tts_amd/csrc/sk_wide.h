@@ -39,6 +39,7 @@ struct SkinnyArgs {
 // Floats per slice partial: two epilogue values per thread (SwiGLU) + 32 row
 // sums of squares.
 constexpr int SK_PSZ = 2 * 512 + 32;
+constexpr int SK_MAX_SPLIT = 4;          // largest K split a launch may use
 
 constexpr int SK_ROWS = 32;             // rows covered (two 16-row MFMA tiles)
 
@@ -301,6 +302,8 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
   float epi_in = 0.f;
   if constexpr (EPI == EPI_BIAS) epi_in = ok ? a.bias[oo] : 0.f;
   if constexpr (EPI == EPI_RESID) epi_in = ok ? a.res[(size_t)r * a.ldr + oo] : 0.f;
+  // the split-form output's gain too (index clamped: no branch around the load)
+  const float gain_in = a.xs_gain ? a.xs_gain[min(oo, a.N - 1)] : 1.f;
   constexpr int STEP = W * BK;
   // This wave's stages: k = kw0 + i * STEP for i < nst.  Up to 4 stages
   // (every K / split of the 0.6B shapes) the wave issues all of its loads up
@@ -394,16 +397,31 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
     if (!last_slice) return;
     if (tid == 0) __hip_atomic_store(a.arrive + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (et) {
+      // All slices' partials loaded together (slice index clamped, unrolled
+      // to SK_MAX_SPLIT), then summed in slice order: a loop over the runtime
+      // S waited for each load before issuing the next.
       const float* all = a.partial + (size_t)tile * S * SK_PSZ;
+      float pv[NA][SK_MAX_SPLIT], sv[XNORM ? SK_MAX_SPLIT : 1];
+#pragma unroll
+      for (int q = 0; q < SK_MAX_SPLIT; ++q) {
+        const size_t qo = (size_t)min(q, S - 1) * SK_PSZ;
+#pragma unroll
+        for (int n = 0; n < NA; ++n) pv[n][q] = all[qo + n * 512 + tid];
+        if constexpr (XNORM) sv[q] = all[qo + 2 * 512 + r];
+      }
 #pragma unroll
       for (int n = 0; n < NA; ++n) {
         float sacc = 0.f;
-        for (int q = 0; q < S; ++q) sacc += all[(size_t)q * SK_PSZ + n * 512 + tid];
+#pragma unroll
+        for (int q = 0; q < SK_MAX_SPLIT; ++q)
+          if (q < S) sacc += pv[n][q];
         c[n] = sacc;
       }
       if constexpr (XNORM) {
         ss = 0.f;
-        for (int q = 0; q < S; ++q) ss += all[(size_t)q * SK_PSZ + 2 * 512 + r];
+#pragma unroll
+        for (int q = 0; q < SK_MAX_SPLIT; ++q)
+          if (q < S) ss += sv[q];
       }
     }
   }
@@ -419,7 +437,7 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
     if constexpr (EPI == EPI_RESID) y = epi_in + y;
     if constexpr (EPI == EPI_SWIGLU) y = y / (1.0f + expf(-y)) * c[NA - 1];
     a.out[(size_t)r * a.ldo + oo] = y;
-    if (a.xs_out) xsplit_store(a.xs_out, r, oo, a.xs_gain ? y * a.xs_gain[oo] : y);
+    if (a.xs_out) xsplit_store(a.xs_out, r, oo, a.xs_gain ? y * gain_in : y);
   }
   if (a.ss_out) {                       // uniform over the workgroup
     if (et) sso[t][v][l] = y * y;

@@ -1716,20 +1716,37 @@ template <typename TL>
 __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, int q, int code) {
   __shared__ float red[2][SWAVES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nr = a.rows_per_utt;         // 1 or 2
   const size_t trow = ((size_t)q * a.V + code) * a.d;
+  // Every operand first, indices clamped in bounds (rows past nr re-read row
+  // 0, dims past d re-read d-1): one round trip, no branch between the
+  // loads, and no load behind the prefix stores that might alias it.
+  float tv[DEPTH_DPT], gv[DEPTH_DPT], pv[2][DEPTH_DPT], hv[2][DEPTH_DPT];
+#pragma unroll
+  for (int i = 0; i < DEPTH_DPT; ++i) {
+    const int k = min(tid + i * SNT, a.d - 1);
+    tv[i] = TL::get(a.table, trow + k);
+    gv[i] = a.w_in[k];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const size_t ro = (size_t)(r0 + (rr < nr ? rr : 0)) * a.d;
+      pv[rr][i] = a.prefix[ro + k];
+      hv[rr][i] = a.hidden[ro + k];
+    }
+  }
   float xv[2][DEPTH_DPT];
-  for (int rr = 0; rr < a.rows_per_utt; ++rr) {
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
     const size_t ro = (size_t)(r0 + rr) * a.d;
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < DEPTH_DPT; ++i) {
       const int k = tid + i * SNT;
-      xv[rr][i] = 0.f;
+      const float p = __fadd_rn(pv[rr][i], __fmul_rn(tv[i], a.scale));
+      const float x = __fadd_rn(hv[rr][i], p);
+      xv[rr][i] = x;
       if (k < a.d) {
-        const float p = __fadd_rn(a.prefix[ro + k], __fmul_rn(TL::get(a.table, trow + k), a.scale));
-        a.prefix[ro + k] = p;
-        const float x = __fadd_rn(a.hidden[ro + k], p);
-        xv[rr][i] = x;
+        if (rr < nr) a.prefix[ro + k] = p;
         ss = fmaf(x, x, ss);
       }
     }
@@ -1737,7 +1754,7 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
     if (lane == 0) red[rr][wave] = ss;
   }
   __syncthreads();
-  for (int rr = 0; rr < a.rows_per_utt; ++rr) {
+  for (int rr = 0; rr < nr; ++rr) {
     float t = 0.f;
 #pragma unroll
     for (int w = 0; w < SWAVES; ++w) t += red[rr][w];
@@ -1747,7 +1764,7 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
     for (int i = 0; i < DEPTH_DPT; ++i) {
       const int k = tid + i * SNT;
       if (k < a.d) {
-        const float y = a.w_in[k] * (xv[rr][i] * inv);
+        const float y = gv[i] * (xv[rr][i] * inv);
         a.abuf[ro + k] = y;
         if (a.xs_abuf) xsplit_store(a.xs_abuf, r0 + rr, k, y);
       }

@@ -1832,12 +1832,14 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   for (int dd = threadIdx.x; dd < a.d; dd += SNT) {
     float e = 0.f;
     for (int j0 = 0; j0 < a.Q; j0 += 16) {
+      // unconditional loads (codebook index clamped), masked afterwards: a
+      // load inside the bound test was waited for before the next was issued
       float t[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        t[j] = (j0 + j < a.Q)
-                   ? TL::get(a.table, (size_t)(j0 + j) * row_stride + (size_t)codes_l[j0 + j] * a.d + dd)
-                   : 0.f;
+      for (int j = 0; j < 16; ++j) {
+        const int jj = min(j0 + j, a.Q - 1);
+        t[j] = TL::get(a.table, (size_t)jj * row_stride + (size_t)codes_l[jj] * a.d + dd);
+      }
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         if (j0 + j < a.Q) e = (j0 + j == 0) ? t[j] : __fadd_rn(e, t[j]);

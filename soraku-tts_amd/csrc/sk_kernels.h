@@ -563,6 +563,69 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
   }
 }
 
+// Residual GEMV with K split over the workgroup's waves (down and output
+// projections): wave w multiplies the K slice [w KT/WAVES, (w+1) KT/WAVES) of
+// all RG rows of the workgroup, so each wave loads only its slice of the
+// activations -- the full-K form loads all of x in every wave, 4x the cache
+// traffic and, at large K, more registers than the weight stream leaves.
+// The WAVES partial sums of an output are added in wave order after one
+// barrier: out[m][n] = res[m][n] + sum_k w[n][k] x[m][k].  Rows past N re-read
+// row N-1 (in bounds) and are not stored.
+template <int M, int KT, int RG, typename WL>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemv_kslice_kernel(GemvArgs a) {
+  constexpr int VEC = WL::VEC;
+  constexpr int KS = KT / WAVES;
+  constexpr int NV = KS / (64 * VEC);
+  static_assert(KT % WAVES == 0 && KS % (64 * VEC) == 0, "K slice must be a multiple of 64 * VEC");
+  static_assert(RG * M <= NT, "one epilogue thread per output");
+  __shared__ float red[WAVES][RG * M];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n0 = blockIdx.x * RG;
+  const int kw = wave * KS;
+  // this wave's activation slice, the residual of this thread's output, then
+  // every weight load: the stream waits only on the small loads before it
+  float xv[M][NV][VEC];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int i = 0; i < VEC; i += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + kw + (j * 64 + lane) * VEC + i);
+        xv[m][j][i] = t.x; xv[m][j][i + 1] = t.y; xv[m][j][i + 2] = t.z; xv[m][j][i + 3] = t.w;
+      }
+  const int eo = tid < RG * M ? tid : 0;
+  const int er = eo / M, em = eo % M;
+  const int en = min(n0 + er, a.N - 1);
+  const float resv = a.res[(size_t)em * a.ldr + en];
+  float wv[RG][NV][VEC];
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const size_t off = (size_t)min(n0 + r, a.N - 1) * KT + kw;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) WL::load(a.w[0], off + (size_t)(j * 64 + lane) * VEC, wv[r][j]);
+  }
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float t = 0.f;
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) t = fmaf(wv[r][j][i], xv[m][j][i], t);
+      t = wave_sum_dpp(t);
+      if (lane == 0) red[wave][r * M + m] = t;
+    }
+  __syncthreads();
+  if (tid < RG * M && n0 + er < a.N) {
+    float sum = red[0][tid];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) sum += red[w][tid];
+    a.out[(size_t)em * a.ldo + n0 + er] = sum + resv;
+  }
+}
+
 // ------------------------------------------------------------ RMSNorm rows
 // out[b] = w * (x[b] (+ x2[b]) * 1/sqrt(mean(.^2) + eps)); grid = rows.
 // Rows with active[b] == 0 are left untouched (prefill of ragged rows).

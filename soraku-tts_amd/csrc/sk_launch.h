@@ -75,12 +75,43 @@ static hipError_t launch_fast_k(const GemvArgs& a, hipStream_t st) {
   }
 }
 
+// K-sliced residual GEMV (4 rows per workgroup, K split over its waves), for
+// the K whose slice is a whole number of 64-lane loads.
+template <int M, int KT, typename WL>
+static bool try_kslice(const GemvArgs& a, hipStream_t st, hipError_t* err) {
+  if constexpr ((KT / WAVES) % (64 * WL::VEC) == 0) {
+    constexpr int RG = 4;
+    const int grid = (a.N + RG - 1) / RG;
+    hipLaunchKernelGGL((gemv_kslice_kernel<M, KT, RG, WL>), dim3(grid), dim3(NT), 0, st, a);
+    *err = hipGetLastError();
+    return true;
+  } else {
+    return false;
+  }
+}
+// Residual GEMVs that take the K-sliced form: BF16 weights (measured at the
+// 1.7B shape: K = 2048, 4096, 6144 all faster); with FP32 weights the full-K
+// form with activations shared through LDS is faster (0.6B: K = 2048, 3072).
+template <typename WL>
+static inline bool use_kslice(int K) {
+  return std::is_same<WL, WBF16>::value && (K == 2048 || K == 4096 || K == 6144);
+}
+
 // K values with a specialised kernel: the decode shapes' hidden sizes for
 // GEMVs fed by a norm / SwiGLU / classifier, and the inner sizes for the
 // down / output projections.  Returns false when no specialisation applies.
 template <int M, int PRO, int EPI, typename WL>
 static bool launch_fast(const GemvArgs& a, hipStream_t st, hipError_t* err) {
   if constexpr (PRO == PRO_NONE && EPI == EPI_RESID) {
+    if (use_kslice<WL>(a.K)) {
+      switch (a.K) {
+        case 2048: if (try_kslice<M, 2048, WL>(a, st, err)) return true; break;
+        case 3072: if (try_kslice<M, 3072, WL>(a, st, err)) return true; break;
+        case 4096: if (try_kslice<M, 4096, WL>(a, st, err)) return true; break;
+        case 6144: if (try_kslice<M, 6144, WL>(a, st, err)) return true; break;
+        default: break;
+      }
+    }
     switch (a.K) {
       case 2048: *err = launch_fast_k<M, 2048, PRO, EPI, WL>(a, st); return true;
       case 3072: *err = launch_fast_k<M, 3072, PRO, EPI, WL>(a, st); return true;

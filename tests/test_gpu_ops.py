@@ -49,7 +49,7 @@ def test_rmsnorm_and_add_rmsnorm(ops, hip_device, eps):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("I", [2048, 3072])
+@pytest.mark.parametrize("I", [2048, 3072, 4096, 6144])
 def test_swiglu_and_down_gemv(ops, hip_device, bf16, I):
     import torch
 
@@ -69,6 +69,28 @@ def test_swiglu_and_down_gemv(ops, hip_device, bf16, I):
     assert _rel(act.cpu().numpy(), ref_act) < TOL
     y = ops.down_residual_gemv(B, D, I)(act, _t(wd, hip_device, dt), _t(res, hip_device))
     ref_y = act.cpu().numpy().astype(np.float64) @ wd.T.astype(np.float64) + res
+    assert _rel(y.cpu().numpy(), ref_y) < TOL
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("I", [2048, 6144])
+def test_down_gemv_ragged_rows(ops, hip_device, bf16, I):
+    """Down projection + residual with an output count that is not a multiple
+    of the 4 rows a K-sliced workgroup owns (the last workgroup's extra rows
+    re-read row N-1 and are not stored)."""
+    rng = np.random.default_rng(5)
+    D, B = 1030, 2
+    import torch
+
+    act = rng.standard_normal((B, I), dtype=np.float32)
+    wd = (rng.standard_normal((D, I), dtype=np.float32) * 0.02).astype(np.float32)
+    res = rng.standard_normal((B, D), dtype=np.float32)
+    if bf16:
+        wd = om.round_bf16(wd)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    y = ops.down_residual_gemv(B, D, I)(_t(act, hip_device), _t(wd, hip_device, dt), _t(res, hip_device))
+    ref_y = act.astype(np.float64) @ wd.T.astype(np.float64) + res
+    assert y.shape == (B, D)
     assert _rel(y.cpu().numpy(), ref_y) < TOL
 
 

@@ -1,7 +1,7 @@
 """Whole-frame engine parity on the GPU against the reference's golden
 vectors and the oracle.
 
-Tolerance (BASELINE north star): logits within 1e-3 relative (normalised by
+Tolerance: logits within 1e-3 relative (normalised by
 the row's max |logit|) of the FP32 reference path; tokens bit-exact when both
 sides get the same logits and the same uniform draw."""
 

@@ -51,6 +51,7 @@ struct sk_engine {
   int rows = 0, G = 0, nqkv = 0, inner_max = 0, max_chunks = 0;
   bool wide = false;          // more rows than the GEMV kernels take: skinny MFMA GEMMs
   int attn_splits = 0;        // > 0: attention_stream_kernel with this many splits per (row, kv head)
+  bool split_k = false;       // many-row BF16 GEMMs may split K (workgroups i, i + 8, ... share an XCD)
   int device = 0;
   hipStream_t stream = nullptr;
 
@@ -146,8 +147,10 @@ int validate_config(const sk_config* c) {
            "n_utts * cfg_rows must be in [1, %d] (decode rows)", SK_ROWS);
   SK_CHECK(c->n_utts * c->cfg_rows <= 4 || c->depth_inner % 32 == 0, SK_EINVAL,
            "depth_inner must be a multiple of 32 for more than 4 decode rows");
-  SK_CHECK(c->n_utts * c->cfg_rows <= 4 || c->weight_dtype != SK_BF16 || c->d_model <= 4096, SK_EINVAL,
-           "d_model must be at most 4096 for more than 4 decode rows with BF16 weights");
+  // The many-row sampler writes the next depth input with DEPTH_DPT values
+  // per thread (depth_input_rows): d_model <= DEPTH_DPT * SNT = 4096.
+  SK_CHECK(c->n_utts * c->cfg_rows <= 4 || c->d_model <= DEPTH_DPT * SNT, SK_EINVAL,
+           "d_model must be at most %d for more than 4 decode rows", DEPTH_DPT * SNT);
   SK_CHECK(c->max_ctx >= 2 && c->max_ctx <= 65536, SK_EINVAL, "max_ctx must be in [2, 65536]");
   SK_CHECK(c->max_frames >= 1, SK_EINVAL, "max_frames must be positive");
   SK_CHECK(c->n_language == 0 || c->n_language == 4, SK_EINVAL, "n_language must be 0 or 4");
@@ -203,10 +206,10 @@ hipError_t launch_skinny_w(const SkinnyArgs& a, hipStream_t st) {
 // a multiple of 32); the slice partials live in `partial`, the arrival counts
 // in `arrive` (zero between launches).
 template <int EPI, bool NORM>
-hipError_t launch_skinny_bf16(SkinnyArgs a, float* partial, unsigned* arrive, hipStream_t st) {
+hipError_t launch_skinny_bf16(SkinnyArgs a, float* partial, unsigned* arrive, bool allow_split, hipStream_t st) {
   const int tiles = (a.N + 15) / 16;
   a.ksplit = 1;
-  if (tiles % 8 == 0) {
+  if (allow_split && tiles % 8 == 0) {
     if (tiles <= 64 && a.K % (4 * 32) == 0) a.ksplit = 4;
     else if (tiles <= 128 && a.K % (2 * 32) == 0) a.ksplit = 2;
   }
@@ -221,7 +224,8 @@ hipError_t launch_skinny_bf16(SkinnyArgs a, float* partial, unsigned* arrive, hi
 }
 template <int EPI, bool NORM = false>
 hipError_t launch_skinny(sk_engine* e, const SkinnyArgs& a) {
-  return e->c.weight_dtype == SK_BF16 ? launch_skinny_bf16<EPI, NORM>(a, e->sk_partial, e->sk_arrive, e->stream)
+  return e->c.weight_dtype == SK_BF16 ? launch_skinny_bf16<EPI, NORM>(a, e->sk_partial, e->sk_arrive, e->split_k,
+                                                                      e->stream)
                                       : launch_skinny_w<EPI, NORM, WF32>(a, e->stream);
 }
 
@@ -580,6 +584,27 @@ int capture(sk_engine* e, hipError_t (*body)(sk_engine*), hipGraph_t* g, hipGrap
   return SK_OK;
 }
 
+// Whether workgroups whose ids agree modulo 8 run on one XCD (read from the
+// XCC_ID register of 2048 probe workgroups): the split-K merge of the
+// many-row GEMMs relies on it.  Single-XCD partitions pass trivially.
+hipError_t probe_xcd_mapping(hipStream_t st, bool* ok) {
+  *ok = false;
+  unsigned* d = nullptr;
+  hipError_t err = hipMalloc(reinterpret_cast<void**>(&d), XCD_PROBE_WGS * sizeof(unsigned));
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(xcd_probe_kernel, dim3(XCD_PROBE_WGS), dim3(64), 0, st, d);
+  std::vector<unsigned> ids(XCD_PROBE_WGS);
+  err = hipGetLastError();
+  if (err == hipSuccess) err = hipMemcpyAsync(ids.data(), d, ids.size() * sizeof(unsigned), hipMemcpyDeviceToHost, st);
+  if (err == hipSuccess) err = hipStreamSynchronize(st);
+  hipFree(d);
+  if (err != hipSuccess) return err;
+  bool same = true;
+  for (int i = 8; i < XCD_PROBE_WGS; ++i) same = same && ids[i] == ids[i % 8];
+  *ok = same;
+  return hipSuccess;
+}
+
 bool parse_layer(const char* key, int* layer, const char** rest) {
   const char* pre = "trunk.layers.";
   const size_t n = strlen(pre);
@@ -715,6 +740,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     if (he == hipSuccess) he = hipStreamSynchronize(e->stream);
   }
   if (he == hipSuccess) he = prepare_sampler();
+  if (he == hipSuccess && e->wide && c.weight_dtype == SK_BF16) he = probe_xcd_mapping(e->stream, &e->split_k);
   if (he == hipSuccess)
     he = hipFuncSetAttribute(c.kv_dtype == SK_BF16 ? reinterpret_cast<const void*>(attention_kernel<uint16_t>)
                                                    : reinterpret_cast<const void*>(attention_kernel<float>),
@@ -922,10 +948,13 @@ int sk_set_row_state(sk_engine* e, int32_t row, int32_t kv_len, int32_t position
   SK_CHECK(row >= 0 && row < e->rows, SK_EINVAL, "row %d out of range", row);
   SK_CHECK(kv_len >= 0 && kv_len < e->c.max_ctx, SK_EKVFULL, "kv_len %d outside [0, max_ctx)", kv_len);
   SK_CHECK(position >= 0 && position < e->c.max_ctx, SK_EINVAL, "position %d outside [0, max_ctx)", position);
-  SK_HIP(hipMemcpy(e->kv_len + row, &kv_len, sizeof(int), hipMemcpyHostToDevice));
-  SK_HIP(hipMemcpy(e->pos + row, &position, sizeof(int), hipMemcpyHostToDevice));
+  // Queued replays advance kv_len / pos on the device: let them finish before
+  // the row's state is overwritten, and write it on the engine's stream.
+  SK_HIP(hipStreamSynchronize(e->stream));
   const int one = 1;
-  SK_HIP(hipMemcpy(e->active + row, &one, sizeof(int), hipMemcpyHostToDevice));
+  SK_HIP(hipMemcpyAsync(e->kv_len + row, &kv_len, sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->pos + row, &position, sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(e->active + row, &one, sizeof(int), hipMemcpyHostToDevice, e->stream));
   hipLaunchKernelGGL(rope_rows_kernel, dim3(1), dim3(NT), 0, e->stream, e->pos, e->inv_freq,
                      e->c.head_dim / 2, row, e->rope);
   SK_HIP(hipGetLastError());

@@ -179,7 +179,10 @@ typedef __bf16 sbf8 __attribute__((ext_vector_type(8)));
 // its L2.  Each slice stores its partial tile, waits until the stores are
 // acknowledged, and counts itself in arrive[tile] (an L2 atomic); the last
 // slice to arrive adds the S partials in slice order, applies the epilogue and
-// resets the count.  No workgroup waits for another.
+// resets the count.  No workgroup waits for another.  The arrival count and
+// the partials are workgroup-scope operations: they are coherent only because
+// every slice of a tile runs on one XCD.  sk_create checks that mapping with
+// xcd_probe_kernel and launches without split K when it does not hold.
 //
 // Split input (XS): x arrives in split form, written by the kernel that
 // produced it with this GEMM's norm gain applied, so a stage is four 16-byte
@@ -187,6 +190,15 @@ typedef __bf16 sbf8 __attribute__((ext_vector_type(8)));
 // squares is the sum of the producer's per-tile partials (ss_in).  Outputs
 // can be written in split form for the next GEMM (xs_out, with that GEMM's
 // gain) together with their per-tile sums of squares (ss_out).
+// XCC_ID hardware register of each workgroup (one 64-thread wave each): the
+// XCD it runs on.  Split K needs workgroups whose ids agree modulo 8 to share
+// an XCD (and so an L2).
+__global__ __launch_bounds__(64) void xcd_probe_kernel(unsigned* ids) {
+  const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);   // hwreg(HW_REG_XCC_ID)
+  if (threadIdx.x == 0) ids[blockIdx.x] = xcc;
+}
+constexpr int XCD_PROBE_WGS = 2048;
+
 template <int EPI, int W, bool NORM, bool XS>
 __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
   static_assert(!XS || W == 8, "split input: one thread per (row, 16th of the partial sums)");

@@ -81,6 +81,7 @@ def shape_from_model(model) -> DecodeShape:
         n_codebooks=int(cfg.num_codebooks), codebook_size=int(cfg.codebook_size),
         text_vocab=int(t.vocab_size), trunk_eps=float(t.rms_norm_eps), rope_theta=float(theta),
         n_language=4 if getattr(cfg, "language_token_ids", ()) else 0,
+        tie_audio_head=bool(getattr(cfg, "tie_audio_head", True)),   # model.py:131,141-145,172
     )
 
 

@@ -24,7 +24,8 @@ def load_golden(name: str):
     sh = [int(v) for v in f["shape"]]
     s = Shape(d_model=sh[0], n_layers=sh[1], n_q_heads=sh[2], n_kv_heads=sh[3], head_dim=sh[4],
               trunk_inter=sh[5], depth_mult=sh[6], n_codebooks=sh[7], codebook_size=sh[8],
-              text_vocab=sh[9], n_language=sh[10])
+              text_vocab=sh[9], n_language=sh[10],
+              tie_audio_head=bool(int(f["tie_audio_head"])) if "tie_audio_head" in f.files else True)
     gen = {}
     for k in f.files:
         if k.startswith("gen_"):

@@ -17,7 +17,15 @@ Recorded per fixture: the seed and shape (weights are regenerated from them by
 handed to ``torch.multinomial`` (sampled runs), the returned codes and the
 depth-input hidden state of every frame for both branches.
 
-Usage:  python tests/golden/make_golden.py [--large]
+Fixtures: ``tiny_greedy``, ``tiny_sampled`` (q0 overrides), ``tiny_nocfg_topp``,
+``tiny_untied`` (untied classifier head ``depth_head.out_proj``, model.py:141-145,
+171-174) and, with ``--large``, ``q06b_greedy`` (Qwen3-0.6B shape, prefix 65,
+greedy) and ``q06b_sampled`` (Qwen3-0.6B shape with the full-utterance prefix
+layout: 96 text ids + BOS frame + 144 prompt frames for the cond row, the text
+BOS id + BOS frame + the prompt for the uncond row, CFG 1.5, T 0.9, top-k 50,
+top-p 0.95: the V = 2051 probability vectors of ``torch.multinomial``).
+
+Usage:  python tests/golden/make_golden.py [--large] [--only NAME ...]
 """
 
 from __future__ import annotations
@@ -56,6 +64,7 @@ def build_reference(shape: Shape, weights, language_ids=()):
     trunk = Qwen3Model._from_config(tcfg, dtype=torch.float32, attn_implementation="sdpa")
     cfg = refmod.SorakuV2Config(num_codebooks=shape.n_codebooks,
                                 codebook_size=shape.codebook_size,
+                                tie_audio_head=shape.tie_audio_head,
                                 language_token_ids=tuple(language_ids))
     model = refmod.SorakuTTSv2(cfg, trunk=trunk)
     state = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in weights.items()}
@@ -115,6 +124,7 @@ def run(shape: Shape, *, wseed, norm_gain_std, bias_std, text_ids, prompt_codes,
         shape=np.array([shape.d_model, shape.n_layers, shape.n_q_heads, shape.n_kv_heads,
                         shape.head_dim, shape.trunk_inter, shape.depth_mult, shape.n_codebooks,
                         shape.codebook_size, shape.text_vocab, len(language_ids)], np.int64),
+        tie_audio_head=np.int64(shape.tie_audio_head),
         seed=np.int64(wseed), norm_gain_std=np.float64(norm_gain_std), bias_std=np.float64(bias_std),
         text_ids=np.asarray(text_ids, np.int64), uncond_ids=np.asarray(uncond_ids, np.int64),
         prompt_codes=np.asarray(prompt_codes, np.int64).reshape(-1, shape.n_codebooks),
@@ -132,8 +142,13 @@ def run(shape: Shape, *, wseed, norm_gain_std, bias_std, text_ids, prompt_codes,
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--large", action="store_true", help="also write the Qwen3-0.6B-shaped fixture")
+    ap.add_argument("--large", action="store_true", help="also write the Qwen3-0.6B-shaped fixtures")
+    ap.add_argument("--only", nargs="*", default=None, help="write only these fixtures")
     args = ap.parse_args()
+
+    def want(name):
+        return args.only is None or name in args.only
+
     rng = np.random.default_rng(7)
     s = Shape(**{**TINY.__dict__, "n_language": 4})
     lang = (90, 91, 92, 93)
@@ -141,16 +156,25 @@ def main():
     prompt = rng.integers(0, s.codebook_size, size=(3, s.n_codebooks))
     common = dict(wseed=0, norm_gain_std=0.1, bias_std=0.02, text_ids=text,
                   prompt_codes=prompt, uncond_ids=[5], language_ids=lang)
-    fx = run(s, **common, max_new_frames=6, min_new_frames=2, temperature=0.0,
-             cfg_scale=1.5)
-    np.savez_compressed(os.path.join(HERE, "tiny_greedy.npz"), **fx)
-    fx = run(s, **common, max_new_frames=8, min_new_frames=2, temperature=0.9, top_k=8,
-             top_p=0.9, temperature_q0=0.7, top_k_q0=5, top_p_q0=0.8, cfg_scale=1.5, seed=123)
-    np.savez_compressed(os.path.join(HERE, "tiny_sampled.npz"), **fx)
-    fx = run(s, **common, max_new_frames=4, min_new_frames=0, temperature=1.0, top_k=None,
-             top_p=0.6, cfg_scale=1.0, seed=5)
-    np.savez_compressed(os.path.join(HERE, "tiny_nocfg_topp.npz"), **fx)
-    if args.large:
+    if want("tiny_greedy"):
+        fx = run(s, **common, max_new_frames=6, min_new_frames=2, temperature=0.0,
+                 cfg_scale=1.5)
+        np.savez_compressed(os.path.join(HERE, "tiny_greedy.npz"), **fx)
+    if want("tiny_sampled"):
+        fx = run(s, **common, max_new_frames=8, min_new_frames=2, temperature=0.9, top_k=8,
+                 top_p=0.9, temperature_q0=0.7, top_k_q0=5, top_p_q0=0.8, cfg_scale=1.5, seed=123)
+        np.savez_compressed(os.path.join(HERE, "tiny_sampled.npz"), **fx)
+    if want("tiny_nocfg_topp"):
+        fx = run(s, **common, max_new_frames=4, min_new_frames=0, temperature=1.0, top_k=None,
+                 top_p=0.6, cfg_scale=1.0, seed=5)
+        np.savez_compressed(os.path.join(HERE, "tiny_nocfg_topp.npz"), **fx)
+    # the draws above advance rng; later fixtures take their own generators
+    if want("tiny_untied"):
+        su = Shape(**{**TINY.__dict__, "n_language": 4, "tie_audio_head": False})
+        fx = run(su, **{**common, "wseed": 4}, max_new_frames=5, min_new_frames=1, temperature=0.9,
+                 top_k=8, top_p=0.9, cfg_scale=1.5, seed=31)
+        np.savez_compressed(os.path.join(HERE, "tiny_untied.npz"), **fx)
+    if args.large and want("q06b_greedy"):
         s6 = QWEN3_06B
         text6 = rng.integers(0, s6.text_vocab, size=40).tolist()
         prompt6 = rng.integers(0, s6.codebook_size, size=(24, s6.n_codebooks))
@@ -158,6 +182,15 @@ def main():
                  prompt_codes=prompt6, uncond_ids=[text6[0]], max_new_frames=3,
                  min_new_frames=8, temperature=0.0, cfg_scale=1.5)
         np.savez_compressed(os.path.join(HERE, "q06b_greedy.npz"), **fx)
+    if args.large and want("q06b_sampled"):
+        s6 = QWEN3_06B
+        r6 = np.random.default_rng(2051)
+        text6 = r6.integers(0, s6.text_vocab, size=96).tolist()
+        prompt6 = r6.integers(0, s6.codebook_size, size=(144, s6.n_codebooks))
+        fx = run(s6, wseed=2, norm_gain_std=0.1, bias_std=0.02, text_ids=text6,
+                 prompt_codes=prompt6, uncond_ids=[151643], max_new_frames=2,
+                 min_new_frames=8, temperature=0.9, top_k=50, top_p=0.95, cfg_scale=1.5, seed=0)
+        np.savez_compressed(os.path.join(HERE, "q06b_sampled.npz"), **fx)
 
 
 if __name__ == "__main__":

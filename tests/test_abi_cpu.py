@@ -168,3 +168,28 @@ def test_synthetic_weights_match_oracle():
     assert sorted(a) == sorted(b)
     for k in a:
         np.testing.assert_array_equal(a[k], b[k])
+
+
+def test_shape_from_model_reads_the_untied_head():
+    """shape_from_model follows SorakuV2Config.tie_audio_head (model.py:131,
+    141-145,171-174): an untied model binds depth_head.out_proj."""
+    from types import SimpleNamespace
+
+    from soraku_amd.config import shape_from_model
+    from soraku_amd.synthetic import weight_shapes
+
+    trunk = SimpleNamespace(config=SimpleNamespace(
+        hidden_size=64, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+        intermediate_size=96, vocab_size=100, rms_norm_eps=1e-6, rope_parameters={"rope_theta": 1e6}))
+    for tie in (True, False):
+        cfg = SimpleNamespace(depth_ffn_mult=2, num_codebooks=4, codebook_size=32, language_token_ids=(),
+                              tie_audio_head=tie)
+        s = shape_from_model(SimpleNamespace(config=cfg, trunk=trunk))
+        assert s.tie_audio_head is tie
+        keys = weight_shapes(s)
+        assert ("depth_head.out_proj" in keys) is (not tie)
+        if not tie:
+            assert keys["depth_head.out_proj"] == (4, 35, 64)
+    # a config without the field is a tied head (the reference default)
+    cfg = SimpleNamespace(depth_ffn_mult=2, num_codebooks=4, codebook_size=32)
+    assert shape_from_model(SimpleNamespace(config=cfg, trunk=trunk)).tie_audio_head is True

@@ -51,8 +51,8 @@ def _engine(f, s, gen, w, hip_device, max_ctx=None):
 def _rowwise_rel(got, ref):
     fin = np.isfinite(ref)
     assert (np.isfinite(got) == fin).all()
-    num = np.where(fin, np.abs(got - ref), 0).max(axis=-1)
-    den = np.where(fin, np.abs(ref), 0).max(axis=-1)
+    num = np.abs(np.where(fin, got, 0) - np.where(fin, ref, 0)).max(axis=-1)
+    den = np.abs(np.where(fin, ref, 0)).max(axis=-1)
     return float((num / den).max())
 
 
@@ -70,7 +70,7 @@ def _teacher_forced(e, f, s, gen):
     return np.stack(out[:n_calls])
 
 
-@pytest.mark.parametrize("name", ["tiny_greedy", "tiny_sampled", "tiny_nocfg_topp", "q06b_greedy"])
+@pytest.mark.parametrize("name", ["tiny_greedy", "tiny_sampled", "tiny_nocfg_topp", "tiny_untied", "q06b_greedy"])
 def test_teacher_forced_logits_match_reference(hip_device, name):
     f, s, gen = load_golden(name)
     e = _engine(f, s, gen, _weights(f, s), hip_device)

@@ -1,0 +1,252 @@
+"""Sampled decoding at the benchmark shapes and prefix lengths, against the
+reference's vectors and the oracle.
+
+* Qwen3-0.6B, FP32, the full-utterance prefix (96 text ids + BOS frame + 144
+  prompt frames = 241 positions for the cond row, text BOS + BOS frame + the
+  prompt = 146 for the uncond row), CFG 1.5, T 0.9, top-k 50, top-p 0.95:
+  teacher-forced logits and V = 2051 distributions against the reference
+  (``q06b_sampled`` fixture), then free-running decode against the float64
+  oracle under identical uniforms.
+* Qwen3-0.6B with 543 / 448 cached positions: decode attention crosses a
+  32-token chunk edge and merges more than 16 chunks (contexts above 512).
+* Qwen3-1.7B, BF16 weights, 240-position prefix, sampled.
+* An untied classifier head bound through ``GraphFrameEngine(model=...)``.
+
+Tolerance: logits within 1e-3 of the reference / oracle, relative to the
+row's largest |logit|.  Codes: equal under identical uniforms; a difference is
+accepted only where the oracle's uniform lies within 1e-5 of a CDF boundary
+of its own distribution (or its top-p mass within 1e-5 of the threshold),
+i.e. where a sub-tolerance logit difference can move the draw, and the
+comparison stops there.
+"""
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+from conftest import load_golden
+from oracle.generate import Record, generate, start_states
+from oracle.model import QWEN3_06B, QWEN3_17B, OracleModel, synthetic_weights
+from oracle.sampler import apply_masks, candidates, filtered_probs, topp_weights
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+MARGIN = 1e-5
+C3 = dict(cfg_scale=1.5, temperature=0.9, top_k=50, top_p=0.95, min_new_frames=8)
+
+
+def _shape(s):
+    from soraku_amd.config import DecodeShape
+
+    return DecodeShape(**{k: getattr(s, k) for k in DecodeShape.__dataclass_fields__})
+
+
+def _rowwise_rel(got, ref):
+    got, ref = np.atleast_2d(got), np.atleast_2d(ref)
+    fin = np.isfinite(ref)
+    assert (np.isfinite(got) == fin).all()
+    num = np.abs(np.where(fin, got, 0) - np.where(fin, ref, 0)).max(axis=-1)
+    den = np.abs(np.where(fin, ref, 0)).max(axis=-1)
+    return float((num / den).max())
+
+
+def _engine(s, w, hip_device, text, uncond, prompt, max_ctx, bf16=False, **gen):
+    from soraku_amd import GraphFrameEngine
+
+    e = GraphFrameEngine(device=hip_device, max_cache_len=max_ctx, cfg_scale=gen["cfg_scale"], batch=2,
+                         state_dict=w, shape=_shape(s), bf16=bf16)
+    e.set_temperature(gen["temperature"])
+    e.set_sampling(sampled=gen["temperature"] > 0, top_k=gen["top_k"], top_p=gen["top_p"])
+    e.set_debug(True)
+    e.prefill(text, uncond, prompt)
+    e.capture()
+    return e
+
+
+def _draw_margin(masked, gen, u):
+    """Distance of u from the nearest CDF boundary of the oracle's filtered
+    distribution, and of the top-p mass from its threshold."""
+    x = (np.asarray(masked, np.float32) / np.float32(gen["temperature"])).astype(np.float32)
+    order = candidates(x, gen["top_k"])
+    _, W, n_keep = topp_weights(x[order], gen["top_p"])
+    F = W[:n_keep] / W[n_keep - 1]
+    m_u = float(np.min(np.abs(F - u)))
+    m_p = float(np.min(np.abs(W / W[-1] - float(np.float32(gen["top_p"])))))
+    return min(m_u, m_p)
+
+
+def _free_running_vs_oracle(e, m, states, s, u, gen, text, prompt, uncond):
+    """Decode len(u) frames on the engine and the oracle with the same
+    uniforms; compare every step's masked logits and code.  Returns
+    (frames compared in full, largest logit error)."""
+    n = u.shape[0]
+    rec = Record()
+    ref, _ = generate(m, input_ids=text, prompt_codes=prompt, uncond_input_ids=uncond, uniforms=u,
+                      max_new_frames=n, batched=True, record=rec, states=states, **gen)
+    worst = 0.0
+    for fi in range(n):
+        codes, lg = e.step_frame(mask_eos_q0=fi < gen["min_new_frames"], uniforms=u[fi], return_logits=True)
+        codes = codes.numpy().reshape(-1)
+        oracle_eos = fi >= ref.shape[0]          # the oracle drew EOS at q0 of this frame
+        for q in range(len(rec.merged[fi])):
+            want = apply_masks(rec.merged[fi][q], q=q, frame_index=fi, min_new_frames=gen["min_new_frames"],
+                               bos_id=s.bos_id, eos_id=s.eos_id, pad_id=s.pad_id)
+            rel = _rowwise_rel(lg[0][q], want)
+            worst = max(worst, rel)
+            assert rel < LOGIT_TOL, (fi, q, rel)
+            want_code = s.eos_id if oracle_eos else ref[fi][q]
+            if codes[q] != want_code:
+                margin = _draw_margin(want, gen, float(u[fi][q]))
+                print(f"codes differ at frame {fi} codebook {q}: engine {codes[q]}, oracle {want_code}, "
+                      f"margin {margin:.2e}")
+                assert margin < MARGIN
+                return fi, worst
+        if oracle_eos:
+            return fi, worst
+    return n, worst
+
+
+def _c3_inputs(f):
+    return f["text_ids"], f["uncond_ids"], f["prompt_codes"]
+
+
+def test_c3_prefix_teacher_forced_matches_reference(hip_device):
+    """Teacher-forced on the reference's own codes: masked CFG logits of every
+    depth step and the top-k / top-p distribution handed to torch.multinomial
+    (V = 2051), from GPU logits, equal the reference's."""
+    f, s, gen = load_golden("q06b_sampled")
+    assert f["text_ids"].size + 1 + f["prompt_codes"].shape[0] == 241
+    w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                          bias_std=float(f["bias_std"]))
+    text, uncond, prompt = _c3_inputs(f)
+    g = {k: gen[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
+    e = _engine(s, w, hip_device, text, uncond, prompt, 260, **g)
+    hid = e.hidden()
+    assert np.abs(hid - f["hidden"][0]).max() / np.abs(f["hidden"][0]).max() < 1e-4
+    got = []
+    for fi in range(f["codes"].shape[0]):
+        _, lg = e.step_frame(mask_eos_q0=True, uniforms=np.zeros(s.n_codebooks), forced_codes=f["codes"][fi],
+                             return_logits=True)
+        got.extend(lg[0])
+        hid = e.hidden()
+        assert np.abs(hid - f["hidden"][fi + 1]).max() / np.abs(f["hidden"][fi + 1]).max() < 1e-4
+    e.close()
+    got = np.stack(got)
+    rel = _rowwise_rel(got, f["sample_logits"])
+    print(f"C3 prefix, 0.6B FP32: max row-relative logit error vs reference {rel:.3e}")
+    assert rel < LOGIT_TOL
+    worst = 0.0
+    for i, lg in enumerate(got):
+        pr = filtered_probs((lg / np.float32(gen["temperature"])).astype(np.float32), gen["top_k"], gen["top_p"])
+        np.testing.assert_array_equal(pr > 0, f["probs"][i] > 0)
+        worst = max(worst, float(np.abs(pr - f["probs"][i]).max()))
+    print(f"C3 prefix: max |p_gpu - p_reference| {worst:.2e}")
+    assert worst < 1e-4
+
+
+def test_c3_prefix_sampled_codes_match_oracle(hip_device):
+    """Free-running sampled decode at the C3 settings: 10 frames of 16
+    codebooks, codes and logits against the float64 oracle under identical
+    uniforms."""
+    f, s, _ = load_golden("q06b_sampled")
+    w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                          bias_std=float(f["bias_std"]))
+    text, uncond, prompt = _c3_inputs(f)
+    n = 10
+    u = np.random.default_rng(240).random((n, s.n_codebooks))
+    m = OracleModel(s, w, np.float64)
+    states = start_states(m, text, prompt, uncond, C3["cfg_scale"], 260)
+    e = _engine(s, w, hip_device, text, uncond, prompt, 260, **C3)
+    done, worst = _free_running_vs_oracle(e, m, states, s, u, C3, text, prompt, uncond)
+    e.close()
+    print(f"C3 sampled: {done} frames equal, max logit error {worst:.3e}")
+    assert done >= 6
+
+
+def test_q06b_context_past_512_tokens(hip_device):
+    """Cond row 543 cached positions, uncond 448, KV capacity 600: decode
+    attention merges 17-18 chunks of 32 (past the merge kernel's first
+    block of 16) and the frames cross the chunk edge at 544 (cond) and start
+    a chunk at 448 (uncond); teacher-forced logits against the float64
+    oracle, then sampled codes."""
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)
+    w = synthetic_weights(s, 12, norm_gain_std=0.1, bias_std=0.02)
+    rng = np.random.default_rng(12)
+    text = rng.integers(0, s.text_vocab, 96)
+    prompt = rng.integers(0, s.codebook_size, (446, s.n_codebooks))
+    uncond = np.array([7])
+    assert text.size + 1 + prompt.shape[0] == 543 and uncond.size + 1 + prompt.shape[0] == 448
+    m = OracleModel(s, w, np.float64)
+    states = start_states(m, text, prompt, uncond, C3["cfg_scale"], 600)
+    e = _engine(s, w, hip_device, text, uncond, prompt, 600, **C3)
+    u = np.random.default_rng(13).random((4, s.n_codebooks))
+    done, worst = _free_running_vs_oracle(e, m, states, s, u, C3, text, prompt, uncond)
+    e.close()
+    print(f"0.6B at 543/448 positions: {done} frames equal, max logit error {worst:.3e}")
+    assert done >= 3
+
+
+def test_q17b_c5_prefix_sampled(hip_device):
+    """Qwen3-1.7B shape, BF16 weights (FP32 accumulation, FP32 KV), 240-position
+    prefix (95 text ids + BOS frame + 144 prompt frames; uncond 146), sampled
+    at T 0.9, top-k 50, top-p 0.95, CFG 1.5: logits and codes against the
+    float64 oracle on the same BF16-rounded weights."""
+    from test_gpu_engine import _device_weights
+
+    s = dataclasses.replace(QWEN3_17B, text_vocab=4096)
+    w = _device_weights(s, 240, hip_device)
+    rng = np.random.default_rng(240)
+    text = rng.integers(0, s.text_vocab, 95)
+    prompt = rng.integers(0, s.codebook_size, (144, s.n_codebooks))
+    uncond = np.array([11])
+    m = OracleModel(s, w, np.float64)
+    states = start_states(m, text, prompt, uncond, C3["cfg_scale"], 260)
+    e = _engine(s, w, hip_device, text, uncond, prompt, 260, bf16=True, **C3)
+    u = np.random.default_rng(241).random((4, s.n_codebooks))
+    done, worst = _free_running_vs_oracle(e, m, states, s, u, C3, text, prompt, uncond)
+    e.close()
+    print(f"1.7B BF16 at 240/146 positions: {done} frames equal, max logit error {worst:.3e}")
+    assert done >= 3
+
+
+def test_untied_head_through_model_binding(hip_device):
+    """GraphFrameEngine(model) with a SorakuTTSv2-like module whose config has
+    tie_audio_head=False binds depth_head.out_proj as the classifier
+    (model.py:141-145,171-174): teacher-forced logits equal the reference's
+    ``tiny_untied`` vectors."""
+    from types import SimpleNamespace
+
+    import torch
+    from soraku_amd import GraphFrameEngine
+
+    f, s, gen = load_golden("tiny_untied")
+    assert not s.tie_audio_head
+    w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                          bias_std=float(f["bias_std"]))
+    lang = tuple(int(v) for v in f["language_ids"])
+    trunk = SimpleNamespace(config=SimpleNamespace(
+        hidden_size=s.d_model, num_hidden_layers=s.n_layers, num_attention_heads=s.n_q_heads,
+        num_key_value_heads=s.n_kv_heads, head_dim=s.head_dim, intermediate_size=s.trunk_inter,
+        vocab_size=s.text_vocab, rms_norm_eps=s.trunk_eps, rope_parameters={"rope_theta": s.rope_theta}))
+    cfg = SimpleNamespace(depth_ffn_mult=s.depth_mult, num_codebooks=s.n_codebooks, codebook_size=s.codebook_size,
+                          language_token_ids=lang, tie_audio_head=False)
+    model = SimpleNamespace(config=cfg, trunk=trunk,
+                            state_dict=lambda: {k: torch.from_numpy(v) for k, v in w.items()})
+    n = f["text_ids"].size + 1 + f["prompt_codes"].shape[0] + gen["max_new_frames"] + 2
+    e = GraphFrameEngine(model, device=hip_device, max_cache_len=n, cfg_scale=gen["cfg_scale"], batch=2)
+    e.set_temperature(gen["temperature"])
+    e.set_sampling(sampled=True, top_k=gen["top_k"], top_p=gen["top_p"])
+    e.set_debug(True)
+    e.prefill(f["text_ids"], f["uncond_ids"], f["prompt_codes"])
+    e.capture()
+    got = []
+    for fi in range(f["codes"].shape[0]):
+        _, lg = e.step_frame(mask_eos_q0=fi < gen["min_new_frames"], uniforms=np.zeros(s.n_codebooks),
+                             forced_codes=f["codes"][fi], return_logits=True)
+        got.extend(lg[0])
+    e.close()
+    rel = _rowwise_rel(np.stack(got)[: f["sample_logits"].shape[0]], f["sample_logits"])
+    print(f"untied head via model=: max row-relative logit error {rel:.3e}")
+    assert rel < LOGIT_TOL

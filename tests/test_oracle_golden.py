@@ -10,7 +10,7 @@ from oracle.generate import Record, generate
 from oracle.model import OracleModel, synthetic_weights
 from oracle.sampler import apply_masks, filtered_probs
 
-TINY_FIXTURES = ["tiny_greedy", "tiny_sampled", "tiny_nocfg_topp"]
+TINY_FIXTURES = ["tiny_greedy", "tiny_sampled", "tiny_nocfg_topp", "tiny_untied"]
 
 
 def _model(f, s, dtype):
@@ -81,11 +81,7 @@ def test_greedy_free_running_codes_match_reference():
     assert info["stop_reason"] == ("eos" if int(f["stop_eos"]) else "max_frames")
 
 
-@pytest.mark.parametrize("name", ["tiny_sampled", "tiny_nocfg_topp"])
-def test_filtered_distribution_matches_reference(name):
-    """Top-k / top-p filter = what _sample_logits hands to torch.multinomial."""
-    f, s, gen = load_golden(name)
-    rec, _, _ = _run(f, s, gen, np.float32)
+def _check_filtered(rec, f, s, gen):
     ref = f["probs"]
     got = _masked_calls(rec, s, gen, ref.shape[0])
     i = 0
@@ -102,6 +98,32 @@ def test_filtered_distribution_matches_reference(name):
             assert np.abs(pr - ref[i]).max() < 1e-6
             i += 1
     assert i == ref.shape[0]
+
+
+@pytest.mark.parametrize("name", ["tiny_sampled", "tiny_nocfg_topp", "tiny_untied"])
+def test_filtered_distribution_matches_reference(name):
+    """Top-k / top-p filter = what _sample_logits hands to torch.multinomial."""
+    f, s, gen = load_golden(name)
+    rec, _, _ = _run(f, s, gen, np.float32)
+    _check_filtered(rec, f, s, gen)
+
+
+def test_untied_fixture_uses_out_proj():
+    """The untied fixture's logits come from depth_head.out_proj: the tied
+    head on the same weights misses them by far (model.py:171-174)."""
+    from dataclasses import replace
+
+    f, s, gen = load_golden("tiny_untied")
+    assert not s.tie_audio_head
+    m = _model(f, replace(s, tie_audio_head=True), np.float64)
+    g = {k: v for k, v in gen.items() if k != "seed"}
+    rec = Record()
+    generate(m, input_ids=f["text_ids"], prompt_codes=f["prompt_codes"], uncond_input_ids=f["uncond_ids"],
+             forced_codes=_forced(f, s), record=rec, **g)
+    ref = f["sample_logits"]
+    got = _masked_calls(rec, s, gen, ref.shape[0])
+    fin = np.isfinite(ref)
+    assert np.abs(got[fin] - ref[fin]).max() / np.abs(ref[fin]).max() > 1e-2
 
 
 def test_batched_rows_equal_native_rows_to_rounding():
@@ -124,6 +146,26 @@ def test_q06b_fixture_prefix_and_first_frames():
     rel = np.abs(got[fin] - ref[fin]).max() / np.abs(ref[fin]).max()
     assert rel < 1e-4, rel
     np.testing.assert_array_equal(codes, f["codes"])
+
+
+def test_q06b_sampled_fixture_full_prefix():
+    """Qwen3-0.6B shape with the full-utterance prefix (96 text ids + BOS frame
+    + 144 prompt frames; uncond = text BOS + BOS frame + prompt), CFG 1.5,
+    T 0.9, top-k 50, top-p 0.95: teacher-forced logits, depth-input hidden
+    states and the V = 2051 distributions handed to torch.multinomial."""
+    f, s, gen = load_golden("q06b_sampled")
+    assert f["text_ids"].size == 96 and f["prompt_codes"].shape == (144, 16) and s.audio_vocab == 2051
+    rec, codes, _ = _run(f, s, gen, np.float32, batched=True)
+    ref = f["sample_logits"]
+    got = _masked_calls(rec, s, gen, ref.shape[0])
+    fin = np.isfinite(ref)
+    assert (np.isfinite(got) == fin).all()
+    rel = np.abs(got[fin] - ref[fin]).max() / np.abs(ref[fin]).max()
+    assert rel < 1e-4, rel
+    h = np.stack(rec.hidden)[: f["hidden"].shape[0]]
+    assert np.abs(h - f["hidden"][: h.shape[0]]).max() / np.abs(f["hidden"]).max() < 1e-4
+    np.testing.assert_array_equal(codes, f["codes"])
+    _check_filtered(rec, f, s, gen)
 
 
 def test_planted_mistakes_are_caught():

@@ -100,6 +100,18 @@ int sk_prefill_row(sk_engine* e, int32_t row, const int64_t* text_ids, int32_t n
 /* Run every staged row through the trunk; leaves per-row hidden and KV length.
  * Every row must be staged; the frame counter starts over. */
 int sk_prefill_run(sk_engine* e);
+/* sk_prefill_run that allocates no device memory.  No counterpart in the
+ * reference: for callers that cannot allocate (code under HIP graph capture,
+ * serving loops that must not stall on hipMalloc).  The prefill's activation
+ * buffers come from a scratch array of SK_NOALLOC_SCRATCH_BYTES in the
+ * library's device code (one per GPU, held until the process ends) instead
+ * of the engine's lazily grown buffers; a packed prefix that needs more
+ * (about 600 tokens at the Qwen3-0.6B shape, 450 at 1.7B) is rejected with
+ * SK_EINVAL -- sk_prefill_run takes any size.  Every call on one GPU shares
+ * that scratch: calls that overlap on one GPU (two engines on two streams)
+ * race.  Results are those of sk_prefill_run, bit for bit. */
+#define SK_NOALLOC_SCRATCH_BYTES (32u << 20)
+int sk_prefill_run_noalloc(sk_engine* e);
 /* Continuous batching (no counterpart in the reference, which decodes one
  * utterance's CFG pair, fast_generate.py:232-328): between frames, run only
  * the rows staged since the last prefill (at least one) through the trunk.

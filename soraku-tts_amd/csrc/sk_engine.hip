@@ -19,6 +19,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -42,6 +43,62 @@ struct LayerW {
 template <typename T>
 hipError_t dalloc(T** p, size_t n) {
   return hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T) + 256);
+}
+
+// Activation buffers of the batched prefill, M = packed prefix tokens.
+struct PrefillBufs {
+  float *X = nullptr, *Xn = nullptr, *QKV = nullptr, *Q = nullptr, *ATT = nullptr, *ACT = nullptr;
+  int *tok_row = nullptr, *tok_pos = nullptr;
+};
+
+// Scratch of sk_prefill_run_noalloc: the prefill's activation buffers for up
+// to SK_NOALLOC_SCRATCH_BYTES, in device memory the code object brings with
+// it.  Host code never uses the symbol itself, only the address
+// hipGetSymbolAddress returns for each device (scratch_ptr below).
+static __device__ __align__(256) float scratch[SK_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Looks up this device's copy of `scratch` once (the device must be current).
+hipError_t scratch_ptr(int device, void** out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return err;
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return hipSuccess;
+}
+
+// Bytes of PrefillBufs for M tokens, each buffer 256-byte aligned.
+size_t prefill_bytes(const sk_config& c, int nqkv, size_t M) {
+  auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const size_t hq = (size_t)c.n_q_heads * c.head_dim;
+  return up(M * c.d_model * 4) * 2 + up(M * nqkv * 4) + up(M * hq * 4) * 2 + up(M * c.trunk_inter * 4) +
+         up(M * 4) * 2;
+}
+
+// Carves PrefillBufs for M tokens out of `base` (prefill_bytes(M) bytes).
+PrefillBufs carve_prefill(const sk_config& c, int nqkv, size_t M, void* base) {
+  auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const size_t hq = (size_t)c.n_q_heads * c.head_dim;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) { char* q = p; p += up(bytes); return q; };
+  PrefillBufs b;
+  b.X = reinterpret_cast<float*>(take(M * c.d_model * 4));
+  b.Xn = reinterpret_cast<float*>(take(M * c.d_model * 4));
+  b.QKV = reinterpret_cast<float*>(take(M * nqkv * 4));
+  b.Q = reinterpret_cast<float*>(take(M * hq * 4));
+  b.ATT = reinterpret_cast<float*>(take(M * hq * 4));
+  b.ACT = reinterpret_cast<float*>(take(M * c.trunk_inter * 4));
+  b.tok_row = reinterpret_cast<int*>(take(M * 4));
+  b.tok_pos = reinterpret_cast<int*>(take(M * 4));
+  return b;
 }
 
 }  // namespace
@@ -97,10 +154,11 @@ struct sk_engine {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
 
-  // batched prefill scratch, sized for the largest packed prefix so far
+  // batched prefill activations, sized for the largest packed prefix so far
   int pf_cap = 0;
-  float *pX = nullptr, *pXn = nullptr, *pQKV = nullptr, *pQ = nullptr, *pATT = nullptr, *pACT = nullptr;
-  int *p_tok_row = nullptr, *p_tok_pos = nullptr, *p_row_start = nullptr;
+  void* pf_mem = nullptr;
+  PrefillBufs pf;
+  int* p_row_start = nullptr;
   float2* p_rope = nullptr;   // [max_ctx + 1][hd/2] (cos, sin) by position, filled at creation
 };
 
@@ -482,37 +540,27 @@ GemmArgs gemm_args(const float* A, int lda, const void* B, int M, int N, int K, 
 
 hipError_t ensure_prefill_bufs(sk_engine* e, int M) {
   if (M <= e->pf_cap) return hipSuccess;
-  void* old[] = {e->pX, e->pXn, e->pQKV, e->pQ, e->pATT, e->pACT, e->p_tok_row, e->p_tok_pos};
-  for (void* p : old)
-    if (p) hipFree(p);
-  e->pX = e->pXn = e->pQKV = e->pQ = e->pATT = e->pACT = nullptr;
-  e->p_tok_row = e->p_tok_pos = nullptr;
+  if (e->pf_mem) hipFree(e->pf_mem);
+  e->pf_mem = nullptr;
+  e->pf = PrefillBufs{};
   e->pf_cap = 0;
-  const sk_config& c = e->c;
-  const size_t m = (size_t)M, hq = (size_t)c.n_q_heads * c.head_dim;
-  hipError_t err = hipSuccess;
-  if (err == hipSuccess) err = dalloc(&e->pX, m * c.d_model);
-  if (err == hipSuccess) err = dalloc(&e->pXn, m * c.d_model);
-  if (err == hipSuccess) err = dalloc(&e->pQKV, m * e->nqkv);
-  if (err == hipSuccess) err = dalloc(&e->pQ, m * hq);
-  if (err == hipSuccess) err = dalloc(&e->pATT, m * hq);
-  if (err == hipSuccess) err = dalloc(&e->pACT, m * c.trunk_inter);
-  if (err == hipSuccess) err = dalloc(&e->p_tok_row, m);
-  if (err == hipSuccess) err = dalloc(&e->p_tok_pos, m);
-  if (err == hipSuccess) e->pf_cap = M;
-  return err;
+  const hipError_t err = hipMalloc(&e->pf_mem, prefill_bytes(e->c, e->nqkv, M));
+  if (err != hipSuccess) return err;
+  e->pf = carve_prefill(e->c, e->nqkv, M, e->pf_mem);
+  e->pf_cap = M;
+  return hipSuccess;
 }
 
 // All staged prefix tokens through the trunk at once (M = total tokens).
-hipError_t enqueue_batched_prefill(sk_engine* e, int M, int max_len) {
+hipError_t enqueue_batched_prefill(sk_engine* e, int M, int max_len, const PrefillBufs& b) {
   const sk_config& c = e->c;
   const int d = c.d_model, hd = c.head_dim, wt = c.weight_dtype;
   const int hq = c.n_q_heads * hd, I = c.trunk_inter;
   const bool bf = c.kv_dtype == SK_BF16;
   hipStream_t st = e->stream;
   hipError_t err;
-  hipLaunchKernelGGL(pf_gather_kernel, dim3(M), dim3(NT), 0, st, e->embeds, c.max_ctx, e->p_tok_row,
-                     e->p_tok_pos, d, e->pX);
+  hipLaunchKernelGGL(pf_gather_kernel, dim3(M), dim3(NT), 0, st, e->embeds, c.max_ctx, b.tok_row,
+                     b.tok_pos, d, b.X);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   const size_t asmem = pf_attn_smem_floats(hd) * sizeof(float);
   const int G = c.n_q_heads / c.n_kv_heads, QB = PF_NQ / G;
@@ -520,44 +568,44 @@ hipError_t enqueue_batched_prefill(sk_engine* e, int M, int max_len) {
     const LayerW& w = e->L[l];
     char* kc = e->kc + (size_t)l * kv_layer_bytes(e);
     char* vc = e->vc + (size_t)l * kv_layer_bytes(e);
-    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(NT), 0, st, e->pX, (const float*)nullptr, w.in_norm,
-                       c.trunk_eps, d, e->pXn, (const int*)nullptr);
-    GemmArgs g = gemm_args(e->pXn, d, w.q, M, e->nqkv, d, e->pQKV, e->nqkv);
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(NT), 0, st, b.X, (const float*)nullptr, w.in_norm,
+                       c.trunk_eps, d, b.Xn, (const int*)nullptr);
+    GemmArgs g = gemm_args(b.Xn, d, w.q, M, e->nqkv, d, b.QKV, e->nqkv);
     g.B[1] = w.k; g.B[2] = w.v;
     g.seg_rows[0] = hq; g.seg_rows[1] = c.n_kv_heads * hd; g.seg_rows[2] = c.n_kv_heads * hd;
     if ((err = launch_gemm<GEPI_STORE>(wt, g, st)) != hipSuccess) return err;
     if (bf)
-      hipLaunchKernelGGL(pf_qkv_kernel<uint16_t>, dim3(M), dim3(NT), 0, st, e->pQKV, e->nqkv, e->p_tok_row,
-                         e->p_tok_pos, w.q_norm, w.k_norm, c.trunk_eps, e->p_rope, c.n_q_heads, c.n_kv_heads, hd,
-                         c.max_ctx, e->pQ, reinterpret_cast<uint16_t*>(kc), reinterpret_cast<uint16_t*>(vc));
+      hipLaunchKernelGGL(pf_qkv_kernel<uint16_t>, dim3(M), dim3(NT), 0, st, b.QKV, e->nqkv, b.tok_row,
+                         b.tok_pos, w.q_norm, w.k_norm, c.trunk_eps, e->p_rope, c.n_q_heads, c.n_kv_heads, hd,
+                         c.max_ctx, b.Q, reinterpret_cast<uint16_t*>(kc), reinterpret_cast<uint16_t*>(vc));
     else
-      hipLaunchKernelGGL(pf_qkv_kernel<float>, dim3(M), dim3(NT), 0, st, e->pQKV, e->nqkv, e->p_tok_row,
-                         e->p_tok_pos, w.q_norm, w.k_norm, c.trunk_eps, e->p_rope, c.n_q_heads, c.n_kv_heads, hd,
-                         c.max_ctx, e->pQ, reinterpret_cast<float*>(kc), reinterpret_cast<float*>(vc));
+      hipLaunchKernelGGL(pf_qkv_kernel<float>, dim3(M), dim3(NT), 0, st, b.QKV, e->nqkv, b.tok_row,
+                         b.tok_pos, w.q_norm, w.k_norm, c.trunk_eps, e->p_rope, c.n_q_heads, c.n_kv_heads, hd,
+                         c.max_ctx, b.Q, reinterpret_cast<float*>(kc), reinterpret_cast<float*>(vc));
     const dim3 agrid((max_len + QB - 1) / QB, c.n_kv_heads, e->rows);
     const float scale = 1.0f / sqrtf((float)hd);
     if (bf)
-      hipLaunchKernelGGL(pf_attention_kernel<uint16_t>, agrid, dim3(NT), asmem, st, e->pQ,
+      hipLaunchKernelGGL(pf_attention_kernel<uint16_t>, agrid, dim3(NT), asmem, st, b.Q,
                          reinterpret_cast<const uint16_t*>(kc), reinterpret_cast<const uint16_t*>(vc),
-                         e->p_row_start, e->plen, c.n_q_heads, c.n_kv_heads, hd, c.max_ctx, scale, e->pATT, hq);
+                         e->p_row_start, e->plen, c.n_q_heads, c.n_kv_heads, hd, c.max_ctx, scale, b.ATT, hq);
     else
-      hipLaunchKernelGGL(pf_attention_kernel<float>, agrid, dim3(NT), asmem, st, e->pQ,
+      hipLaunchKernelGGL(pf_attention_kernel<float>, agrid, dim3(NT), asmem, st, b.Q,
                          reinterpret_cast<const float*>(kc), reinterpret_cast<const float*>(vc), e->p_row_start,
-                         e->plen, c.n_q_heads, c.n_kv_heads, hd, c.max_ctx, scale, e->pATT, hq);
+                         e->plen, c.n_q_heads, c.n_kv_heads, hd, c.max_ctx, scale, b.ATT, hq);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    g = gemm_args(e->pATT, hq, w.o, M, d, hq, e->pX, d);
-    g.res = e->pX; g.ldr = d;
+    g = gemm_args(b.ATT, hq, w.o, M, d, hq, b.X, d);
+    g.res = b.X; g.ldr = d;
     if ((err = launch_gemm<GEPI_RESID>(wt, g, st)) != hipSuccess) return err;
-    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(NT), 0, st, e->pX, (const float*)nullptr, w.post_norm,
-                       c.trunk_eps, d, e->pXn, (const int*)nullptr);
-    g = gemm_args(e->pXn, d, w.gate, M, I, d, e->pACT, I);
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(NT), 0, st, b.X, (const float*)nullptr, w.post_norm,
+                       c.trunk_eps, d, b.Xn, (const int*)nullptr);
+    g = gemm_args(b.Xn, d, w.gate, M, I, d, b.ACT, I);
     g.B2 = w.up;
     if ((err = launch_gemm<GEPI_SWIGLU>(wt, g, st)) != hipSuccess) return err;
-    g = gemm_args(e->pACT, I, w.down, M, d, I, e->pX, d);
-    g.res = e->pX; g.ldr = d;
+    g = gemm_args(b.ACT, I, w.down, M, d, I, b.X, d);
+    g.res = b.X; g.ldr = d;
     if ((err = launch_gemm<GEPI_RESID>(wt, g, st)) != hipSuccess) return err;
   }
-  hipLaunchKernelGGL(pf_finish_kernel, dim3(e->rows), dim3(NT), 0, st, e->pX, e->p_row_start, e->plen,
+  hipLaunchKernelGGL(pf_finish_kernel, dim3(e->rows), dim3(NT), 0, st, b.X, e->p_row_start, e->plen,
                      e->final_norm, c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->inv_freq, hd / 2,
                      e->rope, e->d_norm_in, c.depth_eps, e->abuf, e->xs_abuf);
   return hipGetLastError();
@@ -660,6 +708,11 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     }                                                                                   \
   } while (0)
   if (hipGetDevice(&e->device) != hipSuccess) { fail(SK_EHIP, "no HIP device"); return bail(SK_EHIP); }
+  {
+    void* sp = nullptr;   // this device's copy of the no-alloc prefill scratch, looked up once
+    const hipError_t se = scratch_ptr(e->device, &sp);
+    if (se != hipSuccess) { fail(SK_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(se)); return bail(SK_EHIP); }
+  }
   if (hip_stream) {
     const hipError_t se = hipStreamSynchronize(static_cast<hipStream_t>(hip_stream));
     if (se != hipSuccess) { fail(SK_EHIP, "caller stream: %s", hipGetErrorString(se)); return bail(SK_EHIP); }
@@ -758,7 +811,7 @@ int sk_destroy(sk_engine* e) {
   void* bufs[] = {e->sk_partial, e->sk_arrive, e->xs_x, e->xs_attn, e->xs_act, e->xs_abuf, e->xs_y, e->ss_x, e->ss_y, e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
                   e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->flag_ring, e->u_ring,
-                  e->pX, e->pXn, e->pQKV, e->pQ, e->pATT, e->pACT, e->p_tok_row, e->p_tok_pos,
+                  e->pf_mem,
                   e->p_row_start, e->p_rope,
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
   for (void* p : bufs)
@@ -874,7 +927,7 @@ int sk_prefill_row(sk_engine* e, int32_t row, const int64_t* text_ids, int32_t n
 // rows are touched -- the other rows' caches, lengths and hidden states and
 // the frame counter stay as they are (unstaged rows get length 0 here, which
 // every prefill kernel skips).
-static int prefill_staged(sk_engine* e, bool all) {
+static int prefill_staged(sk_engine* e, bool all, bool noalloc) {
   const int R = e->rows;
   int n_staged = 0;
   for (int r = 0; r < R; ++r) {
@@ -894,18 +947,30 @@ static int prefill_staged(sk_engine* e, bool all) {
     M += row_len[r];
     max_len = row_len[r] > max_len ? row_len[r] : max_len;
   }
-  const hipError_t ae = ensure_prefill_bufs(e, M);
-  SK_CHECK(ae == hipSuccess, SK_EHIP, "prefill buffers for %d tokens: %s", M, hipGetErrorString(ae));
+  PrefillBufs bufs;
+  if (noalloc) {
+    const size_t need = prefill_bytes(e->c, e->nqkv, M);
+    SK_CHECK(need <= SK_NOALLOC_SCRATCH_BYTES, SK_EINVAL,
+             "prefill of %d packed tokens needs %zu bytes of scratch, more than the %zu of "
+             "sk_prefill_run_noalloc (use sk_prefill_run)", M, need, (size_t)SK_NOALLOC_SCRATCH_BYTES);
+    void* base = nullptr;
+    SK_HIP(scratch_ptr(e->device, &base));
+    bufs = carve_prefill(e->c, e->nqkv, M, base);
+  } else {
+    const hipError_t ae = ensure_prefill_bufs(e, M);
+    SK_CHECK(ae == hipSuccess, SK_EHIP, "prefill buffers for %d tokens: %s", M, hipGetErrorString(ae));
+    bufs = e->pf;
+  }
   SK_HIP(hipMemcpyAsync(e->plen, row_len.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
   SK_HIP(hipMemcpyAsync(e->p_row_start, row_start.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  SK_HIP(hipMemcpyAsync(e->p_tok_row, tok_row.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  SK_HIP(hipMemcpyAsync(e->p_tok_pos, tok_pos.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(bufs.tok_row, tok_row.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
+  SK_HIP(hipMemcpyAsync(bufs.tok_pos, tok_pos.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
   if (all) {
     SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
     SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
     SK_HIP(hipMemsetAsync(e->prefix2, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
   }
-  SK_HIP(enqueue_batched_prefill(e, M, max_len));
+  SK_HIP(enqueue_batched_prefill(e, M, max_len, bufs));
   SK_HIP(hipStreamSynchronize(e->stream));
   for (int r = 0; r < R; ++r)
     if (e->staged[r]) { e->kv_host[r] = e->len_host[r]; e->active_host[r] = 1; e->staged[r] = 0; }
@@ -916,13 +981,18 @@ static int prefill_staged(sk_engine* e, bool all) {
 
 int sk_prefill_run(sk_engine* e) {
   SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
-  return prefill_staged(e, true);
+  return prefill_staged(e, true, false);
+}
+
+int sk_prefill_run_noalloc(sk_engine* e) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  return prefill_staged(e, true, true);
 }
 
 int sk_prefill_refill(sk_engine* e) {
   SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
   SK_CHECK(e->ran_full, SK_ESTATE, "refill before the first sk_prefill_run");
-  return prefill_staged(e, false);
+  return prefill_staged(e, false, false);
 }
 
 int sk_retire_row(sk_engine* e, int32_t row) {

@@ -60,6 +60,7 @@ PROTOTYPES = {
     "sk_bind_weight": (_I, [_P, C.c_char_p, _P, _I, _PI64, _I]),
     "sk_prefill_row": (_I, [_P, _I, _PI64, _I, _PI64, _I]),
     "sk_prefill_run": (_I, [_P]),
+    "sk_prefill_run_noalloc": (_I, [_P]),
     "sk_prefill_refill": (_I, [_P]),
     "sk_retire_row": (_I, [_P, _I]),
     "sk_reset_frames": (_I, [_P]),

@@ -19,12 +19,24 @@ GPU (utterances shard across GPUs with no per-frame exchange).
 text ids + BOS frame + 144 prompt frames (240 positions), 480 decoded frames,
 same sampling.
 
+``--greedy-192`` runs the CPU-sized workload instead: Qwen3-0.6B shape, FP32,
+cond prefix = 192 random text ids + BOS frame (193 positions), uncond = [bos] +
+BOS frame, 32 greedy frames (4 warm-up + 28 timed by default), seed 0.
+
+The CPU baseline (``cpu_baseline``) is the oracle in NumPy FP32 on the host
+cores, on the same weights and prefixes: prefill untimed, then 4 warm-up and
+16 timed frames, each frame timed alone (median and p90).  It runs the
+reference's native order, cond and uncond as two B=1 branches
+(soraku_inference/model.py:573-578,611-612), and beside it the same frames
+with both rows batched (M = 2), so the gain from batching alone is visible.
+
 ``--kernels`` times the isolated fused kernels at decode shape M = 2 instead
 (RMSNorm over 1024, SwiGLU gate/up GEMV 1024 -> 2 x 3072, down GEMV
-3072 -> 1024 + residual, the 16 classifier heads 1024 -> 2051 + bias; FP32 and
-BF16 weights): each is captured as a chain of launches over distinct weight
-copies totalling more than the 256 MB last-level cache (so every launch reads
-HBM), replayed, and reported per launch with its bytes and HBM fraction.
+3072 -> 1024 + residual, one classifier head 1024 -> 2051 + bias, and the
+16-head classifier 1024 -> 16 x 2051 + bias as one launch; FP32 and BF16
+weights): each is captured as a chain of launches over distinct weight copies
+totalling more than the 256 MB last-level cache (so every launch reads HBM),
+replayed, and reported per launch with its bytes and HBM fraction.
 
 ``--utterances N`` (N > 1) runs the throughput batch instead: N synthetic
 utterances with CFG decoded together (decode batch 2N) at Qwen3-0.6B shape
@@ -96,60 +108,120 @@ def algorithmic_bytes(shape, kv_lens, w_bytes=4, kv_bytes=4):
 
 
 def cpu_info():
-    model = platform.processor() or ""
+    """(lscpu model name, logical CPUs, CPUs this process may run on)."""
+    model = ""
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
                 model = line.split(":", 1)[1].strip()
                 break
-    except OSError:
+    except (OSError, subprocess.SubprocessError):
         pass
-    return model
+    if not model:
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            model = platform.processor() or ""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, usable
 
 
-def cpu_baseline(shape, weights, text, prompt, uncond, u, n_frames=6, n_warm=1):
-    """The oracle (NumPy FP32, the reference's native two-branch order) on the
-    host cores, over a bounded sample of the same workload."""
+def cpu_baseline(shape, weights, items, u, *, temperature, n_frames=16, n_warm=4, unit="frames/s"):
+    """The oracle (NumPy FP32) on the host cores over a bounded sample of the
+    workload: for each (text, prompt, uncond) in ``items`` (one utterance, or a
+    few of a batch), prefill untimed, then ``n_warm`` + ``n_frames`` frames,
+    each timed alone, first in the reference's order (cond and uncond as two
+    B=1 branches, model.py:573-578,611-612), then again from the same prefilled
+    state with both rows batched (M = 2)."""
+    import copy
+
     from threadpoolctl import threadpool_info, threadpool_limits
 
     from oracle.generate import generate, start_states
     from oracle.model import OracleModel, Shape
 
-    cores = os.cpu_count() or 1
-    with threadpool_limits(limits=cores):
+    model, nproc, usable = cpu_info()
+    with threadpool_limits(limits=usable):
         threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
         os_shape = Shape(**{k: getattr(shape, k) for k in Shape.__dataclass_fields__})
         m = OracleModel(os_shape, weights, np.float32)
-        max_ctx = text.size + 1 + prompt.shape[0] + n_frames + n_warm + 2
-        states = start_states(m, text, prompt, uncond, CFG, max_ctx)
-        kw = dict(min_new_frames=10**6, temperature=TEMP, top_k=TOP_K, top_p=TOP_P, cfg_scale=CFG)
-        generate(m, max_new_frames=n_warm, uniforms=u, states=states, input_ids=text, **kw)
-        t0 = time.perf_counter()
-        generate(m, max_new_frames=n_frames, uniforms=u[n_warm:], states=states, input_ids=text, **kw)
-        dt = time.perf_counter() - t0
-    return {"value": n_frames / dt, "unit": "frames/s", "cores": int(threads), "kind": "port",
-            "sample": (f"oracle/ (NumPy FP32, cond and uncond as separate B=1 branches), "
-                       f"{n_frames} frames timed after {n_warm} warm-up at prefixes "
-                       f"{text.size + 1 + prompt.shape[0]}/{uncond.size + 1 + prompt.shape[0]}; "
-                       f"{dt / n_frames * 1e3:.1f} ms/frame; host {cpu_info()}")}
+        kw = dict(min_new_frames=10**6, temperature=temperature, top_k=TOP_K, top_p=TOP_P, cfg_scale=CFG)
+        times = {False: [], True: []}
+        for i, (text, prompt, uncond) in enumerate(items):
+            max_ctx = text.size + 1 + prompt.shape[0] + n_frames + n_warm + 2
+            st0 = start_states(m, text, prompt, uncond, CFG, max_ctx)
+            for batched in (False, True):
+                st = copy.deepcopy(st0)
+                for f in range(n_warm + n_frames):
+                    t0 = time.perf_counter()
+                    generate(m, max_new_frames=1, uniforms=u[i][f:f + 1], states=st, input_ids=text,
+                             batched=batched, **kw)
+                    if f >= n_warm:
+                        times[batched].append(time.perf_counter() - t0)
+    two, bat = np.array(times[False]) * 1e3, np.array(times[True]) * 1e3
+    text, prompt, uncond = items[0]
+    return {"value": 1e3 / float(np.median(two)), "unit": unit, "cores": int(threads), "kind": "port",
+            "ms_per_frame_median": float(np.median(two)), "ms_per_frame_p90": float(np.percentile(two, 90)),
+            "frames_timed": int(two.size), "warmup_frames": n_warm * len(items),
+            "nproc": nproc, "cpus_usable": usable, "lscpu_model": model, "threads": int(threads),
+            "batched_m2": {"value": 1e3 / float(np.median(bat)), "unit": unit,
+                           "ms_per_frame_median": float(np.median(bat)),
+                           "ms_per_frame_p90": float(np.percentile(bat, 90))},
+            "sample": (f"oracle/ (NumPy FP32) on {threads} BLAS threads: {len(items)} utterance(s), prefill "
+                       f"untimed, {n_warm} warm-up + {n_frames} timed frames each, every frame timed alone; "
+                       f"value = 1 / median frame time with cond and uncond as separate B=1 branches "
+                       f"(the reference's order); batched_m2 = both rows in one pass; prefixes "
+                       f"{text.size + 1 + prompt.shape[0]}/{uncond.size + 1 + prompt.shape[0]}"
+                       + ("" if len(items) == 1 else " (first utterance)"))}
 
 
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "hbm_traffic_decode_frame_q06b_f32.md")
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+TRAFFIC_PROFILES = {
+    "q06b_f32": "hbm_traffic_decode_frame_q06b_f32.md",
+    "q17b_bf16": "hbm_traffic_decode_frame_q17b_bf16.md",
+    "16utt_q06b_bf16": "hbm_traffic_decode_step_16utt_q06b_bf16.md",
+}
 
 
-def measured_traffic():
-    """HBM bytes per frame from the committed counter summary (FETCH_SIZE +
-    WRITE_SIZE passes, copy-calibrated); None when the summary is absent."""
+def measured_traffic(key):
+    """HBM bytes per graph launch from the committed counter summary
+    (FETCH_SIZE + WRITE_SIZE passes, copy-calibrated) and the rows' KV
+    lengths it was measured at; (None, None) when the summary is absent."""
     try:
-        text = open(TRAFFIC_PROFILE).read()
-    except OSError:
-        return None
+        text = open(os.path.join(PROFILES, TRAFFIC_PROFILES[key])).read()
+    except (OSError, KeyError):
+        return None, None
     m = re.search(r"```json\s*(\{.*?\})\s*```", text, re.S)
     if not m:
-        return None
+        return None, None
     d = json.loads(m.group(1))
-    return float(d["read_bytes_per_frame"]) + float(d["write_bytes_per_frame"])
+    return float(d["read_bytes_per_frame"]) + float(d["write_bytes_per_frame"]), d["kv_lens"]
+
+
+def roofline(shape, us, kv_mid, w_bytes, traffic_key, unit_of_work):
+    """Roofline object: algorithmic bytes at the timed frames' average KV
+    lengths over the measured frame time; measured traffic with the KV state
+    it was taken at and the algorithmic bytes of that same state."""
+    alg = algorithmic_bytes(shape, kv_mid, w_bytes=w_bytes)
+    achieved = alg / (us * 1e-6) / 1e9
+    traffic, tkv = measured_traffic(traffic_key)
+    out = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "unit_of_work": unit_of_work,
+           "algorithmic_bytes_per_launch": alg, "algorithmic_kv_lens_avg": [float(k) for k in kv_mid]}
+    if traffic is not None:
+        alg_t = algorithmic_bytes(shape, tkv, w_bytes=w_bytes)
+        out.update({"traffic_source": f"profiles/{TRAFFIC_PROFILES[traffic_key]} (rocprofv3 FETCH_SIZE + "
+                                      "WRITE_SIZE, copy-calibrated, bytes per launch)",
+                    "traffic_kv_lens": tkv, "algorithmic_bytes_at_traffic_kv": alg_t,
+                    "traffic_over_algorithmic": traffic / alg_t})
+    return out
 
 
 def copy_probe(mib):
@@ -215,8 +287,6 @@ def many_utterances(args):
     assert codes.min() >= 0 and codes.max() < shape.codebook_size, "decoded a special id"
     e.close()
     kv_mid = [k + args.warmup + (args.steps - 1) / 2 for k in kv0]
-    alg = algorithmic_bytes(shape, kv_mid, w_bytes=2)
-    achieved = alg / (us * 1e-6) / 1e9
     out = {
         "metric": f"codec frames/sec summed over {n} utterances (CFG, decode batch {2 * n}) + % HBM roofline, "
                   "1 MI355X",
@@ -228,12 +298,20 @@ def many_utterances(args):
                                 "top-k 50, top-p 0.95, seeded uniforms, one hipGraph per frame"),
                    "global_batch": 2 * n, "seq_len": 512, "parallelism": "none",
                    "prefill_ms": t_prefill * 1e3},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "unit_of_work": "one frame of every utterance = one hipGraph launch",
-                     "algorithmic_bytes_per_launch": alg},
-        "cpu_baseline": None,
+        "roofline": roofline(shape, us, kv_mid, 2, f"{n}utt_q06b_bf16",
+                             "one frame of every utterance = one hipGraph launch"),
     }
+    if not args.no_cpu_baseline:
+        # two of the utterances (prefill is the CPU's longest part), BF16-rounded weights as on the GPU
+        from oracle.model import round_bf16
+        from soraku_amd.synthetic import is_matrix
+
+        w32 = {k: (round_bf16(v) if is_matrix(k) else v) for k, v in synthetic_weights(shape, args.seed).items()}
+        cb = cpu_baseline(shape, w32, items[:2], [u[:, i * shape.n_codebooks:(i + 1) * shape.n_codebooks]
+                                                  for i in range(2)],
+                          temperature=TEMP, unit="utterance-frames/s")
+        cb["speedup"] = out["value"] / cb["value"]
+        out["cpu_baseline"] = cb
     print(json.dumps(out))
 
 
@@ -347,68 +425,45 @@ def isolated_kernels(args):
         calls = [lambda i=i, q=q: k(x, tables[i][q], bias[q]) for i in range(n) for q in range(Q)]
         out.append(timed("classifier GEMV 1024 -> 2051 + bias (one of 16 heads)", wname, calls,
                          V * D * wb + V * 4 + B * D * 4 + B * V * 4))
-        del tables
+        # the 16 heads as one unit: [16 x 2051, 1024] in one launch
+        k16 = ops.classifier_gemv(B, Q * V, D)
+        flat = [t.view(Q * V, D) for t in tables]
+        bias16 = bias.view(Q * V)
+        calls = [lambda i=i: k16(x, flat[i], bias16) for i in range(n)]
+        out.append(timed("16-head classifier GEMV 1024 -> 16 x 2051 + bias (one launch)", wname, calls,
+                         Q * V * D * wb + Q * V * 4 + B * D * 4 + B * Q * V * 4))
+        del tables, flat
     print(json.dumps({"metric": "isolated decode kernels at M=2: us per launch and HBM fraction, 1 MI355X",
                       "n_gpus": 1, "data": "synthetic", "unit": "us/launch",
                       "note": "per launch inside a captured chain (includes the ~1.6 us per-kernel graph floor)",
                       "kernels": out}))
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--model", choices=("q06b", "q17b"), default="q06b",
-                    help="q17b: Qwen3-1.7B shape with BF16 weights, 240-position prefix, 480 frames")
-    ap.add_argument("--kernels", action="store_true",
-                    help="time the isolated fused kernels at M=2 (FP32 and BF16 weights) instead")
-    ap.add_argument("--utterances", type=int, default=1,
-                    help="N > 1: the throughput batch of N utterances x CFG (BF16 weights) instead")
-    ap.add_argument("--requests", type=int, default=0,
-                    help="with --utterances N: decode this many requests through the N slots (refills)")
-    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
-                    help="only run 4 device copies of MIB MiB each (HBM counter calibration) and exit")
-    args = ap.parse_args()
-    if args.copy_probe:
-        copy_probe(args.copy_probe)
-        return
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for {args.gpus}): utterances shard across GPUs "
-              "with no per-frame exchange, so the per-GPU figure is the N=1 line.", file=sys.stderr)
-        sys.exit(2)
-    big = args.model == "q17b"
-    n_text, n_prompt, n_frames = (95, 144, 480) if big else (N_TEXT, N_PROMPT, N_FRAMES)
-    if args.steps + args.warmup > n_frames:
-        sys.exit(f"steps + warmup must be <= {n_frames} (the workload's decoded frames)")
-    if args.kernels:
-        isolated_kernels(args)
-        return
-    if args.utterances > 1 and args.requests > args.utterances:
-        continuous_batch(args)
-        return
-    if args.utterances > 1:
-        many_utterances(args)
-        return
-
+def single_utterance(args, mode):
+    """One utterance with CFG (see the module docstring); one JSON line."""
     import torch
 
     from soraku_amd import GraphFrameEngine
     from soraku_amd.config import QWEN3_06B, QWEN3_17B
     from soraku_amd.synthetic import synthetic_weights
 
+    big = mode == "q17b"
+    greedy = mode == "greedy192"
     shape = QWEN3_17B if big else QWEN3_06B
+    n_text, n_prompt, n_frames = {"q17b": (95, 144, 480), "greedy192": (192, 0, 32)}.get(
+        mode, (N_TEXT, N_PROMPT, N_FRAMES))
+    temp = 0.0 if greedy else TEMP
     t_setup = time.perf_counter()
     weights = synthetic_weights(shape, args.seed)
     text, prompt, uncond, u = workload_inputs(shape, args.seed, n_text, n_prompt, n_frames)
+    if greedy:   # 192 random ids, uncond = [bos]: both followed by the BOS frame
+        text = np.random.default_rng(args.seed).integers(0, shape.text_vocab, n_text)
     dev = torch.device("cuda:0")
     max_ctx = text.size + 1 + prompt.shape[0] + n_frames + 8
     e = GraphFrameEngine(device=dev, max_cache_len=max_ctx, cfg_scale=CFG, batch=2,
                          state_dict=weights, shape=shape, max_frames=n_frames, bf16=big)
-    e.set_temperature(TEMP)
-    e.set_sampling(sampled=True, top_k=TOP_K, top_p=TOP_P)
+    e.set_temperature(temp)
+    e.set_sampling(sampled=not greedy, top_k=TOP_K, top_p=TOP_P)
     t0 = time.perf_counter()
     e.prefill(text, uncond, prompt)
     t_prefill = time.perf_counter() - t0
@@ -416,8 +471,8 @@ def main():
     total = args.warmup + args.steps
     e.queue_frames(u[:total], np.ones(total, np.int32))
     kv0 = [text.size + 1 + prompt.shape[0], uncond.size + 1 + prompt.shape[0]]
-    print(f"# setup {time.perf_counter() - t_setup:.1f}s, prefill {t_prefill * 1e3:.1f} ms", file=sys.stderr,
-          flush=True)
+    print(f"# {mode}: setup {time.perf_counter() - t_setup:.1f}s, prefill {t_prefill * 1e3:.1f} ms",
+          file=sys.stderr, flush=True)
 
     stream = torch.cuda.ExternalStream(e.stream_handle, device=dev)
     e.replay(args.warmup)
@@ -434,17 +489,18 @@ def main():
     total_ms = evs[0].elapsed_time(evs[-1])
     codes = e.read_codes(args.steps)
     assert codes.min() >= 0 and codes.max() < shape.codebook_size, "decoded a special id"
+    e.close()
 
     us = total_ms * 1e3 / args.steps
     kv_mid = [k + args.warmup + (args.steps - 1) / 2 for k in kv0]
-    alg = algorithmic_bytes(shape, kv_mid, w_bytes=2 if big else 4)
-    achieved = alg / (us * 1e-6) / 1e9
-    workload = ("larger backbone, Qwen3-1.7B shape, BF16 weights (FP32 KV and accumulation): 95 text ids + "
-                "144 prompt frames (240 positions), 480 frames, CFG 1.5, T 0.9, top-k 50, top-p 0.95, "
-                "seeded uniforms, one hipGraph per frame") if big else (
-                "full synthetic utterance, Qwen3-0.6B shape FP32: 96 text ids + "
-                "144 prompt frames, CFG 1.5, T 0.9, top-k 50, top-p 0.95, seeded "
-                "uniforms, one hipGraph per frame")
+    workload = {
+        "q17b": ("larger backbone, Qwen3-1.7B shape, BF16 weights (FP32 KV and accumulation): 95 text ids + "
+                 "144 prompt frames (240 positions), 480 frames, CFG 1.5, T 0.9, top-k 50, top-p 0.95, "
+                 "seeded uniforms, one hipGraph per frame"),
+        "greedy192": ("CPU-sized greedy utterance, Qwen3-0.6B shape FP32: 192 random text ids + BOS frame "
+                      "(uncond [bos] + BOS frame), 32 greedy frames, CFG 1.5, seed 0, one hipGraph per frame"),
+    }.get(mode, "full synthetic utterance, Qwen3-0.6B shape FP32: 96 text ids + 144 prompt frames, CFG 1.5, "
+                "T 0.9, top-k 50, top-p 0.95, seeded uniforms, one hipGraph per frame")
     out = {
         "metric": METRIC, "value": 1e6 / us, "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": us / 1e3, "higher_is_better": True, "scaling": "weak",
@@ -454,19 +510,68 @@ def main():
                    "us_per_frame_median": float(np.median(per)),
                    "us_per_frame_p90": float(np.percentile(per, 90)),
                    "prefill_ms": t_prefill * 1e3},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None if big else measured_traffic(),
-                     "traffic_source": None if big else (
-                         "profiles/hbm_traffic_decode_frame_q06b_f32.md (rocprofv3 "
-                         "FETCH_SIZE + WRITE_SIZE, copy-calibrated, bytes per frame)"),
-                     "unit_of_work": "one frame = one hipGraph launch",
-                     "algorithmic_bytes_per_launch": alg},
+        "roofline": roofline(shape, us, kv_mid, 2 if big else 4,
+                             "q17b_bf16" if big else ("q06b_f32" if mode == "full" else None),
+                             "one frame = one hipGraph launch"),
     }
-    e.close()
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(shape, weights, text, prompt, uncond, u, n_frames=3 if big else 6)
-        out["cpu_baseline"]["speedup"] = out["value"] / out["cpu_baseline"]["value"]
+        if big:
+            from oracle.model import round_bf16
+            from soraku_amd.synthetic import is_matrix
+
+            weights = {k: (round_bf16(v) if is_matrix(k) else v) for k, v in weights.items()}
+        cb = cpu_baseline(shape, weights, [(text, prompt, uncond)], [u], temperature=temp,
+                          n_frames=16, n_warm=4)
+        cb["speedup"] = out["value"] / cb["value"]
+        out["cpu_baseline"] = cb
     print(json.dumps(out))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="timed frames (default 200; 28 with --greedy-192)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed frames first (default 8; 4 with --greedy-192)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--model", choices=("q06b", "q17b"), default="q06b",
+                    help="q17b: Qwen3-1.7B shape with BF16 weights, 240-position prefix, 480 frames")
+    ap.add_argument("--greedy-192", action="store_true",
+                    help="the CPU-sized workload: 0.6B FP32, 192 random text ids, 32 greedy frames")
+    ap.add_argument("--kernels", action="store_true",
+                    help="time the isolated fused kernels at M=2 (FP32 and BF16 weights) instead")
+    ap.add_argument("--utterances", type=int, default=1,
+                    help="N > 1: the throughput batch of N utterances x CFG (BF16 weights) instead")
+    ap.add_argument("--requests", type=int, default=0,
+                    help="with --utterances N: decode this many requests through the N slots (refills)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 4 device copies of MIB MiB each (HBM counter calibration) and exit")
+    args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}): utterances shard across GPUs "
+              "with no per-frame exchange, so the per-GPU figure is the N=1 line.", file=sys.stderr)
+        sys.exit(2)
+    mode = "q17b" if args.model == "q17b" else ("greedy192" if args.greedy_192 else "full")
+    if args.steps is None:
+        args.steps = 28 if mode == "greedy192" else 200
+    if args.warmup is None:
+        args.warmup = 4 if mode == "greedy192" else 8
+    n_frames = {"q17b": 480, "greedy192": 32}.get(mode, N_FRAMES)
+    if args.steps + args.warmup > n_frames:
+        sys.exit(f"steps + warmup must be <= {n_frames} (the workload's decoded frames)")
+    if args.kernels:
+        isolated_kernels(args)
+        return
+    if args.utterances > 1 and args.requests > args.utterances:
+        continuous_batch(args)
+        return
+    if args.utterances > 1:
+        many_utterances(args)
+        return
+    single_utterance(args, mode)
 
 
 if __name__ == "__main__":

@@ -299,7 +299,7 @@ SkinnyArgs skinny_args(const void* w, int N, int K, const float* x, int ldx, flo
 // Chunked decode attention: one workgroup per 32-token chunk of each (row,
 // kv head), merged by attention_combine_kernel.  Few rows: the chunks fill
 // the chip.
-hipError_t launch_attn_chunks(sk_engine* e, const AttnArgs& at) {
+hipError_t launch_attn_chunks(sk_engine* e, const AttnArgs& at, bool merge = true) {
   const size_t asmem = attn_smem_floats(e->G, at.hd) * sizeof(float);
   const dim3 grid(e->max_chunks, at.Hkv, e->rows);
   if (e->c.kv_dtype == SK_BF16)
@@ -307,9 +307,34 @@ hipError_t launch_attn_chunks(sk_engine* e, const AttnArgs& at) {
   else
     hipLaunchKernelGGL(attention_kernel<float>, grid, dim3(NT), asmem, e->stream, at);
   hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
+  if (err != hipSuccess || !merge) return err;
   hipLaunchKernelGGL(attention_combine_kernel, dim3(at.Hq, e->rows), dim3(NT), 0, e->stream, at);
   return hipGetLastError();
+}
+
+// Output projection + residual with the attention chunk merge folded in
+// (attn_o_kernel): instantiated for K = Hq * hd = 2048 and 1, 2 or 4 decode
+// rows; attn_o_fits says whether an engine takes it, otherwise the chunk
+// merge kernel + residual GEMV run instead.
+template <int M, typename WL>
+hipError_t launch_attn_o_m(const GemvArgs& g, const AttnArgs& at, hipStream_t st) {
+  constexpr int RW = 1;
+  const int grid = (g.N + (AO_NT / 64) * RW - 1) / ((AO_NT / 64) * RW);
+  hipLaunchKernelGGL((attn_o_kernel<M, 2048, RW, WL>), dim3(grid), dim3(AO_NT), 0, st, g, at);
+  return hipGetLastError();
+}
+bool attn_o_fits(const sk_engine* e) {
+  const int K = e->c.n_q_heads * e->c.head_dim, M = e->rows;
+  const int vpth = M * K / AO_NT;
+  return !e->wide && e->attn_splits == 0 && K == 2048 && (M == 1 || M == 2 || M == 4) && e->c.head_dim % vpth == 0;
+}
+template <typename WL>
+hipError_t launch_attn_o_w(int M, const GemvArgs& g, const AttnArgs& at, hipStream_t st) {
+  switch (M) {
+    case 1: return launch_attn_o_m<1, WL>(g, at, st);
+    case 2: return launch_attn_o_m<2, WL>(g, at, st);
+    default: return launch_attn_o_m<4, WL>(g, at, st);
+  }
 }
 
 // Streaming decode attention (many rows): attn_splits workgroups per (row,
@@ -377,7 +402,8 @@ hipError_t enqueue_trunk(sk_engine* e) {
     at.Hq = c.n_q_heads; at.Hkv = c.n_kv_heads; at.hd = hd; at.max_ctx = c.max_ctx;
     at.scale = 1.0f / sqrtf((float)hd);
     at.xs_out = e->xs_attn;
-    if ((err = e->attn_splits > 0 ? launch_attn_stream(e, at) : launch_attn_chunks(e, at)) != hipSuccess)
+    const bool fused_o = attn_o_fits(e);
+    if ((err = e->attn_splits > 0 ? launch_attn_stream(e, at) : launch_attn_chunks(e, at, !fused_o)) != hipSuccess)
       return err;
 
     if (e->wide) {
@@ -402,7 +428,10 @@ hipError_t enqueue_trunk(sk_engine* e) {
     }
     a = gemv_args(w.o, d, c.n_q_heads * hd, e->attn, c.n_q_heads * hd, e->x, d);
     a.res = e->x; a.ldr = d;
-    if ((err = launch_gemv<PRO_NONE, EPI_RESID>(wt, M, a, e->stream)) != hipSuccess) return err;
+    err = fused_o ? (wt == SK_BF16 ? launch_attn_o_w<WBF16>(M, a, at, e->stream)
+                                   : launch_attn_o_w<WF32>(M, a, at, e->stream))
+                  : launch_gemv<PRO_NONE, EPI_RESID>(wt, M, a, e->stream);
+    if (err != hipSuccess) return err;
 
     a = gemv_args(w.gate, c.trunk_inter, d, e->x, d, e->act, e->inner_max);
     a.w[1] = w.up; a.norm_w = w.post_norm; a.eps = c.trunk_eps;
@@ -463,6 +492,9 @@ hipError_t enqueue_frame(sk_engine* e) {
     s.hidden = e->hidden; s.w_in = e->d_norm_in; s.eps_in = c.depth_eps;
     s.abuf = e->abuf; s.xs_abuf = e->xs_abuf;
   }
+  // One utterance: codebook q-1's sampler runs inside codebook q's gate/up
+  // launch (depth_sample_gemv_kernel); only the last codebook's has its own.
+  const bool fuse = !e->wide && c.n_utts == 1 && depth_fused_fits(d, M, c.depth_inner, V);
   for (int q = 0; q < c.n_codebooks; ++q) {
     if (e->wide) {
       if ((err = enqueue_depth_wide(e, q)) != hipSuccess) return err;
@@ -479,6 +511,12 @@ hipError_t enqueue_frame(sk_engine* e) {
     if (q == 0) {
       a.x2 = e->prefix;
       if ((err = launch_gemv<PRO_ADDNORM, EPI_SWIGLU>(wt, M, a, e->stream)) != hipSuccess) return err;
+    } else if (fuse) {
+      a.x2 = (q % 2 == 1) ? e->prefix : e->prefix2;
+      a.gout = (q % 2 == 1) ? e->prefix2 : e->prefix; a.ldgo = d;
+      err = (wt == SK_BF16) ? launch_depth_fused<WBF16>(s, a, M, q, e->stream)
+                            : launch_depth_fused<WF32>(s, a, M, q, e->stream);
+      if (err != hipSuccess) return err;
     } else {
       a.x2 = (q % 2 == 1) ? e->prefix : e->prefix2;
       a.gout = (q % 2 == 1) ? e->prefix2 : e->prefix; a.ldgo = d;
@@ -497,6 +535,7 @@ hipError_t enqueue_frame(sk_engine* e) {
     a.norm_w = e->d_norm_out; a.eps = c.depth_eps; a.bias = e->d_bias + (size_t)q * V;
     if ((err = launch_gemv<PRO_NORM, EPI_BIAS>(wt, M, a, e->stream)) != hipSuccess) return err;
 
+    if (fuse && q + 1 < c.n_codebooks) continue;   // sampled inside the next gate/up launch
     err = (wt == SK_BF16) ? launch_sample_step<WBF16>(s, q, c.n_utts, e->stream)
                           : launch_sample_step<WF32>(s, q, c.n_utts, e->stream);
     if (err != hipSuccess) return err;
@@ -736,7 +775,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     ALLOC(e->sk_partial, (nmax / 16 + 1) * 4 * SK_PSZ);
     ALLOC(e->sk_arrive, nmax / 16 + 1);
   }
-  ALLOC(e->part, R * c.n_q_heads * e->max_chunks * (c.head_dim + 2));
+  ALLOC(e->part, R * c.n_q_heads * e->max_chunks * part_stride(c.head_dim));
   const bool split_in = e->wide && c.weight_dtype == SK_BF16;
   if (split_in) {
     ALLOC(e->xs_x, xsplit_elems(d)); ALLOC(e->xs_attn, xsplit_elems(c.n_q_heads * c.head_dim));

@@ -57,6 +57,12 @@ struct WF32 {
   __device__ __forceinline__ static float get(const void* base, size_t off) {
     return static_cast<const float*>(base)[off];
   }
+  __device__ __forceinline__ static uint4 raw(const void* base, size_t off) {
+    return *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
+  }
+  __device__ __forceinline__ static void widen(const uint4& v, float (&o)[VEC]) {
+    o[0] = __uint_as_float(v.x); o[1] = __uint_as_float(v.y); o[2] = __uint_as_float(v.z); o[3] = __uint_as_float(v.w);
+  }
 };
 // BF16 matrices: 8 elements per 16-byte load, widened to FP32 exactly.
 struct WBF16 {
@@ -73,6 +79,17 @@ struct WBF16 {
   }
   __device__ __forceinline__ static float get(const void* base, size_t off) {
     return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(base)[off]) << 16);
+  }
+  __device__ __forceinline__ static uint4 raw(const void* base, size_t off) {
+    return *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
+  }
+  __device__ __forceinline__ static void widen(const uint4& v, float (&o)[VEC]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
   }
 };
 
@@ -692,7 +709,7 @@ struct AttnArgs {
   const float* qn_w; const float* kn_w; float eps;
   const float2* rope;                    // [rows][hd/2] (cos, sin) at the row's position
   const int* kv_len; const int* active;
-  float* part;                           // [rows][Hq][max_chunks][hd+2]
+  float* part;                           // [rows][Hq][max_chunks][part_stride(hd)]: o[hd], max, sum
   float* out; int ldo;                   // [rows][Hq hd]
   int Hq, Hkv, hd, max_ctx, max_chunks;
   float scale;
@@ -701,6 +718,9 @@ struct AttnArgs {
 };
 
 constexpr int ATT_DPL = 16;      // head dims per lane
+// Floats per chunk partial: the hd outputs, the chunk's max and sum, padded
+// so every partial starts 16-byte aligned (hd is a multiple of 16).
+__host__ __device__ constexpr int part_stride(int hd) { return hd + 4; }
 
 __host__ __device__ constexpr size_t attn_smem_floats(int G, int hd) {
   return ((size_t)G * hd + 4 * (size_t)hd + 3 * (size_t)(hd / 2) + (size_t)G * ATT_CHUNK + (size_t)G * 2 + 3) /
@@ -915,7 +935,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(AttnArgs a) {
     if (lane == 0) { st[2 * g] = m; st[2 * g + 1] = l; }
   }
   __syncthreads();
-  const int stride = hd + 2;
+  const int stride = part_stride(hd);
   for (int i = tid; i < G * hd; i += NT) {
     const int g = i / hd, d = i - g * hd;
     const float* eg = sc + g * ATT_CHUNK;
@@ -959,7 +979,7 @@ __device__ __forceinline__ void merge_block(const float (&mv)[MERGE_CB], const f
 // A kernel of its own, so the partials need no device-scope fence.
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   const int hq = blockIdx.x, r = blockIdx.y, d = threadIdx.x;
-  const int hd = a.hd, stride = hd + 2;
+  const int hd = a.hd, stride = part_stride(hd);
   const int dd = min(d, hd - 1);         // lanes past hd mirror the last dim, no branch
   const float* pp = a.part + ((size_t)r * a.Hq + hq) * a.max_chunks * stride;
   constexpr int CB = MERGE_CB;
@@ -988,6 +1008,138 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   if (act && d < hd) {
     a.out[(size_t)r * a.ldo + (size_t)hq * hd + d] = O / L;
     if (a.xs_out) xsplit_store(a.xs_out, r, hq * hd + d, O / L);
+  }
+}
+
+// Output projection with the chunk merge of attention_kernel in its prologue
+// (few decode rows), in place of attention_combine_kernel + a residual GEMV:
+// out[m][n] = res[m][n] + sum_k W[n][k] attn[m][k].  A workgroup issues its
+// weight rows' loads first; then each thread merges VPTH consecutive outputs
+// of one (row, query head) from every chunk partial (o, max, sum) of that
+// head -- chunks in blocks of CB, loaded together, with a running max and
+// rescale -- and writes attn = O / L to LDS; after one barrier the waves
+// multiply, the weights having streamed in meanwhile.  The partials of all
+// rows and heads are re-read by every workgroup (from L2), so the grid is kept
+// small: one output row per wave, 8 waves.  Inactive rows read zeros.
+constexpr int AO_NT = 512;
+constexpr int AO_CB = 8;                    // chunks merged per block
+template <int M, int KT, int RW, typename WL>
+__global__ __launch_bounds__(AO_NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_o_kernel(GemvArgs g,
+                                                                                                  AttnArgs at) {
+  constexpr int VEC = WL::VEC;
+  constexpr int NV = KT / (64 * VEC);
+  constexpr int NW = AO_NT / 64;
+  constexpr int VPTH = M * KT / AO_NT;          // merged outputs per thread
+  constexpr int CB = AO_CB;
+  static_assert(KT % (64 * VEC) == 0 && (M * KT) % AO_NT == 0 && VPTH % 4 == 0, "attn_o_kernel shape");
+  __shared__ __attribute__((aligned(16))) float xsh[M * KT];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int row0 = (blockIdx.x * NW + wave) * RW;
+
+  // The row's length and state, the residual, the weights; the chunk
+  // partials are loaded block by block once the row's chunk count is known.
+  // (Loading all of them speculatively ahead of the weights measured slower:
+  // the partials of every row and head pass through each CU's load path.)
+  const int f = tid * VPTH, m = f / KT, k = f - m * KT, head = k / at.hd, d0 = k - head * at.hd;
+  const int kvl = at.kv_len[m], act = at.active[m];
+  const int stride = part_stride(at.hd);
+  const float* pp = at.part + ((size_t)m * at.Hq + head) * at.max_chunks * stride;
+  const int nch = act ? (kvl + 1 + ATT_CHUNK - 1) / ATT_CHUNK : 0;
+  float2 ml[CB];
+  float4 ov[CB][VPTH / 4];
+  auto load_block = [&](int c0) {
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const float* pc = pp + (size_t)min(c0 + j, nch - 1) * stride;   // past the last chunk: re-read it
+      ml[j] = *reinterpret_cast<const float2*>(pc + at.hd);
+#pragma unroll
+      for (int i = 0; i < VPTH / 4; ++i) ov[j][i] = *reinterpret_cast<const float4*>(pc + d0 + 4 * i);
+    }
+  };
+  float epi[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = min(row0 + r, g.N - 1);
+    epi[r] = g.res[(size_t)(lane < M ? lane : 0) * g.ldr + n];
+  }
+  float wv[RW][NV][VEC];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const size_t off = (size_t)min(row0 + r, g.N - 1) * KT;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) WL::load(g.w[0], off + (size_t)(j * 64 + lane) * VEC, wv[r][j]);
+  }
+
+  float Mr = -INFINITY, L = 0.f, O[VPTH];
+#pragma unroll
+  for (int v = 0; v < VPTH; ++v) O[v] = 0.f;
+  for (int c0 = 0; c0 < nch; c0 += CB) {
+    load_block(c0);
+    float Mb = Mr;
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+      if (c0 + j < nch) Mb = fmaxf(Mb, ml[j].x);
+    const float sc = expf(Mr - Mb);           // 0 on the first block (Mr = -inf)
+    L *= sc;
+#pragma unroll
+    for (int v = 0; v < VPTH; ++v) O[v] *= sc;
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+      if (c0 + j < nch) {
+        const float e = expf(ml[j].x - Mb);
+        L = fmaf(ml[j].y, e, L);
+#pragma unroll
+        for (int i = 0; i < VPTH / 4; ++i) {
+          O[4 * i] = fmaf(ov[j][i].x, e, O[4 * i]);
+          O[4 * i + 1] = fmaf(ov[j][i].y, e, O[4 * i + 1]);
+          O[4 * i + 2] = fmaf(ov[j][i].z, e, O[4 * i + 2]);
+          O[4 * i + 3] = fmaf(ov[j][i].w, e, O[4 * i + 3]);
+        }
+      }
+    Mr = Mb;
+  }
+#pragma unroll
+  for (int i = 0; i < VPTH / 4; ++i)
+    *reinterpret_cast<float4*>(&xsh[f + 4 * i]) =
+        nch ? make_float4(O[4 * i] / L, O[4 * i + 1] / L, O[4 * i + 2] / L, O[4 * i + 3] / L)
+            : make_float4(0.f, 0.f, 0.f, 0.f);
+  __syncthreads();
+
+  float acc[RW][M];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
+#pragma unroll
+  for (int mm = 0; mm < M; ++mm)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float xv[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; i += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(&xsh[mm * KT + (j * 64 + lane) * VEC + i]);
+        xv[i] = t.x; xv[i + 1] = t.y; xv[i + 2] = t.z; xv[i + 3] = t.w;
+      }
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[r][mm] = fmaf(wv[r][j][i], xv[i], acc[r][mm]);
+    }
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) acc[r][mm] = wave_sum_dpp(acc[r][mm]);
+  if (lane < M) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int n = row0 + r;
+      if (n >= g.N) continue;
+      float v = acc[r][0];
+#pragma unroll
+      for (int mm = 1; mm < M; ++mm)
+        if (mm == lane) v = acc[r][mm];
+      g.out[(size_t)lane * g.ldo + n] = v + epi[r];
+    }
   }
 }
 
@@ -1226,7 +1378,7 @@ __global__ __launch_bounds__(NTH) void attention_stream_kernel(AttnArgs a, int S
       a.out[(size_t)r * a.ldo + (size_t)(h * G + g) * hd + d] = O / L;
       if (a.xs_out) xsplit_store(a.xs_out, r, (h * G + g) * hd + d, O / L);
     } else {
-      float* pp = a.part + (((size_t)r * a.Hq + h * G + g) * a.max_chunks + s) * (hd + 2);
+      float* pp = a.part + (((size_t)r * a.Hq + h * G + g) * a.max_chunks + s) * part_stride(hd);
       pp[d] = O;
       if (d == 0) { pp[hd] = M; pp[hd + 1] = L; }
     }
@@ -1911,6 +2063,176 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
     for (int rr = 0; rr < a.rows_per_utt; ++rr) {
       a.xnext[(size_t)(r0 + rr) * a.d + dd] = e;
       a.prefix[(size_t)(r0 + rr) * a.d + dd] = 0.f;
+    }
+  }
+}
+
+// One depth step of one utterance (few decode rows): the sampler of codebook
+// q-1, the prefix advance prefix += table[q-1][code] * scale (model.py:600-605),
+// the depth input a = RMSNorm_in(hidden + prefix) and codebook q's gate/up
+// GEMV with the SwiGLU epilogue -- one launch instead of a sampler launch and
+// a GEMV launch.  Every workgroup draws the code itself from the same logits,
+// uniform and parameters (the draw is deterministic, so all agree) while its
+// weight rows stream in; workgroup 0 records the code, the advanced prefix
+// (into the other buffer of the ping-pong pair, g.gout) and a (g.norm_out, the
+// depth MLP's residual).  g: gate/up weights (w[0], w[1]), N = depth inner
+// rows, K = KT = d, x = hidden, x2 = the prefix before code q-1, out = act.
+// Dynamic LDS: the sampler's W (V doubles), compaction keys (V rounded up to a
+// power of two) and sorted filter keys (FILTER_MAX).
+__host__ __device__ constexpr int pow2_ceil(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+__host__ __device__ constexpr size_t depth_sample_smem(int V) {
+  return (size_t)V * sizeof(double) + ((size_t)pow2_ceil(V) + FILTER_MAX) * 8;
+}
+template <typename TL, int VPT, int M, int KT, int RW>
+__global__ __launch_bounds__(SNT) void depth_sample_gemv_kernel(SampleArgs a, GemvArgs g, int q) {
+  extern __shared__ unsigned char raw[];
+  double* W = reinterpret_cast<double*>(raw);
+  unsigned long long* ck = reinterpret_cast<unsigned long long*>(W + a.V);
+  unsigned long long* sk = ck + pow2_ceil(a.V);
+  __shared__ SampleSmem s;
+  __shared__ __attribute__((aligned(16))) float xsh[M * KT];
+  __shared__ float red[M][SWAVES];
+  __shared__ int code_sh;
+  constexpr int VEC = TL::VEC;
+  constexpr int NV = KT / (64 * VEC);
+  constexpr int DPT = KT / SNT;                 // input elements per thread
+  static_assert(KT % (64 * VEC) == 0 && KT % SNT == 0 && M <= 2, "depth_sample_gemv_kernel shape");
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qs = q - 1;                         // the codebook sampled here
+  const bool lead = blockIdx.x == 0;
+
+  // Loads that do not depend on the code, before the weight stream: the
+  // draw's inputs, then hidden, the prefix and the norm gain.
+  const double u = a.u_cur[qs];
+  const int forced = a.flag_cur[1];
+  const int slot = *a.fc;
+  const SkParams P = *a.params;
+  float hv[M][DPT], pv[M][DPT], gv[DPT];
+#pragma unroll
+  for (int i = 0; i < DPT; ++i) {
+    const int k = tid + i * SNT;
+    gv[i] = g.norm_w[k];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      hv[m][i] = g.x[(size_t)m * g.ldx + k];
+      pv[m][i] = g.x2[(size_t)m * g.ldx2 + k];
+    }
+  }
+  const bool q0 = (qs == 0) && P.has_q0;
+  const float temp = q0 ? P.temperature_q0 : P.temperature;
+  const int topk = q0 ? P.top_k_q0 : P.top_k;
+  const float topp = q0 ? P.top_p_q0 : P.top_p;
+  float xr[VPT];
+  merge_mask<VPT>(a.logits, M == 2 ? a.logits + a.ldl : nullptr, P.cfg_scale, a.V, a.bos, a.eos, a.pad,
+                  a.flag_cur, 0, qs != 0, temp, (lead && P.record_logits) ? a.dbg + (size_t)qs * a.V : nullptr, xr);
+  // this wave's gate and up rows
+  const int n0 = (blockIdx.x * SWAVES + wave) * RW;
+  uint4 wraw[RW][2][NV];                        // raw 16-byte words, widened where multiplied
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const size_t off = (size_t)min(n0 + r, g.N - 1) * KT;
+#pragma unroll
+    for (int sidx = 0; sidx < 2; ++sidx)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) wraw[r][sidx][j] = TL::raw(g.w[sidx], off + (size_t)(j * 64 + lane) * VEC);
+  }
+
+  int code = sample_core<VPT>(xr, a.V, temp, topk, topp, u, ck, sk, W, s);
+  const size_t uoff = (size_t)slot * a.Q + qs;
+  if (tid == 0) {
+    if (forced) code = (int)a.forced_ring[uoff];
+    code = min(max(code, 0), a.V - 1);
+    code_sh = code;
+    if (lead) {
+      a.codes_ring[uoff] = code;
+      a.codes_cur[qs] = code;
+    }
+  }
+  __syncthreads();
+  code = code_sh;
+
+  // prefix += table[q-1][code] * scale; x = hidden + prefix; a = w * (x / rms(x))
+  const size_t trow = ((size_t)qs * a.V + code) * KT;
+  float tv[DPT];
+#pragma unroll
+  for (int i = 0; i < DPT; ++i) tv[i] = TL::get(a.table, trow + tid + i * SNT);
+  float xv[M][DPT];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) {
+      const float p = __fadd_rn(pv[m][i], __fmul_rn(tv[i], a.scale));
+      xv[m][i] = __fadd_rn(hv[m][i], p);
+      if (lead) g.gout[(size_t)m * g.ldgo + tid + i * SNT] = p;
+      ss = fmaf(xv[m][i], xv[m][i], ss);
+    }
+    ss = wave_sum_dpp(ss);
+    if (lane == 0) red[m][wave] = ss;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < SWAVES; ++w) t += red[m][w];
+    const float inv = 1.0f / sqrtf(t / (float)KT + g.eps);
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) {
+      const float y = gv[i] * (xv[m][i] * inv);
+      xsh[m * KT + tid + i * SNT] = y;
+      if (lead) g.norm_out[(size_t)m * g.ldno + tid + i * SNT] = y;
+    }
+  }
+  __syncthreads();
+
+  float acc[RW][2][M];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int sidx = 0; sidx < 2; ++sidx)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r][sidx][m] = 0.f;
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float x[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; i += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(&xsh[m * KT + (j * 64 + lane) * VEC + i]);
+        x[i] = t.x; x[i + 1] = t.y; x[i + 2] = t.z; x[i + 3] = t.w;
+      }
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int sidx = 0; sidx < 2; ++sidx) {
+          float w[VEC];
+          TL::widen(wraw[r][sidx][j], w);
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[r][sidx][m] = fmaf(w[i], x[i], acc[r][sidx][m]);
+        }
+    }
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int sidx = 0; sidx < 2; ++sidx)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r][sidx][m] = wave_sum_dpp(acc[r][sidx][m]);
+  if (lane < M) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int n = n0 + r;
+      if (n >= g.N) continue;
+      float gt = acc[r][0][0], up = acc[r][1][0];
+#pragma unroll
+      for (int m = 1; m < M; ++m)
+        if (m == lane) { gt = acc[r][0][m]; up = acc[r][1][m]; }
+      g.out[(size_t)lane * g.ldo + n] = gt / (1.0f + expf(-gt)) * up;
     }
   }
 }

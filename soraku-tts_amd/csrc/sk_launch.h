@@ -175,6 +175,34 @@ static hipError_t launch_sample_step(const SampleArgs& a, int q, int n_utts, hip
   });
 }
 
+// Depth step with the previous codebook's sampler folded in
+// (depth_sample_gemv_kernel): one utterance, d = 1024 or 2048, 1 or 2 rows.
+static inline bool depth_fused_fits(int d, int rows, int depth_inner, int V) {
+  const int rw = depth_inner >= 4096 ? 2 : 1;
+  return (d == 1024 || d == 2048) && (rows == 1 || rows == 2) && depth_inner % (SWAVES * rw) == 0 &&
+         V <= MAX_V && depth_sample_smem(V) <= 65536;
+}
+template <typename TL, int VPT, int M, int KT>
+static hipError_t launch_depth_fused_t(const SampleArgs& s, const GemvArgs& g, int q, hipStream_t st) {
+  const size_t smem = depth_sample_smem(s.V);
+  if (g.N >= 4096)
+    hipLaunchKernelGGL((depth_sample_gemv_kernel<TL, VPT, M, KT, 2>), dim3(g.N / (SWAVES * 2)), dim3(SNT), smem, st,
+                       s, g, q);
+  else
+    hipLaunchKernelGGL((depth_sample_gemv_kernel<TL, VPT, M, KT, 1>), dim3(g.N / SWAVES), dim3(SNT), smem, st, s, g,
+                       q);
+  return hipGetLastError();
+}
+template <typename TL>
+static hipError_t launch_depth_fused(const SampleArgs& s, const GemvArgs& g, int rows, int q, hipStream_t st) {
+  return with_vpt(s.V, [&](auto vpt) {
+    constexpr int P = decltype(vpt)::value;
+    if (g.K == 1024)
+      return rows == 2 ? launch_depth_fused_t<TL, P, 2, 1024>(s, g, q, st) : launch_depth_fused_t<TL, P, 1, 1024>(s, g, q, st);
+    return rows == 2 ? launch_depth_fused_t<TL, P, 2, 2048>(s, g, q, st) : launch_depth_fused_t<TL, P, 1, 2048>(s, g, q, st);
+  });
+}
+
 static inline hipError_t prepare_sampler() {
   static bool done = false;
   if (done) return hipSuccess;

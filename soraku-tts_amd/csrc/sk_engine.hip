@@ -151,8 +151,16 @@ struct sk_engine {
   std::vector<char> staged;
   SkParams p_host{};
 
+  // The frame graph.  Its chunk-attention nodes launch `grid_chunks` chunks
+  // per (row, kv head); before each replay the host sets that to the chunks
+  // the active rows hold (only when it changes).  A larger grid is always
+  // correct (chunks past a row's length exit at once), and the count only
+  // grows between prefills, so replays already queued stay correct.
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  std::vector<hipGraphNode_t> attn_nodes;
+  std::vector<hipKernelNodeParams> attn_params;
+  int grid_chunks = 0;
 
   // batched prefill activations, sized for the largest packed prefix so far
   int pf_cap = 0;
@@ -175,6 +183,54 @@ void drop_graphs(sk_engine* e) {
   if (e->exec) hipGraphExecDestroy(e->exec);
   if (e->graph) hipGraphDestroy(e->graph);
   e->exec = nullptr; e->graph = nullptr;
+  e->attn_nodes.clear();
+  e->attn_params.clear();
+  e->grid_chunks = 0;
+}
+
+// Chunks of the frame `ahead` frames after the host's state: every active
+// row's chunk count once that frame's token is appended.
+int frame_chunks(const sk_engine* e, int ahead) {
+  int nch = 1;
+  for (int r = 0; r < e->rows; ++r)
+    if (e->active_host[r]) nch = std::max(nch, (e->kv_host[r] + ahead + 1 + ATT_CHUNK - 1) / ATT_CHUNK);
+  return std::min(nch, e->max_chunks);
+}
+
+// Point the graph's chunk-attention nodes at `nch` chunks (no-op when equal).
+hipError_t set_grid_chunks(sk_engine* e, int nch) {
+  if (e->attn_nodes.empty() || nch == e->grid_chunks) return hipSuccess;
+  for (size_t i = 0; i < e->attn_nodes.size(); ++i) {
+    e->attn_params[i].gridDim.x = nch;
+    const hipError_t err = hipGraphExecKernelNodeSetParams(e->exec, e->attn_nodes[i], &e->attn_params[i]);
+    if (err != hipSuccess) return err;
+  }
+  e->grid_chunks = nch;
+  return hipSuccess;
+}
+
+// The captured frame is a chain; collect its chunk-attention kernel nodes.
+hipError_t find_attn_nodes(sk_engine* e) {
+  size_t n = 0;
+  hipError_t err = hipGraphGetNodes(e->graph, nullptr, &n);
+  if (err != hipSuccess) return err;
+  std::vector<hipGraphNode_t> nodes(n);
+  if ((err = hipGraphGetNodes(e->graph, nodes.data(), &n)) != hipSuccess) return err;
+  const void* fns[2] = {reinterpret_cast<const void*>(attention_kernel<float>),
+                        reinterpret_cast<const void*>(attention_kernel<uint16_t>)};
+  for (hipGraphNode_t node : nodes) {
+    hipGraphNodeType t;
+    if ((err = hipGraphNodeGetType(node, &t)) != hipSuccess) return err;
+    if (t != hipGraphNodeTypeKernel) continue;
+    hipKernelNodeParams p{};
+    if ((err = hipGraphKernelNodeGetParams(node, &p)) != hipSuccess) return err;
+    if (p.func == fns[0] || p.func == fns[1]) {
+      e->attn_nodes.push_back(node);
+      e->attn_params.push_back(p);
+    }
+  }
+  e->grid_chunks = e->max_chunks;   // as captured
+  return hipSuccess;
 }
 
 int validate_config(const sk_config* c) {
@@ -301,7 +357,7 @@ SkinnyArgs skinny_args(const void* w, int N, int K, const float* x, int ldx, flo
 // the chip.
 hipError_t launch_attn_chunks(sk_engine* e, const AttnArgs& at, bool merge = true) {
   const size_t asmem = attn_smem_floats(e->G, at.hd) * sizeof(float);
-  const dim3 grid(e->max_chunks, at.Hkv, e->rows);
+  const dim3 grid(e->max_chunks, at.Hkv, e->rows);   // replays set it to the live chunks
   if (e->c.kv_dtype == SK_BF16)
     hipLaunchKernelGGL(attention_kernel<uint16_t>, grid, dim3(NT), asmem, e->stream, at);
   else
@@ -400,6 +456,7 @@ hipError_t enqueue_trunk(sk_engine* e) {
     at.kv_len = e->kv_len; at.active = e->active;
     at.out = e->attn; at.ldo = c.n_q_heads * hd;
     at.Hq = c.n_q_heads; at.Hkv = c.n_kv_heads; at.hd = hd; at.max_ctx = c.max_ctx;
+
     at.scale = 1.0f / sqrtf((float)hd);
     at.xs_out = e->xs_attn;
     const bool fused_o = attn_o_fits(e);
@@ -665,6 +722,14 @@ int capture(sk_engine* e, hipError_t (*body)(sk_engine*), hipGraph_t* g, hipGrap
   if (ins != hipSuccess) {
     hipGraphDestroy(graph);
     return fail(SK_EHIP, "hipGraphInstantiate failed: %s", hipGetErrorString(ins));
+  }
+  // Upload now, so the first replay of a context bucket's graph (mid-decode)
+  // does not pay for it.
+  const hipError_t up = hipGraphUpload(exec, e->stream);
+  if (up != hipSuccess) {
+    hipGraphExecDestroy(exec);
+    hipGraphDestroy(graph);
+    return fail(SK_EHIP, "hipGraphUpload failed: %s", hipGetErrorString(up));
   }
   *g = graph;
   *x = exec;
@@ -1123,7 +1188,15 @@ int sk_capture(sk_engine* e) {
   if (rc != SK_OK) return rc;
   if (e->exec) return SK_OK;
   SK_HIP(hipStreamSynchronize(e->stream));
-  return capture(e, enqueue_frame, &e->graph, &e->exec);
+  rc = capture(e, enqueue_frame, &e->graph, &e->exec);
+  if (rc != SK_OK) return rc;
+  const hipError_t fe = find_attn_nodes(e);
+  if (fe != hipSuccess) {
+    drop_graphs(e);
+    return fail(SK_EHIP, "frame graph nodes: %s", hipGetErrorString(fe));
+  }
+  SK_HIP(hipStreamSynchronize(e->stream));
+  return SK_OK;
 }
 
 static int check_step(sk_engine* e, int n) {
@@ -1163,6 +1236,7 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
   if (forced_codes)
     SK_HIP(hipMemcpyAsync(e->forced_ring + slot * nq, forced_codes, nq * sizeof(int64_t), hipMemcpyHostToDevice,
                           e->stream));
+  SK_HIP(set_grid_chunks(e, frame_chunks(e, 0)));
   SK_HIP(hipGraphLaunch(e->exec, e->stream));
   SK_HIP(hipMemcpyAsync(codes_out, e->codes_ring + slot * nq, nq * sizeof(int64_t), hipMemcpyDeviceToHost, e->stream));
   if (logits_dbg)
@@ -1198,7 +1272,10 @@ int sk_queue_frames(sk_engine* e, int32_t n, const double* uniforms, const int32
 int sk_replay(sk_engine* e, int32_t n) {
   int rc = check_step(e, n);
   if (rc != SK_OK) return rc;
-  for (int i = 0; i < n; ++i) SK_HIP(hipGraphLaunch(e->exec, e->stream));
+  for (int i = 0; i < n; ++i) {
+    SK_HIP(set_grid_chunks(e, frame_chunks(e, i)));
+    SK_HIP(hipGraphLaunch(e->exec, e->stream));
+  }
   e->fc_host += n;
   for (int r = 0; r < e->rows; ++r) e->kv_host[r] += n * e->active_host[r];
   return SK_OK;

@@ -1014,15 +1014,20 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
 // Output projection with the chunk merge of attention_kernel in its prologue
 // (few decode rows), in place of attention_combine_kernel + a residual GEMV:
 // out[m][n] = res[m][n] + sum_k W[n][k] attn[m][k].  A workgroup issues its
-// weight rows' loads first; then each thread merges VPTH consecutive outputs
-// of one (row, query head) from every chunk partial (o, max, sum) of that
-// head -- chunks in blocks of CB, loaded together, with a running max and
-// rescale -- and writes attn = O / L to LDS; after one barrier the waves
-// multiply, the weights having streamed in meanwhile.  The partials of all
-// rows and heads are re-read by every workgroup (from L2), so the grid is kept
-// small: one output row per wave, 8 waves.  Inactive rows read zeros.
+// weight rows' loads; then, once the row's length has arrived, the chunk
+// partials (o, max, sum) of the (row, query head) each thread merges -- VPTH
+// consecutive outputs -- in blocks of AO_CB chunks, the index clamped to the
+// row's own last chunk (those lines were just written; bounding the first
+// block by the launch's chunk count instead, to skip the length round trip,
+// read colder lines for the shorter row and measured 1.5 us slower per
+// launch).  The merge is in chunk order with a running max and rescale;
+// attn = O / L goes to LDS, and after one barrier the waves multiply.
+// Every workgroup re-reads the partials of all rows and heads, and each load
+// instruction costs its CU's load pipe even when it hits in L1, so blocks are
+// small (16 measured 2.5 us slower per launch) and the grid is small: one
+// output row per wave, 8 waves.  Inactive rows read zeros.
 constexpr int AO_NT = 512;
-constexpr int AO_CB = 8;                    // chunks merged per block
+constexpr int AO_CB = 8;                     // chunks per merge block
 template <int M, int KT, int RW, typename WL>
 __global__ __launch_bounds__(AO_NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_o_kernel(GemvArgs g,
                                                                                                   AttnArgs at) {
@@ -1036,26 +1041,8 @@ __global__ __launch_bounds__(AO_NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int row0 = (blockIdx.x * NW + wave) * RW;
 
-  // The row's length and state, the residual, the weights; the chunk
-  // partials are loaded block by block once the row's chunk count is known.
-  // (Loading all of them speculatively ahead of the weights measured slower:
-  // the partials of every row and head pass through each CU's load path.)
   const int f = tid * VPTH, m = f / KT, k = f - m * KT, head = k / at.hd, d0 = k - head * at.hd;
   const int kvl = at.kv_len[m], act = at.active[m];
-  const int stride = part_stride(at.hd);
-  const float* pp = at.part + ((size_t)m * at.Hq + head) * at.max_chunks * stride;
-  const int nch = act ? (kvl + 1 + ATT_CHUNK - 1) / ATT_CHUNK : 0;
-  float2 ml[CB];
-  float4 ov[CB][VPTH / 4];
-  auto load_block = [&](int c0) {
-#pragma unroll
-    for (int j = 0; j < CB; ++j) {
-      const float* pc = pp + (size_t)min(c0 + j, nch - 1) * stride;   // past the last chunk: re-read it
-      ml[j] = *reinterpret_cast<const float2*>(pc + at.hd);
-#pragma unroll
-      for (int i = 0; i < VPTH / 4; ++i) ov[j][i] = *reinterpret_cast<const float4*>(pc + d0 + 4 * i);
-    }
-  };
   float epi[RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
@@ -1069,7 +1056,20 @@ __global__ __launch_bounds__(AO_NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
 #pragma unroll
     for (int j = 0; j < NV; ++j) WL::load(g.w[0], off + (size_t)(j * 64 + lane) * VEC, wv[r][j]);
   }
-
+  const int stride = part_stride(at.hd);
+  const float* pp = at.part + ((size_t)m * at.Hq + head) * at.max_chunks * stride;
+  float2 ml[CB];
+  float4 ov[CB][VPTH / 4];
+  const int nch = act ? (kvl + 1 + ATT_CHUNK - 1) / ATT_CHUNK : 0;
+  auto load_block = [&](int c0) {
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {            // past the row's last chunk: re-read it
+      const float* pc = pp + (size_t)min(c0 + j, nch - 1) * stride;
+      ml[j] = *reinterpret_cast<const float2*>(pc + at.hd);
+#pragma unroll
+      for (int i = 0; i < VPTH / 4; ++i) ov[j][i] = *reinterpret_cast<const float4*>(pc + d0 + 4 * i);
+    }
+  };
   float Mr = -INFINITY, L = 0.f, O[VPTH];
 #pragma unroll
   for (int v = 0; v < VPTH; ++v) O[v] = 0.f;

@@ -152,6 +152,46 @@ def test_queued_replay_equals_stepwise(hip_device):
     e.close()
 
 
+def test_queued_replay_across_chunk_boundary(hip_device):
+    """Queued replays (no host sync between frames) whose rows cross a 32-token
+    attention chunk boundary mid-queue (cond 28 -> 40 positions): the host
+    widens the attention grid between launches; codes equal step-by-step
+    decoding and the float64 oracle's."""
+    from oracle.model import TINY
+    from soraku_amd import GraphFrameEngine
+
+    s = TINY
+    w = synthetic_weights(s, 61, norm_gain_std=0.1, bias_std=0.02)
+    rng = np.random.default_rng(61)
+    text, uncond = rng.integers(0, s.text_vocab, 26), np.array([4])
+    prompt = rng.integers(0, s.codebook_size, (1, s.n_codebooks))
+    n = 12
+    u = rng.random((n, s.n_codebooks))
+    kw = dict(temperature=0.9, top_k=8, top_p=0.9, cfg_scale=1.5, min_new_frames=n)
+    ref, _ = generate(OracleModel(s, w, np.float64), input_ids=text, prompt_codes=prompt,
+                      uncond_input_ids=uncond, uniforms=u, max_new_frames=n, batched=True, **kw)
+
+    def engine():
+        e = GraphFrameEngine(device=hip_device, max_cache_len=96, cfg_scale=1.5, batch=2, state_dict=w,
+                             shape=_shape(s))
+        e.set_temperature(0.9)
+        e.set_sampling(sampled=True, top_k=8, top_p=0.9)
+        e.prefill(text, uncond, prompt)
+        e.capture()
+        return e
+
+    e = engine()
+    step = np.stack([e.step_frame(mask_eos_q0=True, uniforms=u[i]).numpy() for i in range(n)])
+    e.close()
+    e = engine()
+    e.queue_frames(u, np.ones(n, np.int32))
+    e.replay(n)
+    got = e.read_codes(n)[:, 0]
+    e.close()
+    np.testing.assert_array_equal(step, ref)
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_frame_ring_reset(hip_device):
     """sk_reset_frames: an engine whose frame ring holds 3 frames decodes 7
     (restarting the ring whenever it is full) with the same codes and logits

@@ -152,15 +152,21 @@ struct sk_engine {
   SkParams p_host{};
 
   // The frame graph.  Its chunk-attention nodes launch `grid_chunks` chunks
-  // per (row, kv head); before each replay the host sets that to the chunks
-  // the active rows hold (only when it changes).  A larger grid is always
-  // correct (chunks past a row's length exit at once), and the count only
-  // grows between prefills, so replays already queued stay correct.
+  // per (row, kv head), and its attn_o nodes take each row's chunk count as
+  // an argument; before each replay the host sets both to the chunks the
+  // rows hold (only when they change).  A larger grid or bound is always
+  // correct (chunks past a row's length exit at once / are masked by its
+  // length), and the counts only grow between prefills, so replays already
+  // queued stay correct.
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
-  std::vector<hipGraphNode_t> attn_nodes;
-  std::vector<hipKernelNodeParams> attn_params;
+  std::vector<hipGraphNode_t> attn_nodes, o_nodes;
+  std::vector<hipKernelNodeParams> attn_params, o_params;
+  std::vector<GemvArgs> o_gargs;
+  std::vector<AttnArgs> o_aargs;
+  std::vector<void*> o_kp;           // kernelParams of the attn_o nodes: 2 per node
   int grid_chunks = 0;
+  int row_chunks[4] = {0, 0, 0, 0};
 
   // batched prefill activations, sized for the largest packed prefix so far
   int pf_cap = 0;
@@ -185,27 +191,46 @@ void drop_graphs(sk_engine* e) {
   e->exec = nullptr; e->graph = nullptr;
   e->attn_nodes.clear();
   e->attn_params.clear();
+  e->o_nodes.clear();
+  e->o_params.clear();
+  e->o_gargs.clear();
+  e->o_aargs.clear();
+  e->o_kp.clear();
   e->grid_chunks = 0;
+  for (int& v : e->row_chunks) v = 0;
 }
 
-// Chunks of the frame `ahead` frames after the host's state: every active
-// row's chunk count once that frame's token is appended.
-int frame_chunks(const sk_engine* e, int ahead) {
-  int nch = 1;
-  for (int r = 0; r < e->rows; ++r)
-    if (e->active_host[r]) nch = std::max(nch, (e->kv_host[r] + ahead + 1 + ATT_CHUNK - 1) / ATT_CHUNK);
-  return std::min(nch, e->max_chunks);
+// Each row's chunk count for the frame `ahead` frames after the host's
+// state, once that frame's token is appended (1 for inactive rows).
+int row_frame_chunks(const sk_engine* e, int r, int ahead) {
+  if (!e->active_host[r]) return 1;
+  return std::min(e->max_chunks, (e->kv_host[r] + ahead + 1 + ATT_CHUNK - 1) / ATT_CHUNK);
 }
 
-// Point the graph's chunk-attention nodes at `nch` chunks (no-op when equal).
-hipError_t set_grid_chunks(sk_engine* e, int nch) {
-  if (e->attn_nodes.empty() || nch == e->grid_chunks) return hipSuccess;
-  for (size_t i = 0; i < e->attn_nodes.size(); ++i) {
-    e->attn_params[i].gridDim.x = nch;
-    const hipError_t err = hipGraphExecKernelNodeSetParams(e->exec, e->attn_nodes[i], &e->attn_params[i]);
+// Point the graph's chunk-attention nodes and attn_o nodes at the frame's
+// chunk counts (no-op when unchanged).
+hipError_t set_frame_chunks(sk_engine* e, int ahead) {
+  if (!e->exec) return hipSuccess;
+  int rc[4] = {1, 1, 1, 1}, nch = 1;
+  for (int r = 0; r < e->rows && r < 4; ++r) nch = std::max(nch, rc[r] = row_frame_chunks(e, r, ahead));
+  for (int r = 4; r < e->rows; ++r) nch = std::max(nch, row_frame_chunks(e, r, ahead));
+  hipError_t err = hipSuccess;
+  if (nch != e->grid_chunks) {
+    for (size_t i = 0; i < e->attn_nodes.size() && err == hipSuccess; ++i) {
+      e->attn_params[i].gridDim.x = nch;
+      err = hipGraphExecKernelNodeSetParams(e->exec, e->attn_nodes[i], &e->attn_params[i]);
+    }
     if (err != hipSuccess) return err;
+    e->grid_chunks = nch;
   }
-  e->grid_chunks = nch;
+  if (!std::equal(rc, rc + 4, e->row_chunks)) {
+    for (size_t i = 0; i < e->o_nodes.size() && err == hipSuccess; ++i) {
+      for (int r = 0; r < 4; ++r) e->o_aargs[i].row_chunks[r] = rc[r];
+      err = hipGraphExecKernelNodeSetParams(e->exec, e->o_nodes[i], &e->o_params[i]);
+    }
+    if (err != hipSuccess) return err;
+    std::copy(rc, rc + 4, e->row_chunks);
+  }
   return hipSuccess;
 }
 
@@ -218,6 +243,12 @@ hipError_t find_attn_nodes(sk_engine* e) {
   if ((err = hipGraphGetNodes(e->graph, nodes.data(), &n)) != hipSuccess) return err;
   const void* fns[2] = {reinterpret_cast<const void*>(attention_kernel<float>),
                         reinterpret_cast<const void*>(attention_kernel<uint16_t>)};
+  const void* ofns[6] = {reinterpret_cast<const void*>(attn_o_kernel<1, 2048, 1, WF32>),
+                         reinterpret_cast<const void*>(attn_o_kernel<2, 2048, 1, WF32>),
+                         reinterpret_cast<const void*>(attn_o_kernel<4, 2048, 1, WF32>),
+                         reinterpret_cast<const void*>(attn_o_kernel<1, 2048, 1, WBF16>),
+                         reinterpret_cast<const void*>(attn_o_kernel<2, 2048, 1, WBF16>),
+                         reinterpret_cast<const void*>(attn_o_kernel<4, 2048, 1, WBF16>)};
   for (hipGraphNode_t node : nodes) {
     hipGraphNodeType t;
     if ((err = hipGraphNodeGetType(node, &t)) != hipSuccess) return err;
@@ -227,9 +258,23 @@ hipError_t find_attn_nodes(sk_engine* e) {
     if (p.func == fns[0] || p.func == fns[1]) {
       e->attn_nodes.push_back(node);
       e->attn_params.push_back(p);
+    } else if (std::find(ofns, ofns + 6, p.func) != ofns + 6) {
+      // own copies of the (GemvArgs, AttnArgs) arguments, to rewrite row_chunks
+      e->o_nodes.push_back(node);
+      e->o_params.push_back(p);
+      e->o_gargs.push_back(*static_cast<const GemvArgs*>(p.kernelParams[0]));
+      e->o_aargs.push_back(*static_cast<const AttnArgs*>(p.kernelParams[1]));
     }
   }
+  e->o_kp.resize(2 * e->o_nodes.size());
+  for (size_t i = 0; i < e->o_nodes.size(); ++i) {
+    e->o_kp[2 * i] = &e->o_gargs[i];
+    e->o_kp[2 * i + 1] = &e->o_aargs[i];
+    e->o_params[i].kernelParams = &e->o_kp[2 * i];
+    e->o_params[i].extra = nullptr;
+  }
   e->grid_chunks = e->max_chunks;   // as captured
+  for (int r = 0; r < 4; ++r) e->row_chunks[r] = e->max_chunks;
   return hipSuccess;
 }
 
@@ -459,6 +504,7 @@ hipError_t enqueue_trunk(sk_engine* e) {
 
     at.scale = 1.0f / sqrtf((float)hd);
     at.xs_out = e->xs_attn;
+    for (int& rc : at.row_chunks) rc = e->max_chunks;   // replays set each row's count
     const bool fused_o = attn_o_fits(e);
     if ((err = e->attn_splits > 0 ? launch_attn_stream(e, at) : launch_attn_chunks(e, at, !fused_o)) != hipSuccess)
       return err;
@@ -1236,7 +1282,7 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
   if (forced_codes)
     SK_HIP(hipMemcpyAsync(e->forced_ring + slot * nq, forced_codes, nq * sizeof(int64_t), hipMemcpyHostToDevice,
                           e->stream));
-  SK_HIP(set_grid_chunks(e, frame_chunks(e, 0)));
+  SK_HIP(set_frame_chunks(e, 0));
   SK_HIP(hipGraphLaunch(e->exec, e->stream));
   SK_HIP(hipMemcpyAsync(codes_out, e->codes_ring + slot * nq, nq * sizeof(int64_t), hipMemcpyDeviceToHost, e->stream));
   if (logits_dbg)
@@ -1273,7 +1319,7 @@ int sk_replay(sk_engine* e, int32_t n) {
   int rc = check_step(e, n);
   if (rc != SK_OK) return rc;
   for (int i = 0; i < n; ++i) {
-    SK_HIP(set_grid_chunks(e, frame_chunks(e, i)));
+    SK_HIP(set_frame_chunks(e, i));
     SK_HIP(hipGraphLaunch(e->exec, e->stream));
   }
   e->fc_host += n;

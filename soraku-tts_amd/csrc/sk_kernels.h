@@ -714,6 +714,8 @@ struct AttnArgs {
   int Hq, Hkv, hd, max_ctx, max_chunks;
   float scale;
   int nparts;                            // > 0: partials per (row, q head) to merge (stream kernel splits)
+  int row_chunks[4];                     // attn_o_kernel: an upper bound on each row's chunk count
+                                         // (the host's count for the frame; >= the row's own)
   uint16_t* xs_out;                      // output again in split form (null: none)
 };
 
@@ -1014,13 +1016,14 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
 // Output projection with the chunk merge of attention_kernel in its prologue
 // (few decode rows), in place of attention_combine_kernel + a residual GEMV:
 // out[m][n] = res[m][n] + sum_k W[n][k] attn[m][k].  A workgroup issues its
-// weight rows' loads; then, once the row's length has arrived, the chunk
-// partials (o, max, sum) of the (row, query head) each thread merges -- VPTH
-// consecutive outputs -- in blocks of AO_CB chunks, the index clamped to the
-// row's own last chunk (those lines were just written; bounding the first
-// block by the launch's chunk count instead, to skip the length round trip,
-// read colder lines for the shorter row and measured 1.5 us slower per
-// launch).  The merge is in chunk order with a running max and rescale;
+// weight rows' loads, then the first AO_CB chunk partials (o, max, sum) of
+// the (row, query head) each thread merges -- VPTH consecutive outputs --
+// with the chunk index clamped to the row's chunk count from the launch
+// arguments (at.row_chunks, set by the host), so these loads wait on no
+// memory round trip; the row's length, loaded beside them, then gives the
+// exact count that masks the merge and bounds the later blocks (a bound
+// below it would reload the first block).  (Bounding the first block by the largest row's count
+// instead read colder lines for the shorter row: 1.5 us slower per launch.)  The merge is in chunk order with a running max and rescale;
 // attn = O / L goes to LDS, and after one barrier the waves multiply.
 // Every workgroup re-reads the partials of all rows and heads, and each load
 // instruction costs its CU's load pipe even when it hits in L1, so blocks are
@@ -1043,6 +1046,7 @@ __global__ __launch_bounds__(AO_NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
 
   const int f = tid * VPTH, m = f / KT, k = f - m * KT, head = k / at.hd, d0 = k - head * at.hd;
   const int kvl = at.kv_len[m], act = at.active[m];
+  const int rc = max(1, at.row_chunks[m]);
   float epi[RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
@@ -1060,21 +1064,23 @@ __global__ __launch_bounds__(AO_NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
   const float* pp = at.part + ((size_t)m * at.Hq + head) * at.max_chunks * stride;
   float2 ml[CB];
   float4 ov[CB][VPTH / 4];
-  const int nch = act ? (kvl + 1 + ATT_CHUNK - 1) / ATT_CHUNK : 0;
-  auto load_block = [&](int c0) {
+  auto load_block = [&](int c0, int bound) {
 #pragma unroll
-    for (int j = 0; j < CB; ++j) {            // past the row's last chunk: re-read it
-      const float* pc = pp + (size_t)min(c0 + j, nch - 1) * stride;
+    for (int j = 0; j < CB; ++j) {            // past the bound: re-read its last chunk
+      const float* pc = pp + (size_t)min(c0 + j, bound - 1) * stride;
       ml[j] = *reinterpret_cast<const float2*>(pc + at.hd);
 #pragma unroll
       for (int i = 0; i < VPTH / 4; ++i) ov[j][i] = *reinterpret_cast<const float4*>(pc + d0 + 4 * i);
     }
   };
+  load_block(0, rc);
+  const int nch = act ? (kvl + 1 + ATT_CHUNK - 1) / ATT_CHUNK : 0;
+  if (nch > rc) load_block(0, nch);           // a bound below the row's count: reload (never expected)
   float Mr = -INFINITY, L = 0.f, O[VPTH];
 #pragma unroll
   for (int v = 0; v < VPTH; ++v) O[v] = 0.f;
   for (int c0 = 0; c0 < nch; c0 += CB) {
-    load_block(c0);
+    if (c0 > 0) load_block(c0, nch);
     float Mb = Mr;
 #pragma unroll
     for (int j = 0; j < CB; ++j)

@@ -307,9 +307,9 @@ def many_utterances(args):
         from soraku_amd.synthetic import is_matrix
 
         w32 = {k: (round_bf16(v) if is_matrix(k) else v) for k, v in synthetic_weights(shape, args.seed).items()}
-        cb = cpu_baseline(shape, w32, items[:2], [u[:, i * shape.n_codebooks:(i + 1) * shape.n_codebooks]
-                                                  for i in range(2)],
-                          temperature=TEMP, unit="utterance-frames/s")
+        q = shape.n_codebooks
+        cb = cpu_baseline(shape, w32, [(t, p, un) for t, un, p in items[:2]],   # items hold (text, uncond, prompt)
+                          [u[:, i * q:(i + 1) * q] for i in range(2)], temperature=TEMP, unit="utterance-frames/s")
         cb["speedup"] = out["value"] / cb["value"]
         out["cpu_baseline"] = cb
     print(json.dumps(out))

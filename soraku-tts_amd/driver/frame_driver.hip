@@ -226,6 +226,15 @@ int main(int argc, char** argv) {
   }
   if (wide && kv_mid >= 0)
     for (int r = 0; r < 2 * utts; ++r) SKCHECK(sk_set_row_state(e, r, full_len[r] + kv_mid, full_len[r] + kv_mid));
+  // the rows' KV lengths at the first decoded frame (what byte counts depend on)
+  fprintf(stderr, "kv_lens:");
+  for (int r = 0; r < 2 * utts; ++r) {
+    int kv = full_len[r];
+    if (!wide && kv_c >= 0) kv = r == 0 ? kv_c : kv_u;
+    if (wide && kv_mid >= 0) kv += kv_mid;
+    fprintf(stderr, " %d", kv);
+  }
+  fprintf(stderr, "\n");
   SKCHECK(sk_set_sampling(e, 1.5f, 0.9f, 50, 0.95f, 0, 0.f, 0, 0.f));
   SKCHECK(sk_capture(e));
 

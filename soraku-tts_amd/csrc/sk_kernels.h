@@ -1213,8 +1213,9 @@ __global__ __launch_bounds__(NTH) void attention_stream_kernel(AttnArgs a, int S
   // head dim dim_of(e).
   auto dim_of = [&](int e) { return ((e / EPV) * LPT + sub) * EPV + e % EPV; };
   struct Tok { uint4 k[NLD], v[NLD]; };
+  int t_last = 0;                        // last cached row of this (row, kv head)
   auto load = [&](int j, Tok& b) {       // token index clamped into the cache: always in bounds
-    const int t = min(t0 + j * tstep, a.max_ctx - 1);
+    const int t = min(t0 + j * tstep, t_last);
     const uint4* kp = reinterpret_cast<const uint4*>(static_cast<const KT*>(a.kc) + (head_base + t) * hd) + sub;
     const uint4* vp = reinterpret_cast<const uint4*>(static_cast<const KT*>(a.vc) + (head_base + t) * hd) + sub;
 #pragma unroll
@@ -1236,14 +1237,21 @@ __global__ __launch_bounds__(NTH) void attention_stream_kernel(AttnArgs a, int S
     }
   };
 
-  // Raw q / k / v of this head, norm gains and RoPE entry to registers, then
-  // the first D tokens of every slot -- all before the row's length arrives.
-  const float* row = a.qkv + (size_t)r * a.ldqkv;
-  // The row's length and state first (uniform, scalar loads: waiting for them
-  // does not wait for the vector loads below).  Indices clamped instead of
-  // branched, so these loads and the argument loads they need go together.
-  const int T = a.kv_len[r];
+  // Issue order, kept by compiler barriers: the row's length and state, the
+  // raw q / k / v of this head, norm gains and RoPE entry (indices clamped
+  // instead of branched, so they go as one batch), then the first D tokens
+  // of every slot, clamped to the last cached row so that no row past the
+  // context is fetched (the new token T comes from registers).  All are
+  // vector loads, which retire in order: the stream waits for the length
+  // alone, and the exit test for the state alone.  (Scalar loads of the
+  // length would make the q loads wait for it: the compiler can only wait for
+  // all outstanding scalar loads at once.)  The exit test must not move above
+  // the stream: hoisted, it put the row's state and a second round of
+  // argument loads in front of it.
+  asm volatile("" ::: "memory");
+  const int T_raw = a.kv_len[r];
   const int act = a.active[r];
+  const float* row = a.qkv + (size_t)r * a.ldqkv;
   const int tq = min(tid, G * hd - 1), th = min(tid, hd - 1), tr = min(tid, half - 1);
   const float q_r = row[(size_t)h * G * hd + tq];
   const float kn_r = row[(size_t)a.Hq * hd + (size_t)h * hd + th];
@@ -1251,11 +1259,12 @@ __global__ __launch_bounds__(NTH) void attention_stream_kernel(AttnArgs a, int S
   const float qw_r = a.qn_w[th];
   const float kw_r = a.kn_w[th];
   const float2 cs_r = a.rope[(size_t)r * half + tr];
+  __builtin_amdgcn_sched_barrier(0);
+  const int T = __builtin_amdgcn_readfirstlane(T_raw);
+  t_last = max(min(T, a.max_ctx) - 1, 0);
   Tok ring[D];
 #pragma unroll
   for (int u = 0; u < D; ++u) load(u, ring[u]);
-  // The exit test below must not move above these loads: hoisted, it put the
-  // row's state and a second round of argument loads in front of the stream.
   asm volatile("" ::: "memory");
   if (!act) return;
   const int ctx = T + 1;
@@ -1310,37 +1319,42 @@ __global__ __launch_bounds__(NTH) void attention_stream_kernel(AttnArgs a, int S
 #pragma unroll
     for (int i = 0; i < ATT_DPL; ++i) o[g][i] = 0.f;
   }
-  for (int j0 = 0; j0 < n_iter; j0 += D) {
+  // The trip count is padded to a multiple of D, and every iteration consumes
+  // one ring entry and refills it after its last use with an unconditional
+  // load (clamped; the last round's refills are not used).  Conditional
+  // refills left the compiler unsure which loads were in flight, and it then
+  // waited for all of them before each token.  Tokens past the context are
+  // masked.
+  const int n_pad = (n_iter + D - 1) / D * D;
+  for (int j0 = 0; j0 < n_pad; j0 += D) {
 #pragma unroll
     for (int u = 0; u < D; ++u) {
       const int j = j0 + u;
-      if (j < n_iter) {                  // uniform over the workgroup
-        const int t = t0 + j * tstep;
-        float kr[ATT_DPL], vr[ATT_DPL];
-        widen(ring[u].k, kr);
-        widen(ring[u].v, vr);
-        if (j + D < n_iter) load(j + D, ring[u]);
-        if (t == T) {
+      const int t = t0 + j * tstep;
+      float kr[ATT_DPL], vr[ATT_DPL];
+      widen(ring[u].k, kr);
+      widen(ring[u].v, vr);
+      if (t == T) {
 #pragma unroll
-          for (int i = 0; i < ATT_DPL; ++i) { kr[i] = knew[dim_of(i)]; vr[i] = vnew[dim_of(i)]; }
-        }
+        for (int i = 0; i < ATT_DPL; ++i) { kr[i] = knew[dim_of(i)]; vr[i] = vnew[dim_of(i)]; }
+      }
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float dot = 0.f;
+      for (int g = 0; g < G; ++g) {
+        float dot = 0.f;
 #pragma unroll
-          for (int i = 0; i < ATT_DPL; ++i) dot = fmaf(q[g][i], kr[i], dot);
-          const float sc = group_allsum(dot, LPT) * a.scale;
-          if (t < ctx) {
-            const float mn = fmaxf(m[g], sc);
-            const float f = expf(m[g] - mn);   // 0 while the slot is empty (m = -inf)
-            const float p = expf(sc - mn);
-            l[g] = fmaf(l[g], f, p);
+        for (int i = 0; i < ATT_DPL; ++i) dot = fmaf(q[g][i], kr[i], dot);
+        const float sc = group_allsum(dot, LPT) * a.scale;
+        if (t < ctx) {
+          const float mn = fmaxf(m[g], sc);
+          const float f = expf(m[g] - mn);   // 0 while the slot is empty (m = -inf)
+          const float p = expf(sc - mn);
+          l[g] = fmaf(l[g], f, p);
 #pragma unroll
-            for (int i = 0; i < ATT_DPL; ++i) o[g][i] = fmaf(o[g][i], f, p * vr[i]);
-            m[g] = mn;
-          }
+          for (int i = 0; i < ATT_DPL; ++i) o[g][i] = fmaf(o[g][i], f, p * vr[i]);
+          m[g] = mn;
         }
       }
+      load(j + D, ring[u]);
     }
   }
   // Merge the slots of the wave (lanes with the same sub), then the waves.

@@ -40,7 +40,8 @@ replayed, and reported per launch with its bytes and HBM fraction.
 
 ``--utterances N`` (N > 1) runs the throughput batch instead: N synthetic
 utterances with CFG decoded together (decode batch 2N) at Qwen3-0.6B shape
-with BF16 weights (FP32 KV cache and accumulation); each prefix is 120-240
+with BF16 weights and a BF16 KV cache (FP32 accumulation; the reference's
+cache takes the weights' dtype, graph_frame.py:45-52); each prefix is 120-240
 tokens drawn uniformly (text ids + BOS frame + prompt frames, the prompt ~60%
 of it; the uncond row is [bos] + BOS frame + the same prompt); KV capacity
 512.  A step is one frame of every utterance; ``value`` is utterance-frames/s.
@@ -133,7 +134,7 @@ def cpu_info():
     return model, os.cpu_count() or 1, usable
 
 
-def cpu_baseline(shape, weights, items, u, *, temperature, n_frames=16, n_warm=4, unit="frames/s"):
+def cpu_baseline(shape, weights, items, u, *, temperature, n_frames=16, n_warm=4, unit="frames/s", kv_bf16=False):
     """The oracle (NumPy FP32) on the host cores over a bounded sample of the
     workload: for each (text, prompt, uncond) in ``items`` (one utterance, or a
     few of a batch), prefill untimed, then ``n_warm`` + ``n_frames`` frames,
@@ -151,7 +152,7 @@ def cpu_baseline(shape, weights, items, u, *, temperature, n_frames=16, n_warm=4
     with threadpool_limits(limits=usable):
         threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
         os_shape = Shape(**{k: getattr(shape, k) for k in Shape.__dataclass_fields__})
-        m = OracleModel(os_shape, weights, np.float32)
+        m = OracleModel(os_shape, weights, np.float32, kv_bf16=kv_bf16)
         kw = dict(min_new_frames=10**6, temperature=temperature, top_k=TOP_K, top_p=TOP_P, cfg_scale=CFG)
         times = {False: [], True: []}
         for i, (text, prompt, uncond) in enumerate(items):
@@ -205,18 +206,18 @@ def measured_traffic(key):
     return float(d["read_bytes_per_frame"]) + float(d["write_bytes_per_frame"]), d["kv_lens"]
 
 
-def roofline(shape, us, kv_mid, w_bytes, traffic_key, unit_of_work):
+def roofline(shape, us, kv_mid, w_bytes, traffic_key, unit_of_work, kv_bytes=4):
     """Roofline object: algorithmic bytes at the timed frames' average KV
     lengths over the measured frame time; measured traffic with the KV state
     it was taken at and the algorithmic bytes of that same state."""
-    alg = algorithmic_bytes(shape, kv_mid, w_bytes=w_bytes)
+    alg = algorithmic_bytes(shape, kv_mid, w_bytes=w_bytes, kv_bytes=kv_bytes)
     achieved = alg / (us * 1e-6) / 1e9
     traffic, tkv = measured_traffic(traffic_key)
     out = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "unit_of_work": unit_of_work,
            "algorithmic_bytes_per_launch": alg, "algorithmic_kv_lens_avg": [float(k) for k in kv_mid]}
     if traffic is not None:
-        alg_t = algorithmic_bytes(shape, tkv, w_bytes=w_bytes)
+        alg_t = algorithmic_bytes(shape, tkv, w_bytes=w_bytes, kv_bytes=kv_bytes)
         out.update({"traffic_source": f"profiles/{TRAFFIC_PROFILES[traffic_key]} (rocprofv3 FETCH_SIZE + "
                                       "WRITE_SIZE, copy-calibrated, bytes per launch)",
                     "traffic_kv_lens": tkv, "algorithmic_bytes_at_traffic_kv": alg_t,
@@ -260,8 +261,10 @@ def many_utterances(args):
         kv0 += [p_len, n_prompt + 2]
     u = rng.random((N_FRAMES, n * shape.n_codebooks))
     dev = torch.device("cuda:0")
+    # BF16 KV cache: the reference's StaticCache takes the weights' dtype
+    # (soraku_inference/acceleration/graph_frame.py:45-52)
     e = GraphFrameEngine(device=dev, max_cache_len=512, cfg_scale=CFG, batch=2, state_dict=weights, shape=shape,
-                         n_utts=n, bf16=True, max_frames=N_FRAMES)
+                         n_utts=n, bf16=True, kv_bf16=True, max_frames=N_FRAMES)
     del weights
     e.set_temperature(TEMP)
     e.set_sampling(sampled=True, top_k=TOP_K, top_p=TOP_P)
@@ -294,12 +297,13 @@ def many_utterances(args):
         "warmup": args.warmup, "ms_per_step": us / 1e3, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": (f"throughput batch: {n} synthetic utterances x CFG, Qwen3-0.6B shape, BF16 "
-                                "weights, FP32 KV, ragged prefixes 120-240, KV capacity 512, CFG 1.5, T 0.9, "
+                                "weights, BF16 KV (the reference's cache takes the weights' dtype), FP32 "
+                                "accumulation, ragged prefixes 120-240, KV capacity 512, CFG 1.5, T 0.9, "
                                 "top-k 50, top-p 0.95, seeded uniforms, one hipGraph per frame"),
                    "global_batch": 2 * n, "seq_len": 512, "parallelism": "none",
                    "prefill_ms": t_prefill * 1e3},
         "roofline": roofline(shape, us, kv_mid, 2, f"{n}utt_q06b_bf16",
-                             "one frame of every utterance = one hipGraph launch"),
+                             "one frame of every utterance = one hipGraph launch", kv_bytes=2),
     }
     if not args.no_cpu_baseline:
         # two of the utterances (prefill is the CPU's longest part), BF16-rounded weights as on the GPU
@@ -309,7 +313,8 @@ def many_utterances(args):
         w32 = {k: (round_bf16(v) if is_matrix(k) else v) for k, v in synthetic_weights(shape, args.seed).items()}
         q = shape.n_codebooks
         cb = cpu_baseline(shape, w32, [(t, p, un) for t, un, p in items[:2]],   # items hold (text, uncond, prompt)
-                          [u[:, i * q:(i + 1) * q] for i in range(2)], temperature=TEMP, unit="utterance-frames/s")
+                          [u[:, i * q:(i + 1) * q] for i in range(2)], temperature=TEMP, unit="utterance-frames/s",
+                          kv_bf16=True)
         cb["speedup"] = out["value"] / cb["value"]
         out["cpu_baseline"] = cb
     print(json.dumps(out))
@@ -335,7 +340,7 @@ def continuous_batch(args):
         reqs.append(dict(input_ids=torch.tensor(text[None]),
                          prompt_codes=torch.tensor(rng.integers(0, shape.codebook_size, (n_prompt, shape.n_codebooks))),
                          uncond_input_ids=torch.tensor([[TEXT_BOS]])))
-    g = FastGenerator(device=torch.device("cuda:0"), state_dict=weights, shape=shape, bf16=True)
+    g = FastGenerator(device=torch.device("cuda:0"), state_dict=weights, shape=shape, bf16=True, kv_bf16=True)
     del weights
     kw = dict(max_new_frames=N_FRAMES, min_new_frames=4, temperature=TEMP, top_k=TOP_K, top_p=TOP_P,
               cfg_scale=CFG, max_batch=n)
@@ -351,7 +356,7 @@ def continuous_batch(args):
         "metric": f"codec frames/sec over {R} requests through {n} CFG slots (continuous batching), 1 MI355X",
         "value": frames / dt, "unit": "utterance-frames/s", "n_gpus": 1, "higher_is_better": True,
         "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": (f"{R} synthetic requests x CFG, Qwen3-0.6B shape, BF16 weights, FP32 KV, ragged "
+        "config": {"workload": (f"{R} synthetic requests x CFG, Qwen3-0.6B shape, BF16 weights, BF16 KV, ragged "
                                 f"prefixes 120-240, up to {N_FRAMES} frames each, CFG 1.5, T 0.9, top-k 50, "
                                 "top-p 0.95; a retired slot is refilled between frames"),
                    "slots": n, "requests": R, "frames_decoded": frames, "stopped_at_eos": stops,

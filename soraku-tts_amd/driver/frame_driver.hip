@@ -16,6 +16,7 @@
 //                         rows' KV lengths jump to C / U
 //     --kv-mid M          --utts: after the prefill, every row's KV length jumps
 //                         to its drawn prefix length + M
+//     --kv-bf16           BF16 KV cache (default FP32)
 //   sk_frame_driver --copy MiB   (only a device copy of MiB MiB, 4 times: the
 //                                 reference for HBM byte counters)
 //
@@ -99,7 +100,7 @@ static uint32_t rnd() {
 
 static int usage() {
   fprintf(stderr, "usage: sk_frame_driver [--model q06b|q17b] [--utts N] [--prefix T P] [--kv C U] "
-                  "[--kv-mid M] [frames] [warmup]\n       sk_frame_driver --copy MiB\n");
+                  "[--kv-mid M] [--kv-bf16] [frames] [warmup]\n       sk_frame_driver --copy MiB\n");
   return 2;
 }
 
@@ -107,6 +108,7 @@ int main(int argc, char** argv) {
   if (argc > 2 && std::string(argv[1]) == "--copy") return copy_probe(atoi(argv[2]));
   bool big = false;
   int utts = 1, p_text = -1, p_prompt = -1, kv_c = -1, kv_u = -1, kv_mid = -1;
+  bool kv_bf16 = false;
   std::vector<int> pos;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
@@ -116,6 +118,7 @@ int main(int argc, char** argv) {
     else if (a == "--prefix" && need(2)) { p_text = atoi(argv[i + 1]); p_prompt = atoi(argv[i + 2]); i += 2; }
     else if (a == "--kv" && need(2)) { kv_c = atoi(argv[i + 1]); kv_u = atoi(argv[i + 2]); i += 2; }
     else if (a == "--kv-mid" && need(1)) { kv_mid = atoi(argv[++i]); }
+    else if (a == "--kv-bf16") { kv_bf16 = true; }
     else if (!a.empty() && a[0] != '-') { pos.push_back(atoi(argv[i])); }
     else return usage();
   }
@@ -133,7 +136,7 @@ int main(int argc, char** argv) {
   c.trunk_inter = big ? 6144 : 3072; c.depth_inner = 2 * c.d_model; c.n_codebooks = 16; c.audio_vocab = 2051;
   c.text_vocab = 151936; c.bos_id = 2048; c.eos_id = 2049; c.pad_id = 2050;
   c.trunk_eps = 1e-6f; c.depth_eps = 1.1920929e-07f; c.rope_theta = 1e6f; c.frame_scale = 0.25f;
-  c.weight_dtype = (big || wide) ? SK_BF16 : SK_F32; c.kv_dtype = SK_F32;
+  c.weight_dtype = (big || wide) ? SK_BF16 : SK_F32; c.kv_dtype = kv_bf16 ? SK_BF16 : SK_F32;
   c.n_utts = utts; c.cfg_rows = 2;
   c.max_ctx = wide ? 512 : def_text + 1 + def_prompt + max_frames + 8;
   c.max_frames = max_frames; c.n_language = 0;
@@ -192,7 +195,7 @@ int main(int argc, char** argv) {
     for (int kv = 0; kv < 2; ++kv) {
       void* p = nullptr;
       SKCHECK(sk_kv_ptr(e, l, kv, &p));
-      HIPCHECK(hipMemset(p, 0, (size_t)2 * utts * c.n_kv_heads * c.max_ctx * c.head_dim * sizeof(float)));
+      HIPCHECK(hipMemset(p, 0, (size_t)2 * utts * c.n_kv_heads * c.max_ctx * c.head_dim * (kv_bf16 ? 2 : 4)));
     }
 
   // ---- prefixes: cond = text ids + BOS frame + prompt frames; uncond = one text id + the same frames

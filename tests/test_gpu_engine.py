@@ -503,10 +503,13 @@ def test_batched_prefill_matches_oracle(hip_device, kv_bf16):
     assert worst < (1e-2 if kv_bf16 else 1e-3)
 
 
-def _many_utterance_case(s, w, n_utts, seed, hip_device, bf16=False, frames=2, max_len=64, text_len=(5, 30)):
+def _many_utterance_case(s, w, n_utts, seed, hip_device, bf16=False, frames=2, max_len=64, text_len=(5, 30),
+                         kv_bf16=False):
     """n_utts utterances with ragged prefixes, teacher-forced for `frames`
     frames through one engine; per utterance, the engine's masked merged
-    logits and the oracle's for the same prefix and codes."""
+    logits and the oracle's for the same prefix and codes.  With kv_bf16 the
+    engine and the oracle keep BF16 caches, and the result is the pair
+    (engine vs FP64 oracle, FP32 oracle vs FP64 oracle)."""
     from soraku_amd import GraphFrameEngine
 
     rng = np.random.default_rng(seed)
@@ -519,7 +522,7 @@ def _many_utterance_case(s, w, n_utts, seed, hip_device, bf16=False, frames=2, m
     codes = np.stack(codes)                       # [utts, frames, Q]
     cfg = 1.5
     e = GraphFrameEngine(device=hip_device, max_cache_len=max_len, cfg_scale=cfg, batch=2, state_dict=w,
-                         shape=_shape(s), n_utts=n_utts, bf16=bf16)
+                         shape=_shape(s), n_utts=n_utts, bf16=bf16, kv_bf16=kv_bf16)
     e.set_temperature(0.0)
     e.set_debug(True)
     e.prefill_utterances(items)
@@ -531,12 +534,16 @@ def _many_utterance_case(s, w, n_utts, seed, hip_device, bf16=False, frames=2, m
         got.append(lg)
     e.close()
     got = np.stack(got, axis=1)                   # [utts, frames, Q, V]
-    worst = 0.0
-    m = OracleModel(s, w, np.float64)
+    worst = spread = 0.0
+    m = OracleModel(s, w, np.float64, kv_bf16=kv_bf16)
+    m32 = OracleModel(s, w, np.float32, kv_bf16=True) if kv_bf16 else None
     for u, (text, uncond, prompt) in enumerate(items):
         ref = _oracle_forced_logits(m, s, text, prompt, uncond, codes[u], cfg)
         worst = max(worst, _rowwise_rel(got[u].reshape(-1, got.shape[-1]), ref))
-    return worst
+        if kv_bf16:
+            ref32 = _oracle_forced_logits(m32, s, text, prompt, uncond, codes[u], cfg)
+            spread = max(spread, _rowwise_rel(ref32, ref))
+    return (worst, spread) if kv_bf16 else worst
 
 
 def test_many_utterances_tiny(hip_device):
@@ -564,6 +571,19 @@ def test_many_utterances_tiny_bf16_ten_rows(hip_device):
     assert rel < LOGIT_TOL
 
 
+def test_many_utterances_tiny_bf16_kv(hip_device):
+    """Ten decode rows with BF16 weights and a BF16 KV cache at the tiny
+    shape (head_dim 16: the streaming attention's slots are single lanes and
+    merge over every lane distance); held to max(1e-3, 2 x the oracle's
+    FP32-vs-FP64 spread with the same BF16 cache)."""
+    from oracle.model import TINY
+
+    w = _device_weights(TINY, 43, hip_device)
+    rel, spread = _many_utterance_case(TINY, w, 5, 9, hip_device, bf16=True, frames=3, kv_bf16=True)
+    print(f"tiny BF16 weights + BF16 KV, 5 utterances: engine {rel:.3e}, oracle FP32 vs FP64 {spread:.3e}")
+    assert rel < max(LOGIT_TOL, 2 * spread)
+
+
 def test_sixteen_utterances_q06b_bf16(hip_device):
     """Batch-32 decode (16 utterances x CFG) at the Qwen3-0.6B shape with BF16
     weights (FP32 accumulation), ragged prefixes: every utterance against the
@@ -577,6 +597,23 @@ def test_sixteen_utterances_q06b_bf16(hip_device):
     rel = _many_utterance_case(s, w, 16, 5, hip_device, bf16=True, frames=2)
     print(f"q06b BF16, 16 utterances: max row-relative logit error {rel:.3e}")
     assert rel < LOGIT_TOL
+
+
+def test_sixteen_utterances_q06b_bf16_kv(hip_device):
+    """The throughput batch's precision: 16 utterances x CFG at the
+    Qwen3-0.6B shape with BF16 weights and a BF16 KV cache (the streaming
+    attention reads BF16 K/V).  Rounding K/V to BF16 is discontinuous, so the
+    logits are held, as for the 1.7B shape, to max(1e-3, 2 x the oracle's own
+    FP32-vs-FP64 spread with the same BF16 cache)."""
+    import dataclasses
+
+    from oracle.model import QWEN3_06B
+
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)
+    w = _device_weights(s, 17, hip_device)
+    rel, spread = _many_utterance_case(s, w, 16, 5, hip_device, bf16=True, frames=2, kv_bf16=True)
+    print(f"q06b BF16 weights + BF16 KV, 16 utterances: engine {rel:.3e}, oracle FP32 vs FP64 {spread:.3e}")
+    assert rel < max(LOGIT_TOL, 2 * spread)
 
 
 def test_generate_batch_per_utterance_equals_oracle(hip_device):

@@ -17,6 +17,8 @@
 //     --kv-mid M          --utts: after the prefill, every row's KV length jumps
 //                         to its drawn prefix length + M
 //     --kv-bf16           BF16 KV cache (default FP32)
+//     --max-ctx N         KV capacity per row (default: the prefix and the
+//                         frames exactly, or 512 with --utts)
 //   sk_frame_driver --copy MiB   (only a device copy of MiB MiB, 4 times: the
 //                                 reference for HBM byte counters)
 //
@@ -100,7 +102,7 @@ static uint32_t rnd() {
 
 static int usage() {
   fprintf(stderr, "usage: sk_frame_driver [--model q06b|q17b] [--utts N] [--prefix T P] [--kv C U] "
-                  "[--kv-mid M] [--kv-bf16] [frames] [warmup]\n       sk_frame_driver --copy MiB\n");
+                  "[--kv-mid M] [--kv-bf16] [--max-ctx N] [frames] [warmup]\n       sk_frame_driver --copy MiB\n");
   return 2;
 }
 
@@ -109,6 +111,7 @@ int main(int argc, char** argv) {
   bool big = false;
   int utts = 1, p_text = -1, p_prompt = -1, kv_c = -1, kv_u = -1, kv_mid = -1;
   bool kv_bf16 = false;
+  int max_ctx = -1;
   std::vector<int> pos;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
@@ -119,6 +122,7 @@ int main(int argc, char** argv) {
     else if (a == "--kv" && need(2)) { kv_c = atoi(argv[i + 1]); kv_u = atoi(argv[i + 2]); i += 2; }
     else if (a == "--kv-mid" && need(1)) { kv_mid = atoi(argv[++i]); }
     else if (a == "--kv-bf16") { kv_bf16 = true; }
+    else if (a == "--max-ctx" && need(1)) { max_ctx = atoi(argv[++i]); }
     else if (!a.empty() && a[0] != '-') { pos.push_back(atoi(argv[i])); }
     else return usage();
   }
@@ -138,7 +142,7 @@ int main(int argc, char** argv) {
   c.trunk_eps = 1e-6f; c.depth_eps = 1.1920929e-07f; c.rope_theta = 1e6f; c.frame_scale = 0.25f;
   c.weight_dtype = (big || wide) ? SK_BF16 : SK_F32; c.kv_dtype = kv_bf16 ? SK_BF16 : SK_F32;
   c.n_utts = utts; c.cfg_rows = 2;
-  c.max_ctx = wide ? 512 : def_text + 1 + def_prompt + max_frames + 8;
+  c.max_ctx = max_ctx > 0 ? max_ctx : wide ? 512 : def_text + 1 + def_prompt + max_frames + 8;
   c.max_frames = max_frames; c.n_language = 0;
   for (int i = 0; i < 4; ++i) c.language_ids[i] = -1;
   sk_engine* e = nullptr;

@@ -5,6 +5,9 @@
         (dispatches after the last prefill kernel, frames delimited by the
         trunk's ``final_norm_kernel``)
 
+    python -m soraku_amd.prof_summary prefill OUT/tr_results.db
+        per-kernel table of the first batched prefill in the same run
+
     python -m soraku_amd.prof_summary counters FRAME_FETCH FRAME_WRITE COPY_FETCH COPY_WRITE MIB [KV ...]
         HBM bytes per frame from two ``--pmc`` runs (FETCH_SIZE, then
         WRITE_SIZE; ``*_counter_collection.csv`` under each directory) and the
@@ -79,6 +82,26 @@ def trace(db: str) -> str:
     return "\n".join(out)
 
 
+def prefill(db: str) -> str:
+    """Per-kernel table of the first batched prefill in a ``--kernel-trace`` run
+    (``pf_rope_table_kernel`` through ``pf_finish_kernel``)."""
+    con = sqlite3.connect(db)
+    rows = con.execute("select name, start, end from kernels order by start").fetchall()
+    names = [short_name(r[0]) for r in rows]
+    a = next(i for i, n in enumerate(names) if "pf_rope_table_kernel" in n)
+    b = next(i for i, n in enumerate(names) if i > a and "pf_finish_kernel" in n)
+    agg = collections.OrderedDict()
+    for i in range(a, b + 1):
+        s = agg.setdefault(names[i], [0, 0.0])
+        s[0] += 1
+        s[1] += (rows[i][2] - rows[i][1]) / 1e3
+    out = [f"prefill span {(rows[b][2] - rows[a][1]) / 1e3:.0f} us, kernels {sum(v[1] for v in agg.values()):.0f} us",
+           f"{'kernel':48s} {'calls':>6s} {'avg us':>8s} {'total us':>9s}"]
+    for k, (c, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"{k[:48]:48s} {c:6d} {t / c:8.1f} {t:9.1f}")
+    return "\n".join(out)
+
+
 def _csv(d: str):
     path = glob.glob(os.path.join(d, "*counter_collection.csv"))
     if len(path) != 1:
@@ -138,6 +161,8 @@ def counters(fetch: str, write: str, cfetch: str, cwrite: str, mib: int, kv) -> 
 def main(argv):
     if len(argv) >= 2 and argv[0] == "trace":
         print(trace(argv[1]))
+    elif len(argv) >= 2 and argv[0] == "prefill":
+        print(prefill(argv[1]))
     elif len(argv) >= 6 and argv[0] == "counters":
         print(counters(*argv[1:5], int(argv[5]), [int(k) for k in argv[6:]]))
     else:

@@ -149,7 +149,12 @@ int sk_set_sampling(sk_engine* e, float cfg_scale, float temperature, int32_t to
 int sk_set_debug(sk_engine* e, int32_t record_logits);
 
 /* Capture one whole frame (16 depth steps + sampling + frame embedding +
- * trunk step) as one hipGraph. */
+ * trunk step) as one hipGraph.  With one utterance with CFG at the
+ * Qwen3-0.6B shape with FP32 weights or the Qwen3-1.7B shape with BF16
+ * weights, capture also derives the depth steps' code tables from the bound
+ * codebook table, depth norm_in gain and gate/up weights
+ * ((Q-1) x V x 2 x depth_inner floats: 0.5 GB / 1.0 GB); those weights must
+ * not change afterwards. */
 int sk_capture(sk_engine* e);
 
 /* Replay one frame.  mask_eos_q0: bit u masks EOS at codebook 0 for

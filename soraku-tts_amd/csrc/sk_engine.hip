@@ -168,6 +168,13 @@ struct sk_engine {
   int grid_chunks = 0;
   int row_chunks[4] = {0, 0, 0, 0};
 
+  // One utterance's depth steps by code tables (depth_step_kernel): the
+  // tables P_j[c] = W_gu (norm_in gain * table[j][c]) for j < Q-1, built when
+  // the frame is captured, and the ping-pong G buffers [rows][2 * depth_inner].
+  bool code_tables = false;
+  float* ptab = nullptr;
+  float* gbuf[2] = {nullptr, nullptr};
+
   // batched prefill activations, sized for the largest packed prefix so far
   int pf_cap = 0;
   void* pf_mem = nullptr;
@@ -570,6 +577,8 @@ hipError_t enqueue_depth_wide(sk_engine* e, int q) {
   return launch_skinny<EPI_BIAS, true>(e, k);
 }
 
+hipError_t enqueue_tail(sk_engine* e);
+
 hipError_t enqueue_frame(sk_engine* e) {
   const sk_config& c = e->c;
   const int d = c.d_model, M = e->rows, V = c.audio_vocab;
@@ -594,6 +603,38 @@ hipError_t enqueue_frame(sk_engine* e) {
   if (e->wide) {
     s.hidden = e->hidden; s.w_in = e->d_norm_in; s.eps_in = c.depth_eps;
     s.abuf = e->abuf; s.xs_abuf = e->xs_abuf;
+  }
+  // One utterance with code tables: per codebook one depth_step_kernel launch
+  // (codebook q-1's sampler, the prefix, SwiGLU, down projection and the next
+  // step's G) and the classifier; codebook 0 takes G_1, then SwiGLU + down.
+  if (e->code_tables) {
+    DepthArgs g{};
+    g.w_gate = e->d_gate; g.w_up = e->d_up; g.w_down = e->d_down; g.hidden = e->hidden;
+    g.norm_w = e->d_norm_in; g.eps = c.depth_eps; g.ptab = e->ptab; g.y = e->ybuf; g.scale = c.frame_scale;
+    for (int q = 0; q < c.n_codebooks; ++q) {
+      if (q == 0) {
+        g.g_out = e->gbuf[0];
+        if ((err = launch_depth_step<0>(wt, d, s, g, 0, e->stream)) != hipSuccess) return err;
+        g.g_in = e->gbuf[0];
+        if ((err = launch_depth_step<1>(wt, d, s, g, 0, e->stream)) != hipSuccess) return err;
+      } else {
+        g.prefix_in = (q % 2 == 1) ? e->prefix : e->prefix2;
+        g.prefix_out = (q % 2 == 1) ? e->prefix2 : e->prefix;
+        g.g_in = e->gbuf[(q - 1) % 2];
+        g.g_out = e->gbuf[q % 2];
+        err = (q + 1 < c.n_codebooks) ? launch_depth_step<2>(wt, d, s, g, q, e->stream)
+                                      : launch_depth_step<3>(wt, d, s, g, q, e->stream);
+        if (err != hipSuccess) return err;
+      }
+      const void* tq = static_cast<const char*>(e->out_proj ? e->out_proj : e->table) + (size_t)q * V * d * tsz;
+      GemvArgs a = gemv_args(tq, V, d, e->ybuf, d, e->logits, V);
+      a.norm_w = e->d_norm_out; a.eps = c.depth_eps; a.bias = e->d_bias + (size_t)q * V;
+      if ((err = launch_gemv<PRO_NORM, EPI_BIAS>(wt, M, a, e->stream)) != hipSuccess) return err;
+    }
+    err = (wt == SK_BF16) ? launch_sample_step<WBF16>(s, c.n_codebooks - 1, 1, e->stream)
+                          : launch_sample_step<WF32>(s, c.n_codebooks - 1, 1, e->stream);
+    if (err != hipSuccess) return err;
+    return enqueue_tail(e);
   }
   // One utterance: codebook q-1's sampler runs inside codebook q's gate/up
   // launch (depth_sample_gemv_kernel); only the last codebook's has its own.
@@ -643,6 +684,14 @@ hipError_t enqueue_frame(sk_engine* e) {
                           : launch_sample_step<WF32>(s, q, c.n_utts, e->stream);
     if (err != hipSuccess) return err;
   }
+  return enqueue_tail(e);
+}
+
+// The frame's trunk step and final norm (after its depth steps).
+hipError_t enqueue_tail(sk_engine* e) {
+  const sk_config& c = e->c;
+  const int d = c.d_model, M = e->rows;
+  hipError_t err;
   if ((err = enqueue_trunk(e)) != hipSuccess) return err;
   hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x, e->final_norm,
                      c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->fc, e->u_ring,
@@ -650,6 +699,50 @@ hipError_t enqueue_frame(sk_engine* e) {
                      e->inv_freq, c.head_dim / 2, e->rope, (const float2*)e->p_rope, c.max_ctx + 1,
                      e->d_norm_in, c.depth_eps, e->wide ? e->abuf : nullptr, e->xs_abuf);
   return hipGetLastError();
+}
+
+// Code tables of the depth steps (depth_step_kernel): P_j = (table[j] * norm_in
+// gain) W_gu^T for j < Q-1, [V][gate | up] per codebook, on the FP32 matrix
+// cores (BF16 weights widened exactly); derived from the weights bound when the
+// frame is captured.
+template <typename TL>
+hipError_t build_code_tables_t(sk_engine* e, float* tmp) {
+  const sk_config& c = e->c;
+  const int d = c.d_model, KI = c.depth_inner, V = c.audio_vocab;
+  const size_t tsz = sizeof(typename TL::elem);
+  for (int j = 0; j + 1 < c.n_codebooks; ++j) {
+    const void* tj = static_cast<const char*>(e->table) + (size_t)j * V * d * tsz;
+    hipLaunchKernelGGL(scale_rows_kernel<TL>, dim3(1024), dim3(256), 0, e->stream, tj, e->d_norm_in, V, d, tmp);
+    GemmArgs g{};
+    g.A = tmp; g.lda = d;
+    g.B[0] = e->d_gate; g.B[1] = e->d_up; g.B[2] = nullptr;
+    g.seg_rows[0] = KI; g.seg_rows[1] = KI; g.seg_rows[2] = 0;
+    g.out = e->ptab + (size_t)j * V * 2 * KI; g.ldo = 2 * KI;
+    g.M = V; g.N = 2 * KI; g.K = d;
+    hipLaunchKernelGGL((gemm_nt_kernel<GEPI_STORE, TL, 64>), dim3((2 * KI + GBN - 1) / GBN, (V + 63) / 64), dim3(256),
+                       0, e->stream, g);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+int build_code_tables(sk_engine* e) {
+  const sk_config& c = e->c;
+  const size_t KI = c.depth_inner, V = c.audio_vocab, d = c.d_model;
+  if (!e->ptab) {
+    SK_HIP(dalloc(&e->ptab, (size_t)(c.n_codebooks - 1) * V * 2 * KI));
+    SK_HIP(dalloc(&e->gbuf[0], (size_t)e->rows * 2 * KI));
+    SK_HIP(dalloc(&e->gbuf[1], (size_t)e->rows * 2 * KI));
+  }
+  float* tmp = nullptr;
+  SK_HIP(dalloc(&tmp, V * d));
+  const hipError_t err = c.weight_dtype == SK_BF16 ? build_code_tables_t<WBF16>(e, tmp)
+                                                   : build_code_tables_t<WF32>(e, tmp);
+  const hipError_t serr = hipStreamSynchronize(e->stream);
+  hipFree(tmp);
+  SK_HIP(err);
+  SK_HIP(serr);
+  return SK_OK;
 }
 
 // ---- batched prefill -------------------------------------------------------
@@ -961,7 +1054,7 @@ int sk_destroy(sk_engine* e) {
   void* bufs[] = {e->sk_partial, e->sk_arrive, e->xs_x, e->xs_attn, e->xs_act, e->xs_abuf, e->xs_y, e->ss_x, e->ss_y, e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
                   e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->flag_ring, e->u_ring,
-                  e->pf_mem,
+                  e->pf_mem, e->ptab, e->gbuf[0], e->gbuf[1],
                   e->p_row_start, e->p_rope,
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
   for (void* p : bufs)
@@ -1234,6 +1327,9 @@ int sk_capture(sk_engine* e) {
   if (rc != SK_OK) return rc;
   if (e->exec) return SK_OK;
   SK_HIP(hipStreamSynchronize(e->stream));
+  e->code_tables = !e->wide && e->c.n_utts == 1 &&
+                   code_tables_fit(e->c.d_model, e->rows, e->c.depth_inner, e->c.audio_vocab, e->c.weight_dtype);
+  if (e->code_tables && (rc = build_code_tables(e)) != SK_OK) return rc;
   rc = capture(e, enqueue_frame, &e->graph, &e->exec);
   if (rc != SK_OK) return rc;
   const hipError_t fe = find_attn_nodes(e);

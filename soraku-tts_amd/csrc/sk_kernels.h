@@ -1895,16 +1895,35 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
 // are clamped into the row and entries past V become -inf afterwards, so no
 // load sits behind a branch.
 template <int VPT>
-__device__ __forceinline__ void merge_mask(const float* lc, const float* lu, float s, int V, int bos, int eos,
-                                           int pad, const int* mask_flag, int mask_bit, bool force_mask, float temp,
-                                           float* dbg, float (&xr)[VPT]) {
-  float cvv[VPT], uvv[VPT];
+__device__ __forceinline__ void load_logits(const float* lc, const float* lu, int V, float (&cvv)[VPT],
+                                            float (&uvv)[VPT]) {
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int v = min((int)threadIdx.x + i * SNT, V - 1);
     cvv[i] = lc[v];
     uvv[i] = lu ? lu[v] : 0.f;
   }
+}
+template <int VPT>
+__device__ __forceinline__ void merge_mask_loaded(const float (&cvv)[VPT], const float (&uvv)[VPT], bool lu, float s,
+                                                  int V, int bos, int eos, int pad, const int* mask_flag,
+                                                  int mask_bit, bool force_mask, float temp, float* dbg,
+                                                  float (&xr)[VPT]);
+template <int VPT>
+__device__ __forceinline__ void merge_mask(const float* lc, const float* lu, float s, int V, int bos, int eos,
+                                           int pad, const int* mask_flag, int mask_bit, bool force_mask, float temp,
+                                           float* dbg, float (&xr)[VPT]) {
+  float cvv[VPT], uvv[VPT];
+  load_logits<VPT>(lc, lu, V, cvv, uvv);
+  merge_mask_loaded<VPT>(cvv, uvv, lu != nullptr, s, V, bos, eos, pad, mask_flag, mask_bit, force_mask, temp, dbg,
+                         xr);
+}
+// The CFG merge and masks of loaded logits (see merge_mask).
+template <int VPT>
+__device__ __forceinline__ void merge_mask_loaded(const float (&cvv)[VPT], const float (&uvv)[VPT], bool lu, float s,
+                                                  int V, int bos, int eos, int pad, const int* mask_flag,
+                                                  int mask_bit, bool force_mask, float temp, float* dbg,
+                                                  float (&xr)[VPT]) {
   const bool mask_eos = force_mask || (mask_flag && ((*mask_flag >> mask_bit) & 1));
   const bool divide = temp > 0.f;
   // Chunks below the lowest special id need no mask compares (uniform test).
@@ -2255,6 +2274,391 @@ __global__ __launch_bounds__(SNT) void depth_sample_gemv_kernel(SampleArgs a, Ge
       g.out[(size_t)lane * g.ldo + n] = gt / (1.0f + expf(-gt)) * up;
     }
   }
+}
+
+// Totals of N words over the 64 lanes of a wave (N = 4, 8 or 16): lane l
+// returns the total of word l / (64 / N).  Halving steps: each exchange keeps
+// one word of a pair in each half of the lanes it pairs (permlane32 / 16
+// swaps for lane bits 5 and 4, DPP row mirror and half mirror for bits 3 and
+// 2), so N words cost about N adds instead of N full reductions; then the
+// lanes left holding one word sum within their group.  Every step adds a pair
+// of lanes' values in both lanes, so all lanes of a group get the same bits.
+template <int N>
+__device__ __forceinline__ float wave_reduce_words(float (&w)[N], int lane) {
+  static_assert(N == 4 || N == 8 || N == 16, "wave_reduce_words: N");
+  float v[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {          // lane bit 5
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(w[i]), __float_as_uint(w[i + N / 2]), false,
+                                                   false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  float t[N / 4];
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) {          // lane bit 4
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + N / 4]), false,
+                                                   false);
+    t[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  float x;
+  if constexpr (N == 4) {
+    x = t[0];
+    x += dpp_keep<0x140, 0xf>(x);            // row mirror: lane i <-> 15 - i
+  } else {
+    const bool b3 = (lane >> 3) & 1;         // lane bit 3: row mirror pairs it
+    float c[N / 8];
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+      const float a0 = t[i] + dpp_keep<0x140, 0xf>(t[i]);
+      const float a1 = t[i + N / 8] + dpp_keep<0x140, 0xf>(t[i + N / 8]);
+      c[i] = b3 ? a1 : a0;
+    }
+    if constexpr (N == 8) {
+      x = c[0];
+    } else {                                 // lane bit 2: half mirror pairs it
+      const bool b2 = (lane >> 2) & 1;
+      const float a0 = c[0] + dpp_keep<0x141, 0xf>(c[0]);
+      const float a1 = c[1] + dpp_keep<0x141, 0xf>(c[1]);
+      x = b2 ? a1 : a0;
+    }
+  }
+  if constexpr (N <= 8) x += dpp_keep<0x141, 0xf>(x);   // half mirror: lane i <-> 7 - i
+  x += dpp_keep<0x4e, 0xf>(x);               // quad_perm [2,3,0,1]
+  x += dpp_keep<0xb1, 0xf>(x);               // quad_perm [1,0,3,2]
+  return x;
+}
+
+// ------------------------------------------------------------ depth step (code tables)
+// One utterance's depth step with the SwiGLU input taken apart by linearity.
+// The gate/up input of codebook q is a_q = w_in * x_q * r_q, with x_q = hidden +
+// prefix_q, r_q = 1 / rms(x_q), and x_q = x_{q-1} + scale * table[q-1][c] once
+// code c of codebook q-1 is drawn.  So
+//
+//   W_gu a_q = r_q * (G_q + scale * P_{q-1}[c]),   G_q = W_gu (w_in * x_{q-1}),
+//                                                  P_j[c] = W_gu (w_in * table[j][c]),
+//
+// where G_q is computed by the previous step (it does not depend on c) and
+// P_j is a weight-only table of every code's contribution, built when the
+// frame is captured.  Once c is known every workgroup forms the whole SwiGLU
+// output elementwise, so codebook q-1's sampler, the prefix advance, the
+// SwiGLU, the down projection with its residual (y_q = a_q + W_d act_q,
+// model.py:163-170) and the next step's G_{q+1} fit one launch, and the
+// classifier follows.  Launches per codebook: two instead of three.
+//
+// Work of one launch (256 workgroups of SNT threads): each wave owns RWG gate
+// rows and the same RWG up rows of W_gu (whole rows, K = KD) for G_{q+1}, and
+// for the down projection the workgroup owns RD = KD / 256 output rows while
+// its 8 waves split the inner dimension KI into 8 chunks of 64 * VEC (one
+// 16-byte weight load per lane and row).  Every weight load is issued before
+// the sampler runs.
+//   MODE 0: G_1 = W_gu (w_in * hidden) only (x_0 = hidden; no sampler).
+//   MODE 1: codebook 0's SwiGLU + down: act_0 = SwiGLU(r_0 G_1), y_0.
+//   MODE 2: codebooks 1 .. Q-2: sampler of q-1, prefix, act_q, y_q, G_{q+1}.
+//   MODE 3: codebook Q-1: as MODE 2 without G_{q+1}.
+struct DepthArgs {
+  const void* w_gate; const void* w_up;    // [KI][KD]
+  const void* w_down;                      // [KD][KI]
+  const float* hidden;                     // [M][KD]
+  const float* prefix_in; float* prefix_out;   // [M][KD] before / after code q-1 (MODE 2, 3)
+  const float* norm_w; float eps;          // norm_in gain [KD], FLT_EPSILON
+  const float* g_in;                       // [M][2 KI] G_q (gate | up), MODE 1-3
+  float* g_out;                            // [M][2 KI] G_{q+1}, MODE 0 and 2
+  const float* ptab;                       // [Q-1][V][2 KI] code tables, MODE 2 and 3
+  float* y;                                // [M][KD] depth MLP output, MODE 1-3
+  float scale;                             // frame scale 1/sqrt(Q)
+};
+constexpr int DEPTH_WGS = 256;
+
+template <typename TL, int VPT, int M, int KD, int KI, int MODE>
+__global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs g, int q) {
+  extern __shared__ unsigned char raw[];
+  double* W = reinterpret_cast<double*>(raw);
+  unsigned long long* ck = reinterpret_cast<unsigned long long*>(W + a.V);
+  unsigned long long* sk = ck + pow2_ceil(a.V);
+  constexpr bool SAMPLE = MODE >= 2, GPART = MODE == 0 || MODE == 2, DPART = MODE >= 1;
+  constexpr int VEC = TL::VEC;
+  constexpr int NV = KD / (64 * VEC);           // 16-byte loads per lane of one W_gu row
+  constexpr int DPT = KD / SNT;                 // elements of x per thread
+  constexpr int RWG = KI / (DEPTH_WGS * SWAVES);
+  constexpr int RD = KD / DEPTH_WGS;
+  static_assert(KD % (64 * VEC) == 0 && KD % SNT == 0 && KD % DEPTH_WGS == 0 && M <= 2, "depth_step shape");
+  static_assert(RWG >= 1 && RWG * DEPTH_WGS * SWAVES == KI && KI == SWAVES * 64 * VEC, "depth_step inner");
+  __shared__ SampleSmem s;
+  __shared__ __attribute__((aligned(16))) float xsh[M * KD];
+  __shared__ __attribute__((aligned(16))) float gsh[KD];
+  __shared__ float red[M][SWAVES];
+  __shared__ float dsum[SWAVES][RD][M];
+  __shared__ int code_sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qs = q - 1;                         // the codebook sampled here (MODE 2, 3)
+  const bool lead = blockIdx.x == 0;
+
+  // Loads that do not depend on the code, before the weight stream: the
+  // logits first (the sampler waits for them), then the draw's inputs, the
+  // hidden rows, the prefix and the norm gain.
+  float xr[VPT], cvv[VPT], uvv[VPT];
+  if constexpr (SAMPLE) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int v = min(tid + i * SNT, a.V - 1);
+      cvv[i] = a.logits[v];
+      uvv[i] = M == 2 ? a.logits[a.ldl + v] : 0.f;
+    }
+  }
+  double u = 0.0;
+  int forced = 0, slot = 0, mflag = 0;
+  int64_t fcode = 0;
+  SkParams P{};
+  if constexpr (SAMPLE) {
+    u = a.u_cur[qs];
+    mflag = a.flag_cur[0];
+    forced = a.flag_cur[1];
+    P = *a.params;
+  }
+  float hv[M][DPT], pv[M][DPT], gv[DPT];
+#pragma unroll
+  for (int i = 0; i < DPT; ++i) {
+    const int k = tid + i * SNT;
+    gv[i] = g.norm_w[k];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      hv[m][i] = g.hidden[(size_t)m * KD + k];
+      pv[m][i] = SAMPLE ? g.prefix_in[(size_t)m * KD + k] : 0.f;
+    }
+  }
+  // G_q at this lane's inner indices of its wave's chunk (gate and up): at
+  // entry without a sampler, else with the code's table entries after it
+  // (they are needed only then, and they do not hold registers through it).
+  const int kc = (wave * 64 + lane) * VEC;
+  float gq[M][2][VEC];
+  auto load_gq = [&]() {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < VEC; i += 4) {
+          const float4 t = *reinterpret_cast<const float4*>(g.g_in + (size_t)m * 2 * KI + h * KI + kc + i);
+          gq[m][h][i] = t.x; gq[m][h][i + 1] = t.y; gq[m][h][i + 2] = t.z; gq[m][h][i + 3] = t.w;
+        }
+  };
+  if constexpr (MODE == 1) load_gq();
+  // Weights: this wave's gate / up rows, this workgroup's down rows at the
+  // chunk -- issued behind the logits and before any of them is used (the
+  // scheduling barrier below keeps them there: sunk under the CFG merge they
+  // started only once the logits had arrived).
+  const int n0 = (blockIdx.x * SWAVES + wave) * RWG;
+  uint4 wgu[GPART ? RWG : 1][2][NV];
+  if constexpr (GPART) {
+#pragma unroll
+    for (int r = 0; r < RWG; ++r)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const size_t off = (size_t)(n0 + r) * KD + (size_t)(j * 64 + lane) * VEC;
+        wgu[r][0][j] = TL::raw(g.w_gate, off);
+        wgu[r][1][j] = TL::raw(g.w_up, off);
+      }
+  }
+  const int row0 = blockIdx.x * RD;
+  uint4 wd[DPART ? RD : 1];
+  if constexpr (DPART) {
+#pragma unroll
+    for (int i = 0; i < RD; ++i) wd[i] = TL::raw(g.w_down, (size_t)(row0 + i) * KI + kc);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // The ring slot and the forced code as scalar loads behind the weights: a
+  // vector load here would be waited for behind the whole weight stream, and
+  // ahead of the weights its address chain held them back.
+  if constexpr (SAMPLE) {
+    slot = *a.fc;
+    fcode = a.forced_ring[(size_t)slot * a.Q + qs];
+  }
+  if constexpr (SAMPLE) {
+    const bool q0 = (qs == 0) && P.has_q0;
+    merge_mask_loaded<VPT>(cvv, uvv, M == 2, P.cfg_scale, a.V, a.bos, a.eos, a.pad, &mflag, 0, qs != 0,
+                           q0 ? P.temperature_q0 : P.temperature,
+                           (lead && P.record_logits) ? a.dbg + (size_t)qs * a.V : nullptr, xr);
+  }
+
+  // The code of codebook q-1 (every workgroup draws the same one), then its
+  // table row and its code-table entries at this lane's chunk.
+  int code = 0;
+  float tv[DPT], pr[2][VEC];
+  if constexpr (SAMPLE) {
+    const bool q0 = (qs == 0) && P.has_q0;
+    code = sample_core<VPT>(xr, a.V, q0 ? P.temperature_q0 : P.temperature, q0 ? P.top_k_q0 : P.top_k,
+                            q0 ? P.top_p_q0 : P.top_p, u, ck, sk, W, s);
+    const size_t uoff = (size_t)slot * a.Q + qs;
+    if (tid == 0) {
+      if (forced) code = (int)fcode;
+      code = min(max(code, 0), a.V - 1);
+      code_sh = code;
+      if (lead) {
+        a.codes_ring[uoff] = code;
+        a.codes_cur[qs] = code;
+      }
+    }
+    __syncthreads();
+    code = code_sh;
+    const size_t trow = ((size_t)qs * a.V + code) * KD;
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) tv[i] = TL::get(a.table, trow + tid + i * SNT);
+    load_gq();
+    const float* pp = g.ptab + ((size_t)qs * a.V + code) * 2 * KI + kc;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < VEC; i += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(pp + h * KI + i);
+        pr[h][i] = t.x; pr[h][i + 1] = t.y; pr[h][i + 2] = t.z; pr[h][i + 3] = t.w;
+      }
+  }
+
+  // x = hidden + (prefix + table row * scale), in the oracle's order; r = 1/rms(x)
+#pragma unroll
+  for (int i = 0; i < DPT; ++i) gsh[tid + i * SNT] = gv[i];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) {
+      float x = hv[m][i];
+      if constexpr (SAMPLE) {
+        const float p = __fadd_rn(pv[m][i], __fmul_rn(tv[i], g.scale));
+        x = __fadd_rn(hv[m][i], p);
+        if (lead) g.prefix_out[(size_t)m * KD + tid + i * SNT] = p;
+      }
+      xsh[m * KD + tid + i * SNT] = x;
+      ss = fmaf(x, x, ss);
+    }
+    ss = wave_sum_dpp(ss);
+    if (lane == 0) red[m][wave] = ss;
+  }
+  __syncthreads();
+  float inv[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < SWAVES; ++w) t += red[m][w];
+    inv[m] = 1.0f / sqrtf(t / (float)KD + g.eps);
+  }
+
+  // G_{q+1} = W_gu (w_in * x_q): this wave's gate and up rows
+  if constexpr (GPART) {
+    float acc[RWG][2][M];
+#pragma unroll
+    for (int r = 0; r < RWG; ++r)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r][h][m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int k0 = (j * 64 + lane) * VEC;
+      float gw[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; i += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(&gsh[k0 + i]);
+        gw[i] = t.x; gw[i + 1] = t.y; gw[i + 2] = t.z; gw[i + 3] = t.w;
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float x[VEC];
+#pragma unroll
+        for (int i = 0; i < VEC; i += 4) {
+          const float4 t = *reinterpret_cast<const float4*>(&xsh[m * KD + k0 + i]);
+          x[i] = __fmul_rn(gw[i], t.x); x[i + 1] = __fmul_rn(gw[i + 1], t.y);
+          x[i + 2] = __fmul_rn(gw[i + 2], t.z); x[i + 3] = __fmul_rn(gw[i + 3], t.w);
+        }
+#pragma unroll
+        for (int r = 0; r < RWG; ++r)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            float w[VEC];
+            TL::widen(wgu[r][h][j], w);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) acc[r][h][m] = fmaf(w[i], x[i], acc[r][h][m]);
+          }
+      }
+    }
+    // word (r * 2 + h) * M + m; its total lands in lanes word * (64 / NG) ...
+    constexpr int NG = RWG * 2 * M;
+    float wv[NG];
+#pragma unroll
+    for (int r = 0; r < RWG; ++r)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int m = 0; m < M; ++m) wv[(r * 2 + h) * M + m] = acc[r][h][m];
+    const float tot = wave_reduce_words<NG>(wv, lane);
+    if (lane % (64 / NG) == 0) {
+      const int word = lane / (64 / NG), m = word % M, h = (word / M) % 2, r = word / (2 * M);
+      g.g_out[(size_t)m * 2 * KI + h * KI + n0 + r] = tot;
+    }
+  }
+
+  // act = SwiGLU(r (G_q + scale P[c])) at this lane's chunk; y = a + W_d act
+  if constexpr (DPART) {
+    float act[M][VEC];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float gt = gq[m][0][i], up = gq[m][1][i];
+        if constexpr (SAMPLE) {
+          gt = fmaf(g.scale, pr[0][i], gt);
+          up = fmaf(g.scale, pr[1][i], up);
+        }
+        gt *= inv[m];
+        up *= inv[m];
+        // SwiGLU with the hardware exp2 and reciprocal (~1 ulp each): every
+        // workgroup forms all of the step's inner activations, so their cost
+        // is paid 256 times over.
+        act[m][i] = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
+      }
+    constexpr int ND = RD * M;                  // word i * M + m
+    float dw[ND];
+#pragma unroll
+    for (int i = 0; i < RD; ++i) {
+      float w[VEC];
+      TL::widen(wd[i], w);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float t = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) t = fmaf(w[e], act[m][e], t);
+        dw[i * M + m] = t;
+      }
+    }
+    const float dt = wave_reduce_words<ND>(dw, lane);
+    if (lane % (64 / ND) == 0) {
+      const int word = lane / (64 / ND);
+      dsum[wave][word / M][word % M] = dt;
+    }
+    __syncthreads();
+    if (tid < RD * M) {
+      const int i = tid / M, m = tid - i * M, row = row0 + i;
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < SWAVES; ++w) t += dsum[w][i][m];
+      const float av = gsh[row] * (xsh[m * KD + row] * inv[m]);   // residual a = w_in * (x * r)
+      g.y[(size_t)m * KD + row] = av + t;
+    }
+  }
+}
+
+__host__ __device__ constexpr bool depth_step_fits(int d, int inner, int vec) {
+  return (d == 1024 || d == 2048) && inner == SWAVES * 64 * vec && inner % (DEPTH_WGS * SWAVES) == 0;
+}
+
+// Code tables P_j[c] = W_gu (w_in * table[j][c]) are built with the prefill
+// GEMM from rows of table[j] times the norm gain (FP32).
+template <typename TL>
+__global__ void scale_rows_kernel(const void* table, const float* gain, int rows, int d, float* out) {
+  const size_t n = (size_t)rows * d;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    out[i] = TL::get(table, i) * gain[i % d];
 }
 
 // Standalone sampler (operator API): one utterance, parameters by value.

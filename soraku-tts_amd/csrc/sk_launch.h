@@ -203,6 +203,36 @@ static hipError_t launch_depth_fused(const SampleArgs& s, const GemvArgs& g, int
   });
 }
 
+// Depth steps by code tables (depth_step_kernel): CFG rows (2), the Qwen3-0.6B
+// shape with FP32 weights (d 1024, inner 2048) or the 1.7B shape with BF16
+// weights (d 2048, inner 4096) -- the shapes whose inner dimension is eight
+// waves' 16-byte loads.
+static inline bool code_tables_fit(int d, int rows, int depth_inner, int V, int wdtype) {
+  const int vec = wdtype == SK_BF16 ? 8 : 4;
+  return rows == 2 && ((d == 1024 && wdtype == SK_F32) || (d == 2048 && wdtype == SK_BF16)) &&
+         depth_step_fits(d, depth_inner, vec) && V <= MAX_V && depth_sample_smem(V) <= 65536;
+}
+template <typename TL, int KD, int KI, int MODE>
+static hipError_t launch_depth_step_t(const SampleArgs& s, const DepthArgs& g, int q, hipStream_t st) {
+  if constexpr (MODE >= 2) {
+    return with_vpt(s.V, [&](auto vpt) {
+      hipLaunchKernelGGL((depth_step_kernel<TL, decltype(vpt)::value, 2, KD, KI, MODE>), dim3(DEPTH_WGS), dim3(SNT),
+                         depth_sample_smem(s.V), st, s, g, q);
+      return hipGetLastError();
+    });
+  } else {
+    hipLaunchKernelGGL((depth_step_kernel<TL, 1, 2, KD, KI, MODE>), dim3(DEPTH_WGS), dim3(SNT), 0, st, s, g, q);
+    return hipGetLastError();
+  }
+}
+template <int MODE>
+static hipError_t launch_depth_step(int wdtype, int d, const SampleArgs& s, const DepthArgs& g, int q,
+                                    hipStream_t st) {
+  if (wdtype == SK_BF16 && d == 2048) return launch_depth_step_t<WBF16, 2048, 4096, MODE>(s, g, q, st);
+  if (wdtype == SK_F32 && d == 1024) return launch_depth_step_t<WF32, 1024, 2048, MODE>(s, g, q, st);
+  return hipErrorInvalidConfiguration;   // not selected at capture
+}
+
 static inline hipError_t prepare_sampler() {
   static bool done = false;
   if (done) return hipSuccess;

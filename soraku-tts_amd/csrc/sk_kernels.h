@@ -2459,9 +2459,14 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
         wgu[r][1][j] = TL::raw(g.w_up, off);
       }
   }
+  // The down rows go ahead of the sampler too when few loads are in flight
+  // per lane; with more (the 1.7B shape: 16 gate/up + 8 down per lane) the
+  // sampler itself ran slower behind them (code drawn after 10.7 us instead of
+  // 8.6), so there they follow the code with its table entries.
+  constexpr bool WD_EARLY = 2 * RWG * NV + RD <= 16;
   const int row0 = blockIdx.x * RD;
   uint4 wd[DPART ? RD : 1];
-  if constexpr (DPART) {
+  if constexpr (DPART && (!SAMPLE || WD_EARLY)) {
 #pragma unroll
     for (int i = 0; i < RD; ++i) wd[i] = TL::raw(g.w_down, (size_t)(row0 + i) * KI + kc);
   }
@@ -2504,6 +2509,10 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
 #pragma unroll
     for (int i = 0; i < DPT; ++i) tv[i] = TL::get(a.table, trow + tid + i * SNT);
     load_gq();
+    if constexpr (!WD_EARLY) {
+#pragma unroll
+      for (int i = 0; i < RD; ++i) wd[i] = TL::raw(g.w_down, (size_t)(row0 + i) * KI + kc);
+    }
     const float* pp = g.ptab + ((size_t)qs * a.V + code) * 2 * KI + kc;
 #pragma unroll
     for (int h = 0; h < 2; ++h)

@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -26,6 +27,7 @@
 #include "sk_error.h"
 #include "sk_kernels.h"
 #include "sk_launch.h"
+#include "sk_layer.h"
 #include "sk_prefill.h"
 #include "sk_wide.h"
 #include "soraku_mi355x.h"
@@ -174,6 +176,14 @@ struct sk_engine {
   bool code_tables = false;
   float* ptab = nullptr;
   float* gbuf[2] = {nullptr, nullptr};
+
+  // XCD-resident trunk layers (lx_attn_kernel + lx_mlp_kernel per layer, one
+  // utterance with CFG, 8 KV heads): residual stream after each launch, the
+  // launches' per-XCD partials, a zero block for the first layer's input,
+  // barrier epochs and the error word (nonzero: a barrier timed out).
+  bool lx = false;
+  float *lx_xl = nullptr, *lx_xm = nullptr, *lx_opart = nullptr, *lx_dpart = nullptr, *lx_zero = nullptr;
+  unsigned *lx_flags = nullptr, *lx_err = nullptr;
 
   // batched prefill activations, sized for the largest packed prefix so far
   int pf_cap = 0;
@@ -476,7 +486,56 @@ hipError_t launch_attn_stream(sk_engine* e, const AttnArgs& at) {
   return e->c.kv_dtype == SK_BF16 ? launch_attn_stream_kt<uint16_t>(e, at) : launch_attn_stream_kt<float>(e, at);
 }
 
+// XCD-resident layers (sk_layer.h): one utterance with CFG at the Qwen3-0.6B
+// trunk shape (d 1024, SwiGLU 3072, 16 q / 8 KV heads of 128), FP32 or BF16
+// weights and cache.
+bool lx_fits(const sk_engine* e) {
+  const sk_config& c = e->c;
+  return e->rows == LX_M && !e->wide && e->attn_splits == 0 && c.n_kv_heads == LX_HKV && c.n_q_heads == LX_HQ &&
+         c.head_dim == LX_HD && c.d_model == 1024 && c.trunk_inter == 3072;
+}
+
+template <typename WL, typename KT>
+hipError_t launch_lx(const LxArgs& A, const LxArgs& C, hipStream_t st) {
+  hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 1024>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
+  hipLaunchKernelGGL((lx_mlp_kernel<WL, 1024, 3072>), dim3(LX_WGS), dim3(LX_NT), 0, st, C);
+  return hipGetLastError();
+}
+
+// Each layer as two launches: attention half (x + partials -> q/k/v ->
+// attention -> O partials) and MLP half (x + O partials -> SwiGLU -> down
+// partials); the final norm adds the last layer's down partials.
+hipError_t enqueue_trunk_lx(sk_engine* e) {
+  const sk_config& c = e->c;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerW& w = e->L[l];
+    LxArgs A{};
+    A.wq = w.q; A.wk = w.k; A.wv = w.v; A.wo = w.o;
+    A.gain = w.in_norm; A.q_norm = w.q_norm; A.k_norm = w.k_norm;
+    A.xin = l == 0 ? e->x : e->lx_xm;
+    A.pin = l == 0 ? e->lx_zero : e->lx_dpart;
+    A.xout = e->lx_xl; A.pout = e->lx_opart;
+    A.qkv = e->qkv; A.part = e->part; A.act = e->act; A.ld_act = e->inner_max;
+    A.kc = e->kc + (size_t)l * kv_layer_bytes(e);
+    A.vc = e->vc + (size_t)l * kv_layer_bytes(e);
+    A.rope = e->rope; A.kv_len = e->kv_len; A.active = e->active;
+    A.flags = e->lx_flags; A.err = e->lx_err;
+    A.max_ctx = c.max_ctx; A.max_chunks = e->max_chunks;
+    A.eps = c.trunk_eps; A.scale = 1.0f / sqrtf((float)c.head_dim);
+    A.spin_ticks = LX_SPIN_TICKS;
+    LxArgs C = A;
+    C.wg = w.gate; C.wu = w.up; C.wd = w.down; C.gain = w.post_norm;
+    C.xin = e->lx_xl; C.pin = e->lx_opart; C.xout = e->lx_xm; C.pout = e->lx_dpart;
+    const bool wbf = c.weight_dtype == SK_BF16, kbf = c.kv_dtype == SK_BF16;
+    const hipError_t err = wbf ? (kbf ? launch_lx<WBF16, uint16_t>(A, C, e->stream) : launch_lx<WBF16, float>(A, C, e->stream))
+                               : (kbf ? launch_lx<WF32, uint16_t>(A, C, e->stream) : launch_lx<WF32, float>(A, C, e->stream));
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
 hipError_t enqueue_trunk(sk_engine* e) {
+  if (e->lx) return enqueue_trunk_lx(e);
   const sk_config& c = e->c;
   const int d = c.d_model, hd = c.head_dim, M = e->rows;
   const int wt = c.weight_dtype;
@@ -693,7 +752,8 @@ hipError_t enqueue_tail(sk_engine* e) {
   const int d = c.d_model, M = e->rows;
   hipError_t err;
   if ((err = enqueue_trunk(e)) != hipSuccess) return err;
-  hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x, e->final_norm,
+  hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->lx ? e->lx_xm : e->x,
+                     e->lx ? e->lx_dpart : nullptr, e->final_norm,
                      c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->fc, e->u_ring,
                      e->flag_ring, e->u_cur, e->flag_cur, c.n_utts * c.n_codebooks, c.max_frames,
                      e->inv_freq, c.head_dim / 2, e->rope, (const float2*)e->p_rope, c.max_ctx + 1,
@@ -1037,6 +1097,29 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   }
   if (he == hipSuccess) he = prepare_sampler();
   if (he == hipSuccess && e->wide && c.weight_dtype == SK_BF16) he = probe_xcd_mapping(e->stream, &e->split_k);
+  // XCD-resident layers: the shape fits, the device has 8 x 32 CUs, workgroups
+  // whose ids agree mod 8 share an XCD, and SORAKU_XCD_LAYERS is not "0"
+  if (he == hipSuccess && lx_fits(e)) {
+    const char* env = getenv("SORAKU_XCD_LAYERS");
+    int cus = 0;
+    he = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device);
+    bool mapped = false;
+    if (he == hipSuccess && cus == LX_WGS && !(env && strcmp(env, "0") == 0)) he = probe_xcd_mapping(e->stream, &mapped);
+    e->lx = he == hipSuccess && mapped;
+  }
+  if (he == hipSuccess && e->lx) {
+    const size_t pe = (size_t)LX_XCDS * R * d;
+    he = dalloc(&e->lx_xl, R * d);
+    if (he == hipSuccess) he = dalloc(&e->lx_xm, R * d);
+    if (he == hipSuccess) he = dalloc(&e->lx_opart, pe);
+    if (he == hipSuccess) he = dalloc(&e->lx_dpart, pe);
+    if (he == hipSuccess) he = dalloc(&e->lx_zero, pe);
+    if (he == hipSuccess) he = dalloc(&e->lx_flags, (size_t)LX_XCDS * LX_FLAGS);
+    if (he == hipSuccess) he = dalloc(&e->lx_err, 1);
+    if (he == hipSuccess) he = hipMemset(e->lx_zero, 0, pe * sizeof(float));
+    if (he == hipSuccess) he = hipMemset(e->lx_flags, 0, (size_t)LX_XCDS * LX_FLAGS * sizeof(unsigned));
+    if (he == hipSuccess) he = hipMemset(e->lx_err, 0, sizeof(unsigned));
+  }
   if (he == hipSuccess)
     he = hipFuncSetAttribute(c.kv_dtype == SK_BF16 ? reinterpret_cast<const void*>(attention_kernel<uint16_t>)
                                                    : reinterpret_cast<const void*>(attention_kernel<float>),
@@ -1055,6 +1138,7 @@ int sk_destroy(sk_engine* e) {
                   e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->flag_ring, e->u_ring,
                   e->pf_mem, e->ptab, e->gbuf[0], e->gbuf[1],
+                  e->lx_xl, e->lx_xm, e->lx_opart, e->lx_dpart, e->lx_zero, e->lx_flags, e->lx_err,
                   e->p_row_start, e->p_rope,
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
   for (void* p : bufs)
@@ -1341,6 +1425,15 @@ int sk_capture(sk_engine* e) {
   return SK_OK;
 }
 
+// The XCD-resident layers' error word (read after the stream is drained).
+static int check_lx(sk_engine* e) {
+  if (!e->lx) return SK_OK;
+  unsigned w = 0;
+  SK_HIP(hipMemcpy(&w, e->lx_err, sizeof(w), hipMemcpyDeviceToHost));
+  SK_CHECK(w == 0u, SK_EHIP, "trunk layer barrier timed out (error word 0x%x); the engine must be recreated", w);
+  return SK_OK;
+}
+
 static int check_step(sk_engine* e, int n) {
   SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
   SK_CHECK(e->exec != nullptr, SK_ENOCAPTURE, "step before capture");
@@ -1386,7 +1479,7 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
   SK_HIP(hipStreamSynchronize(e->stream));
   e->fc_host += 1;
   for (int r = 0; r < e->rows; ++r) e->kv_host[r] += e->active_host[r];
-  return SK_OK;
+  return check_lx(e);
 }
 
 int sk_queue_frames(sk_engine* e, int32_t n, const double* uniforms, const int32_t* mask_eos_q0) {
@@ -1430,13 +1523,13 @@ int sk_read_codes(sk_engine* e, int32_t n, int64_t* codes_out) {
   SK_HIP(hipStreamSynchronize(e->stream));
   SK_HIP(hipMemcpy(codes_out, e->codes_ring + (size_t)(e->fc_host - n) * nq, (size_t)n * nq * sizeof(int64_t),
                    hipMemcpyDeviceToHost));
-  return SK_OK;
+  return check_lx(e);
 }
 
 int sk_synchronize(sk_engine* e) {
   SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
   SK_HIP(hipStreamSynchronize(e->stream));
-  return SK_OK;
+  return check_lx(e);
 }
 
 void* sk_stream(sk_engine* e) { return e ? (void*)e->stream : nullptr; }

@@ -2712,8 +2712,10 @@ __global__ __launch_bounds__(NT) void rope_rows_kernel(const int* pos, const flo
 // new position), the frame counter moves on and the next frame's draws and flags
 // are copied from the ring to the fixed current-frame slots.  With abuf set it
 // also writes depth step 0's input, RMSNorm_in(hidden) (the codebook prefix is
-// zero when a frame starts), and its split form when xs_abuf is set.
-__global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const float* w, float eps,
+// zero when a frame starts), and its split form when xs_abuf is set.  With
+// parts set the trunk's last layer left its residual update as 8 per-XCD
+// partials [8][rows][D]: x + parts[0] + ... + parts[7] is normed, in that order.
+__global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const float* parts, const float* w, float eps,
                                                         int D, float* hidden, int* kv_len, int* pos,
                                                         const int* active, int* counter,
                                                         const double* u_ring, const int* flag_ring,
@@ -2737,6 +2739,18 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
         xv[i] = xr[k];
         wv[i] = w[k];
         gv[i] = abuf ? w_in[k] : 0.f;
+      }
+      if (parts) {
+        const size_t ps = (size_t)gridDim.x * D;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int k = min((int)threadIdx.x + i * NT, D - 1);
+          float pv[8];
+#pragma unroll
+          for (int h = 0; h < 8; ++h) pv[h] = parts[h * ps + ro + k];
+#pragma unroll
+          for (int h = 0; h < 8; ++h) xv[i] = __fadd_rn(xv[i], pv[h]);
+        }
       }
       float s = 0.f;
 #pragma unroll
@@ -2766,7 +2780,7 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
           }
         }
       }
-    } else {
+    } else {   // (parts are only used with D <= NT * PER)
       float s = 0.f;
       for (int k = threadIdx.x; k < D; k += NT) s += xr[k] * xr[k];
       const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);

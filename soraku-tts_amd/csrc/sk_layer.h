@@ -1,0 +1,805 @@
+// XCD-resident trunk layer for one utterance with CFG (two decode rows) and
+// eight KV heads: two launches per layer instead of five.
+//
+// MI355X has 8 XCDs of 32 CUs; each XCD has its own L2, and the workgroups of
+// a launch are dealt to the XCDs round-robin (lx_xcd).  KV head g's work goes
+// to XCD g, so the dependencies inside a layer that are local to
+// a head -- q/k/v rows -> attention chunks -> chunk merge -> that head pair's
+// columns of the O projection -- and local to an eighth of the SwiGLU inner
+// dimension -- gate/up rows -> those columns of the down projection -- stay on
+// one XCD and pass through its L2:
+//
+//   lx_attn_kernel: x = x_in + sum_h part_in[h] (h = 0..7, fixed order) ->
+//     RMSNorm -> q/k/v rows of KV head g -> barrier -> QK-norm, RoPE, KV
+//     append, 32-token attention chunks of head g -> barrier -> chunk merge ->
+//     O[:, head g's 256 columns] . attn = this XCD's partial of the residual
+//     update, part_out[g];
+//   lx_mlp_kernel: x = x_in + sum_h part_in[h] -> RMSNorm -> gate/up rows of
+//     inner slice g -> SwiGLU -> barrier -> down[:, slice g] . act =
+//     part_out[g].
+//
+// The next launch (or the final norm) adds the 8 partials in XCD order, so the
+// projections' sums are taken in a fixed order and replays stay bitwise equal.
+//
+// Barrier among the 32 workgroups of an XCD (lx_xcd_barrier): each workgroup
+// stores its epoch in its own word of the XCD's flag line and one wave polls
+// the 32 words with agent-scope loads, which read the L2 (0.5 us measured,
+// against 1.6 us for a kernel boundary).  Data exchanged through it is written
+// with plain stores whose completion the writer waits for, and read with
+// agent-scope loads.  On gfx9 one counter (vmcnt) covers loads and stores and
+// retires in issue order, so waiting for a store also waits for every load
+// issued before it, and a load's data is usable only once every earlier load
+// of the wave has arrived.  Each workgroup therefore splits its 8 waves:
+//   * exchange waves (0-3) issue the first phase's weights, and do every
+//     exchange store, flag and agent-scope load; they hold no prefetch across
+//     a barrier;
+//   * stream waves (4-7) issue the later phases' K/V and weights at entry and
+//     take their inputs from LDS, so nothing they wait for is behind a barrier.
+// Each role is straight-line code and both execute the same sequence of LDS
+// barriers (lx_sync); none of them waits for global loads.
+//
+// Every spin is bounded (spin_ticks of the 100 MHz real-time counter): a
+// workgroup that times out sets err bit 0 and leaves the launch (so would a
+// dispatch that gave an XCD other than 32 of the workgroups).  The host
+// reports err after a frame; a set bit makes every later barrier exit at once.
+#pragma once
+
+#include "sk_kernels.h"
+
+namespace sk {
+namespace {
+
+constexpr int LX_XCDS = 8;
+constexpr int LX_PER = 32;                      // workgroups per XCD
+constexpr int LX_WGS = LX_XCDS * LX_PER;
+constexpr int LX_NT = 512;                      // 4 exchange + 4 stream waves
+constexpr int LX_FLAGS = 64;                    // flag words per XCD (32 used; 256 B apart)
+constexpr int LX_M = 2, LX_HD = 128, LX_G = 2, LX_HKV = 8, LX_HQ = LX_G * LX_HKV;
+// A barrier wait longer than this (50 ms of the 100 MHz real-time counter)
+// ends the launch with an error instead of waiting further.
+constexpr unsigned long long LX_SPIN_TICKS = 5000000ull;
+
+struct LxArgs {
+  const void* wq; const void* wk; const void* wv; const void* wo;   // [out][in], weight dtype
+  const void* wg; const void* wu; const void* wd;
+  const float* gain;                 // RMSNorm gain of the launch's input (in_norm / post_norm)
+  const float* q_norm; const float* k_norm;
+  const float* xin;                  // [M][D] residual stream entering the launch
+  const float* pin;                  // [8][M][D] partials to add (zeros for the first layer)
+  float* xout;                       // [M][D] xin + sum(pin), written by workgroup 0
+  float* pout;                       // [8][M][D] this launch's partials
+  float* qkv;                        // [M][(HQ + 2 HKV) HD] raw projections (exchanged)
+  float* part;                       // [M][HQ][max_chunks][HD + 4] chunk partials (exchanged)
+  float* act; int ld_act;            // [M][ld_act] SwiGLU output (exchanged)
+  void* kc; void* vc;                // this layer's cache, [M][HKV][max_ctx][HD]
+  const float2* rope;                // [M][HD / 2] (cos, sin) at each row's position
+  const int* kv_len; const int* active;
+  unsigned* flags;                   // [8][LX_FLAGS] barrier epochs
+  unsigned* err;
+  int max_ctx, max_chunks;
+  float eps, scale;
+  unsigned long long spin_ticks;
+};
+
+// The XCD this workgroup runs on (the XCC_ID hardware register).  The
+// dispatcher deals a launch's workgroups to the 8 XCDs round-robin, starting
+// at an XCD that can differ between launches (it did with two streams in
+// use), so the XCD is read, not derived from blockIdx.x; the workgroups of one
+// XCD are those with one blockIdx.x mod 8, so blockIdx.x / 8 numbers them
+// 0..31 within it (sk_create checks the round-robin with xcd_probe_kernel).
+__device__ __forceinline__ int lx_xcd() { return (int)(__builtin_amdgcn_s_getreg((31 << 11) | 20) & 7u); }
+
+// Workgroup barrier for LDS only: waits for this wave's LDS operations, never
+// for its global loads (a fenced __syncthreads would wait for the prefetches).
+__device__ __forceinline__ void lx_sync() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void lx_wait_stores() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+  asm volatile("" ::: "memory");
+}
+// Exchanged data (written in this launch by other workgroups of the XCD) is
+// read with plain loads: the L1 starts every launch empty, a CU reads each
+// exchanged line once, after the barrier, and L1 does not allocate on stores,
+// so the loads miss in L1 and read the XCD's L2 (0.36 us after a barrier,
+// against 0.96 us for agent-scope loads).
+__device__ __forceinline__ float lx_ld(const float* p) { return *p; }
+
+// The 32 workgroups of this XCD meet.  The exchange waves have waited for
+// their stores; wave 0 stores this workgroup's epoch and polls all 32.
+// Returns false (uniformly) on a timeout, or when err0 (the error word as the
+// launch found it) is set.
+__device__ __forceinline__ bool lx_xcd_barrier(unsigned* fl, int j, unsigned target, unsigned long long deadline,
+                                               unsigned err0, unsigned* err, int* okf) {
+  lx_sync();
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    if (tid == 0) __hip_atomic_store(fl + j, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    int good = 1;
+    for (;;) {
+      const unsigned v = __hip_atomic_load(fl + (tid & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_ballot_w64((int)(v - target) < 0) == 0ull) break;
+      if (__builtin_amdgcn_s_memrealtime() > deadline) { good = 0; break; }
+    }
+    if (err0 != 0u) good = 0;   // an earlier launch failed: leave at once
+    if (tid == 0) {
+      *okf = good;
+      if (!good) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+  lx_sync();
+  return *okf != 0;
+}
+
+// Input of a launch: x = xin + pin[0] + ... + pin[7] for both rows, EPT
+// consecutive elements per thread (a wave's elements lie in one row), and the
+// RMSNorm gain.  issue() only loads; finish() sums, stores x (pre-norm) and
+// the gain to LDS and each wave's sum of squares to ssq[wave].
+template <int D>
+struct LxInput {
+  static constexpr int EPT = LX_M * D / LX_NT;   // 4 or 8
+  static constexpr int GPT = D / LX_NT;          // 2 or 4
+  static_assert(EPT % 4 == 0 && (GPT == 2 || GPT == 4) && (64 * EPT) <= D, "LxInput shape");
+  float4 v[9][EPT / 4];
+  float gv[GPT];
+  __device__ __forceinline__ void issue(const LxArgs& a, int tid) {
+    const size_t e0 = (size_t)tid * EPT;
+#pragma unroll
+    for (int i = 0; i < EPT / 4; ++i) v[0][i] = *reinterpret_cast<const float4*>(a.xin + e0 + 4 * i);
+#pragma unroll
+    for (int h = 0; h < 8; ++h)
+#pragma unroll
+      for (int i = 0; i < EPT / 4; ++i)
+        v[1 + h][i] = *reinterpret_cast<const float4*>(a.pin + (size_t)h * LX_M * D + e0 + 4 * i);
+    if constexpr (GPT == 2) {
+      const float2 t = *reinterpret_cast<const float2*>(a.gain + tid * 2);
+      gv[0] = t.x; gv[1] = t.y;
+    } else {
+      const float4 t = *reinterpret_cast<const float4*>(a.gain + tid * 4);
+      gv[0] = t.x; gv[1] = t.y; gv[2] = t.z; gv[3] = t.w;
+    }
+  }
+  __device__ __forceinline__ void finish(float* xsh, float* gsh, float* ssq, int tid, int wave) {
+    // The loaded values enter the sums only here, inside each role's code: the
+    // compiler may not start the sums (and wait for these loads) above the
+    // role branch, ahead of the role's weight stream.
+#pragma unroll
+    for (int h = 0; h < 9; ++h)
+#pragma unroll
+      for (int i = 0; i < EPT / 4; ++i) asm volatile("" : "+v"(v[h][i].x), "+v"(v[h][i].y), "+v"(v[h][i].z), "+v"(v[h][i].w));
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPT / 4; ++i) {
+      float4 s = v[0][i];
+#pragma unroll
+      for (int h = 1; h < 9; ++h) {
+        s.x = __fadd_rn(s.x, v[h][i].x); s.y = __fadd_rn(s.y, v[h][i].y);
+        s.z = __fadd_rn(s.z, v[h][i].z); s.w = __fadd_rn(s.w, v[h][i].w);
+      }
+      *reinterpret_cast<float4*>(xsh + tid * EPT + 4 * i) = s;
+      ss = fmaf(s.x, s.x, ss); ss = fmaf(s.y, s.y, ss); ss = fmaf(s.z, s.z, ss); ss = fmaf(s.w, s.w, ss);
+    }
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) gsh[tid * GPT + i] = gv[i];
+    ss = wave_sum_dpp(ss);
+    if ((tid & 63) == 0) ssq[wave] = ss;
+  }
+};
+
+// 1 / rms of row m from the per-wave sums (waves 4m .. 4m+3 hold row m).
+template <int D>
+__device__ __forceinline__ float lx_inv_rms(const float* ssq, int m, float eps) {
+  const float s = ((ssq[4 * m] + ssq[4 * m + 1]) + ssq[4 * m + 2]) + ssq[4 * m + 3];
+  return 1.0f / sqrtf(s / (float)D + eps);
+}
+
+// RW rows of a GEMV over K = D against the normalized input rows held in LDS:
+// acc[r][m] = sum_k w[r][k] gain[k] (x[m][k] inv[m]).  Weights are raw 16-byte
+// words in registers (BF16 widened where multiplied), in the lane layout of
+// gemv_fast_kernel (lane l holds k = (jj*64 + l)*VEC + i); x is read from LDS
+// one slice at a time.  acc holds this lane's partial sums; the caller
+// reduces them together (wave_reduce_words).
+template <int D, int RW, typename WL>
+__device__ __forceinline__ void lx_dots(const uint4 (&w)[RW][D / (64 * WL::VEC)], const float* xsh, const float* gsh,
+                                        const float (&inv)[LX_M], int lane, float (&acc)[RW][LX_M]) {
+  constexpr int VEC = WL::VEC, NV = D / (64 * VEC);
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int m = 0; m < LX_M; ++m) acc[r][m] = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < NV; ++jj) {
+    float xv[LX_M][VEC];
+    const int k0 = (jj * 64 + lane) * VEC;
+#pragma unroll
+    for (int i = 0; i < VEC; i += 4) {
+      const float4 gg = *reinterpret_cast<const float4*>(gsh + k0 + i);
+#pragma unroll
+      for (int m = 0; m < LX_M; ++m) {
+        const float4 t = *reinterpret_cast<const float4*>(xsh + m * D + k0 + i);
+        xv[m][i] = gg.x * (t.x * inv[m]);
+        xv[m][i + 1] = gg.y * (t.y * inv[m]);
+        xv[m][i + 2] = gg.z * (t.z * inv[m]);
+        xv[m][i + 3] = gg.w * (t.w * inv[m]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      float wf[VEC];
+      WL::widen(w[r][jj], wf);
+#pragma unroll
+      for (int m = 0; m < LX_M; ++m)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[r][m] = fmaf(wf[i], xv[m][i], acc[r][m]);
+    }
+  }
+}
+
+// Wave sums of R x M per-lane partials at once: word w = r * M + m (padded to
+// N words with zeros) ends in lanes [w * 64 / N, (w + 1) * 64 / N).
+template <int N, int R>
+__device__ __forceinline__ float lx_reduce(const float (&acc)[R][LX_M], int lane) {
+  static_assert(R * LX_M <= N, "lx_reduce: too many words");
+  float w[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) w[i] = i < R * LX_M ? acc[i / LX_M][i % LX_M] : 0.f;
+  return wave_reduce_words<N>(w, lane);
+}
+
+// E consecutive elements of a weight row (the O and down projections' column
+// slices), widened to FP32: FP32 E = 2 (8 bytes); BF16 E = 4 (8 bytes) or 2
+// (4 bytes) when the slice is not a multiple of 256 columns.
+template <typename WL, int E> struct LxCols;
+template <> struct LxCols<WF32, 2> {
+  __device__ __forceinline__ static void load(const void* base, size_t off, float (&o)[2]) {
+    const float2 t = *reinterpret_cast<const float2*>(static_cast<const float*>(base) + off);
+    o[0] = t.x; o[1] = t.y;
+  }
+};
+template <> struct LxCols<WBF16, 4> {
+  __device__ __forceinline__ static void load(const void* base, size_t off, float (&o)[4]) {
+    const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+    o[0] = __uint_as_float(t.x << 16); o[1] = __uint_as_float(t.x & 0xffff0000u);
+    o[2] = __uint_as_float(t.y << 16); o[3] = __uint_as_float(t.y & 0xffff0000u);
+  }
+};
+template <> struct LxCols<WBF16, 2> {
+  __device__ __forceinline__ static void load(const void* base, size_t off, float (&o)[2]) {
+    const uint32_t t = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(base) + off);
+    o[0] = __uint_as_float(t << 16); o[1] = __uint_as_float(t & 0xffff0000u);
+  }
+};
+template <typename WL>
+__host__ __device__ constexpr int lx_col_elems(int ncols) {
+  return sizeof(typename WL::elem) == 4 ? 2 : (ncols % 256 == 0 ? 4 : 2);
+}
+
+// ---------------------------------------------------------------------------
+// Attention half of a layer.  Grid LX_WGS, block LX_NT.
+// KT: KV cache element (float or uint16_t BF16 bits).
+template <typename WL, typename KT, int D>
+__global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
+  constexpr int M = LX_M, HD = LX_HD, G = LX_G, HQ = LX_HQ, HKV = LX_HKV;
+  constexpr int VEC = WL::VEC, NVQ = D / (64 * VEC);
+  constexpr int QRW = (G + 2) * HD / LX_PER / 4;        // q/k/v rows per exchange wave
+  constexpr int OROWS = D / LX_PER, ORW = OROWS / 4;     // W_o rows per workgroup / stream wave
+  constexpr int OCOL = G * HD;                           // W_o columns of one KV head
+  constexpr int OE = lx_col_elems<WL>(OCOL);
+  using NL = LxCols<WL, OE>;
+  constexpr int OU = OCOL / (64 * OE);                   // column units per lane per W_o row
+  constexpr int LPT = HD / ATT_DPL;                      // lanes per token
+  constexpr int NLD = ATT_DPL * (int)sizeof(KT) / 16;    // 16-byte K (and V) loads per lane
+  constexpr bool KBF = sizeof(KT) == 2;
+  constexpr int PS = part_stride(HD);
+  static_assert(QRW == 4 && OCOL % (64 * OE) == 0 && LX_NT / 2 / LPT == ATT_CHUNK, "lx_attn_kernel shape");
+  static_assert(D % (64 * VEC) == 0 && ORW * 4 == OROWS, "lx_attn_kernel shape");
+
+  __shared__ __attribute__((aligned(16))) float xsh[M * D];
+  __shared__ __attribute__((aligned(16))) float gsh[D];
+  __shared__ float ssq[8];
+  __shared__ __attribute__((aligned(16))) float qs[M][G * HD];   // raw, then normalized + rotated
+  __shared__ __attribute__((aligned(16))) float kn[M][HD];
+  __shared__ __attribute__((aligned(16))) float vn[M][HD];
+  __shared__ float sc[G][ATT_CHUNK];
+  __shared__ float stt[G][2];
+  __shared__ __attribute__((aligned(16))) float vs[ATT_CHUNK * HD];
+  __shared__ float pb[G][HD + 2];
+  __shared__ __attribute__((aligned(16))) float ash[M][OCOL];
+  __shared__ float qwn[HD], kwn[HD];
+  __shared__ float2 csh[M][HD / 2];
+  __shared__ int stsh[2][6];   // row 0: kv_len[0..1], active[0..1], barrier epoch, error word
+  __shared__ int okf;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lx_xcd(), j = blockIdx.x >> 3;
+  const unsigned long long deadline = __builtin_amdgcn_s_memrealtime() + a.spin_ticks;
+  unsigned* fl = a.flags + g * LX_FLAGS;
+  // Row lengths decide the chunk slots: slot s is row 0's chunk s, then row
+  // 1's chunk s - nch0; workgroup j takes slots j, j + 32, ...  The loads sit
+  // where each role first needs them (see the role sections).
+  // The stream waves load them (they need the lengths first, for their K/V
+  // loads) together with the barrier epoch and the error word, and pass all
+  // six to the exchange waves through LDS (stsh), whose own loads would sit
+  // behind their weight stream.
+  int T0, T1, nch0, nch1, nsl, nit;
+  auto rows_state = [&](int t0, int t1, int a0, int a1) {
+    T0 = t0; T1 = t1;
+    nch0 = a0 ? (T0 + ATT_CHUNK) / ATT_CHUNK : 0;   // chunks holding T + 1 tokens
+    nch1 = a1 ? (T1 + ATT_CHUNK) / ATT_CHUNK : 0;
+    nsl = nch0 + nch1;
+    nit = (nsl + LX_PER - 1) / LX_PER;              // slots per workgroup (one bound for all)
+  };
+  LxInput<D> in;
+  in.issue(a, tid);
+  // Chunk merge after the second barrier, by all 8 waves: thread t -> row
+  // t >> 8, head (t >> 7) & 1 of the pair, dim t & 127; up to 16 chunks'
+  // partials per batch of loads, merged in chunk order with a running max.
+  auto merge = [&]() {
+    const int m = tid >> 8, gi = (tid >> 7) & 1, d = tid & (HD - 1);
+    const int nch = m == 0 ? nch0 : nch1;
+    const float* pp = a.part + (((size_t)m * HQ + g * G + gi) * a.max_chunks) * PS;
+    float Mr = -INFINITY, L = 0.f, O = 0.f;
+    constexpr int CB = 16;
+    for (int c0 = 0; c0 < nch; c0 += CB) {
+      float2 ml[CB];
+      float ov[CB];
+#pragma unroll
+      for (int q = 0; q < CB; ++q) {
+        const float* pc = pp + (size_t)min(c0 + q, nch - 1) * PS;
+        ml[q] = *reinterpret_cast<const float2*>(pc + HD);
+        ov[q] = lx_ld(pc + d);
+      }
+      float Mb = Mr;
+#pragma unroll
+      for (int q = 0; q < CB; ++q)
+        if (c0 + q < nch) Mb = fmaxf(Mb, ml[q].x);
+      const float rs = expf(Mr - Mb);   // 0 on the first block
+      L *= rs; O *= rs;
+#pragma unroll
+      for (int q = 0; q < CB; ++q)
+        if (c0 + q < nch) {
+          const float e = expf(ml[q].x - Mb);
+          L = fmaf(ml[q].y, e, L);
+          O = fmaf(ov[q], e, O);
+        }
+      Mr = Mb;
+    }
+    ash[m][gi * HD + d] = nch ? O / L : 0.f;
+  };
+
+  if (wave >= 4) {
+    // ===================== stream waves =====================
+    __builtin_amdgcn_sched_barrier(1);
+    const int w4 = wave - 4, st = tid - 256;
+    const int tok = st / LPT, sub = st % LPT;
+    {
+      const int t0 = a.kv_len[0], t1 = a.kv_len[1], a0 = a.active[0], a1 = a.active[1];
+      const unsigned ep = fl[j], er = *a.err;
+      rows_state(t0, t1, a0, a1);
+      // every stream thread writes (thread 0 to row 0, the rest to row 1):
+      // no branch for the compiler to sink these loads into
+      int* sd = stsh[st == 0 ? 0 : 1];
+      sd[0] = t0; sd[1] = t1; sd[2] = a0; sd[3] = a1; sd[4] = (int)ep; sd[5] = (int)er;
+    }
+    // K/V of this workgroup's first slot (clamped into the cache when the
+    // slot does not exist; then unused)
+    const int s0 = j < nsl ? j : 0;
+    const int m0 = s0 < nch0 ? 0 : 1, c0s = s0 < nch0 ? s0 : s0 - nch0;
+    uint4 kraw[NLD], vraw[NLD];
+    auto load_kv = [&](int m, int c) {
+      const int tt = min(c * ATT_CHUNK + tok, a.max_ctx - 1);
+      const size_t off = (((size_t)m * HKV + g) * a.max_ctx + tt) * HD + sub * ATT_DPL;
+      const uint4* kp = reinterpret_cast<const uint4*>(static_cast<const KT*>(a.kc) + off);
+      const uint4* vp = reinterpret_cast<const uint4*>(static_cast<const KT*>(a.vc) + off);
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) { kraw[i] = kp[i]; vraw[i] = vp[i]; }
+    };
+    in.finish(xsh, gsh, ssq, tid, wave);
+    lx_sync();                                                   // 1
+    // The first slot's K/V, issued once the exchange waves' q/k/v weights
+    // are in flight (the projections are on the critical path; the cache rows
+    // are needed only after the first barrier)
+    load_kv(m0, c0s);
+    lx_sync(); lx_sync();                                        // 2, 3 (barrier)
+    if (okf == 0) return;
+    // this wave's W_o rows, head g's columns: needed only after the merge
+    const int n0 = j * OROWS + w4 * ORW;
+    float wo[ORW][OU][OE];
+#pragma unroll
+    for (int r = 0; r < ORW; ++r)
+#pragma unroll
+      for (int u = 0; u < OU; ++u)
+        NL::load(a.wo, (size_t)(n0 + r) * (HQ * HD) + g * OCOL + (size_t)(u * 64 + lane) * OE, wo[r][u]);
+    lx_sync();                                                   // 4
+    lx_sync();                                                   // 5
+    lx_sync();                                                   // 6
+    // One slot: scores, chunk softmax, partial (o, max, sum) into pb.
+    auto attend = [&](int it) {
+      const int s = j + it * LX_PER;
+      const bool live = s < nsl;
+      const int m = s < nch0 ? 0 : 1, c = s < nch0 ? s : s - nch0;
+      const int Tm = m == 0 ? T0 : T1;
+      const int ctx = Tm + 1, tb = c * ATT_CHUNK;
+      const int n_t = live ? min(ATT_CHUNK, ctx - tb) : 0;
+      float4 kr[ATT_DPL / 4], vr[ATT_DPL / 4];
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        if constexpr (KBF) {
+          const uint32_t wk[4] = {kraw[i].x, kraw[i].y, kraw[i].z, kraw[i].w};
+          const uint32_t wv[4] = {vraw[i].x, vraw[i].y, vraw[i].z, vraw[i].w};
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            kr[2 * i + h] = make_float4(__uint_as_float(wk[2 * h] << 16), __uint_as_float(wk[2 * h] & 0xffff0000u),
+                                        __uint_as_float(wk[2 * h + 1] << 16), __uint_as_float(wk[2 * h + 1] & 0xffff0000u));
+            vr[2 * i + h] = make_float4(__uint_as_float(wv[2 * h] << 16), __uint_as_float(wv[2 * h] & 0xffff0000u),
+                                        __uint_as_float(wv[2 * h + 1] << 16), __uint_as_float(wv[2 * h + 1] & 0xffff0000u));
+          }
+        } else {
+          kr[i] = make_float4(__uint_as_float(kraw[i].x), __uint_as_float(kraw[i].y), __uint_as_float(kraw[i].z),
+                              __uint_as_float(kraw[i].w));
+          vr[i] = make_float4(__uint_as_float(vraw[i].x), __uint_as_float(vraw[i].y), __uint_as_float(vraw[i].z),
+                              __uint_as_float(vraw[i].w));
+        }
+      }
+      if (live && tb + tok == Tm) {   // the new token: not in the cache yet when loaded
+#pragma unroll
+        for (int i = 0; i < ATT_DPL / 4; ++i) {
+          const int d = sub * ATT_DPL + 4 * i;
+          kr[i] = make_float4(kn[m][d], kn[m][d + 1], kn[m][d + 2], kn[m][d + 3]);
+          vr[i] = make_float4(vn[m][d], vn[m][d + 1], vn[m][d + 2], vn[m][d + 3]);
+        }
+      }
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        const float* qg = &qs[m][gi * HD + sub * ATT_DPL];
+        float sdot = 0.f;
+#pragma unroll
+        for (int i = 0; i < ATT_DPL / 4; ++i) {
+          sdot = fmaf(qg[4 * i], kr[i].x, sdot);
+          sdot = fmaf(qg[4 * i + 1], kr[i].y, sdot);
+          sdot = fmaf(qg[4 * i + 2], kr[i].z, sdot);
+          sdot = fmaf(qg[4 * i + 3], kr[i].w, sdot);
+        }
+        sdot = group_sum_first(sdot, LPT);
+        if (sub == 0) sc[gi][tok] = tok < n_t ? sdot * a.scale : -INFINITY;
+      }
+      {
+        float4* vd = reinterpret_cast<float4*>(vs + (size_t)tok * HD + sub * ATT_DPL);
+        const bool ok = tok < n_t;
+#pragma unroll
+        for (int i = 0; i < ATT_DPL / 4; ++i) vd[i] = ok ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      lx_sync();                                                 // A
+      if (w4 < G) {   // chunk softmax statistics: one wave per q head, one lane per token
+        const float v = lane < ATT_CHUNK ? sc[w4][lane] : -INFINITY;
+        const float mx = wave_max_dpp(v);
+        const float ex = (lane < n_t) ? expf(v - mx) : 0.f;
+        const float l = wave_sum_dpp(ex);
+        if (lane < ATT_CHUNK) sc[w4][lane] = ex;
+        if (lane == 0) { stt[w4][0] = mx; stt[w4][1] = l; }
+      }
+      lx_sync();                                                 // B
+      {
+        const int gi = st / HD, d = st - gi * HD;
+        float o = 0.f;
+#pragma unroll 8
+        for (int tl = 0; tl < ATT_CHUNK; ++tl) o = fmaf(sc[gi][tl], vs[(size_t)tl * HD + d], o);
+        pb[gi][d] = o;
+        if (d < 2) pb[gi][HD + d] = stt[gi][d];
+      }
+      lx_sync();                                                 // C
+      lx_sync();                                                 // D
+    };
+    attend(0);   // the first slot apart, so waiting for its K/V does not wait for W_o
+    for (int it = 1; it < nit; ++it) {
+      const int s = j + it * LX_PER;
+      const bool live = s < nsl;
+      load_kv(live ? (s < nch0 ? 0 : 1) : 0, live ? (s < nch0 ? s : s - nch0) : 0);
+      attend(it);
+    }
+    lx_sync(); lx_sync();                                        // 7, 8 (barrier)
+    if (okf == 0) return;
+    merge();
+    lx_sync();                                                   // 9
+    float acc[ORW][M];
+#pragma unroll
+    for (int r = 0; r < ORW; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+#pragma unroll
+    for (int u = 0; u < OU; ++u) {
+      const int k0 = (u * 64 + lane) * OE;
+      float xv[M][OE];
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < OE; ++i) xv[m][i] = ash[m][k0 + i];
+#pragma unroll
+      for (int r = 0; r < ORW; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int i = 0; i < OE; ++i) acc[r][m] = fmaf(wo[r][u][i], xv[m][i], acc[r][m]);
+    }
+    static_assert(ORW * M == 16 || ORW * M == 32, "O rows per stream wave");
+    if constexpr (ORW * M == 16) {
+      const float v = lx_reduce<16, ORW>(acc, lane);   // word r * M + m in lanes [4 w, 4 w + 4)
+      const int wd = lane >> 2;
+      if ((lane & 3) == 0) a.pout[((size_t)g * M + (wd & 1)) * D + n0 + (wd >> 1)] = v;
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float part[ORW / 2][M];
+#pragma unroll
+        for (int r = 0; r < ORW / 2; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) part[r][m] = acc[h * (ORW / 2) + r][m];
+        const float v = lx_reduce<16, ORW / 2>(part, lane);
+        const int wd = lane >> 2;
+        if ((lane & 3) == 0) a.pout[((size_t)g * M + (wd & 1)) * D + n0 + h * (ORW / 2) + (wd >> 1)] = v;
+      }
+    }
+  } else {
+    // ===================== exchange waves =====================
+    // (the two roles start with different scheduling barriers, so no code of
+    // either is hoisted above the branch and made to wait for the other's loads)
+    __builtin_amdgcn_sched_barrier(0);
+    const int w4 = wave;
+    // norm gains and RoPE entries (needed after the q/k/v exchange)
+    const int t = tid, tr = t & 127, trow = t >> 7;
+    const float qw_r = a.q_norm[tr], kw_r = a.k_norm[tr];
+    const float2 cs_r = a.rope[(size_t)trow * (HD / 2) + (tr & (HD / 2 - 1))];
+    // this wave's q/k/v rows (the 512 rows of KV head g: q heads gG.., k, v)
+    const int r0 = j * (QRW * 4) + w4 * QRW;
+    const void* wb;
+    int wrow, ocol;
+    if (r0 < G * HD) { wb = a.wq; wrow = g * G * HD + r0; ocol = wrow; }
+    else if (r0 < (G + 1) * HD) { wb = a.wk; wrow = g * HD + r0 - G * HD; ocol = HQ * HD + wrow; }
+    else { wb = a.wv; wrow = g * HD + r0 - (G + 1) * HD; ocol = (HQ + HKV) * HD + wrow; }
+    uint4 w[QRW][NVQ];
+#pragma unroll
+    for (int r = 0; r < QRW; ++r)
+#pragma unroll
+      for (int jj = 0; jj < NVQ; ++jj) w[r][jj] = WL::raw(wb, (size_t)(wrow + r) * D + (size_t)(jj * 64 + lane) * VEC);
+    in.finish(xsh, gsh, ssq, tid, wave);
+    if (trow == 0) { qwn[tr] = qw_r; kwn[tr] = kw_r; }
+    if (tr < HD / 2) csh[trow][tr] = cs_r;
+    lx_sync();                                                   // 1
+    const unsigned ep0 = (unsigned)stsh[0][4], err0 = (unsigned)stsh[0][5];
+    rows_state(stsh[0][0], stsh[0][1], stsh[0][2], stsh[0][3]);
+    const float inv[M] = {lx_inv_rms<D>(ssq, 0, a.eps), lx_inv_rms<D>(ssq, 1, a.eps)};
+    if (blockIdx.x == 0)
+      for (int e = tid * 4; e < M * D; e += 256 * 4)
+        *reinterpret_cast<float4*>(a.xout + e) = *reinterpret_cast<const float4*>(xsh + e);
+    float acc[QRW][M];
+    lx_dots<D, QRW, WL>(w, xsh, gsh, inv, lane, acc);
+    {
+      const float v = lx_reduce<8, QRW>(acc, lane);   // word r * M + m in lanes [8 w, 8 w + 8)
+      const int wd = lane >> 3;
+      if ((lane & 7) == 0) a.qkv[(size_t)(wd & 1) * (HQ + 2 * HKV) * HD + ocol + (wd >> 1)] = v;
+    }
+    lx_wait_stores();
+    if (!lx_xcd_barrier(fl, j, ep0 + 1, deadline, err0, a.err, &okf)) return;   // 2, 3
+    // raw q (both rows, this head pair), new k and v
+    {
+      const int ldq = (HQ + 2 * HKV) * HD;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = t + 256 * i, m = e >> 8, o = e & 255;
+        qs[m][o] = lx_ld(a.qkv + (size_t)m * ldq + g * G * HD + o);
+      }
+      kn[trow][tr] = lx_ld(a.qkv + (size_t)trow * ldq + HQ * HD + g * HD + tr);
+      vn[trow][tr] = lx_ld(a.qkv + (size_t)trow * ldq + (HQ + HKV) * HD + g * HD + tr);
+    }
+    lx_sync();                                                   // 4
+    // Qwen3 per-head RMSNorm, then rotate-half RoPE: vectors (row, q head 0,
+    // q head 1, k) = 6, waves 0-3 take 0-3 and 4-5.  Lane l holds dims l and l + 64.
+    for (int vi = w4; vi < 3 * M; vi += 4) {
+      const int m = vi / 3, kind = vi % 3;
+      float* v = kind < G ? &qs[m][kind * HD] : kn[m];
+      const float x1 = v[lane], x2 = v[lane + 64];
+      const float ssum = wave_sum_dpp(fmaf(x1, x1, x2 * x2));
+      const float rinv = 1.0f / sqrtf(ssum / (float)HD + a.eps);
+      const float* wn = kind < G ? qwn : kwn;
+      const float g1 = wn[lane], g2 = wn[lane + 64];
+      const float2 cs = csh[m][lane];
+      const float y1 = g1 * (x1 * rinv), y2 = g2 * (x2 * rinv);
+      v[lane] = y1 * cs.x - y2 * cs.y;
+      v[lane + 64] = y2 * cs.x + y1 * cs.y;
+    }
+    lx_sync();                                                   // 5
+    // append the new token (workgroup owning each row's last chunk); a BF16
+    // cache stores it rounded and this step attends to the rounded values
+    {
+      const int m = trow, d = tr;
+      const int nchm = m == 0 ? nch0 : nch1, Tm = m == 0 ? T0 : T1;
+      const int slast = (m == 0 ? 0 : nch0) + nchm - 1;
+      if (nchm > 0 && slast % LX_PER == j) {
+        const size_t off = (((size_t)m * HKV + g) * a.max_ctx + Tm) * HD + d;
+        if constexpr (KBF) {
+          static_cast<uint16_t*>(a.kc)[off] = (uint16_t)bf16_bits(kn[m][d]);
+          static_cast<uint16_t*>(a.vc)[off] = (uint16_t)bf16_bits(vn[m][d]);
+        } else {
+          static_cast<float*>(a.kc)[off] = kn[m][d];
+          static_cast<float*>(a.vc)[off] = vn[m][d];
+        }
+      }
+      if constexpr (KBF) {   // each thread rounds the element it appended
+        kn[m][d] = bf16_round(kn[m][d]);
+        vn[m][d] = bf16_round(vn[m][d]);
+      }
+    }
+    lx_sync();                                                   // 6
+    for (int it = 0; it < nit; ++it) {
+      lx_sync();                                                 // A: scores, V in LDS
+      lx_sync();                                                 // B: softmax
+      lx_sync();                                                 // C: partials in pb
+      const int s = j + it * LX_PER;
+      if (s < nsl) {
+        const int m = s < nch0 ? 0 : 1, c = s < nch0 ? s : s - nch0;
+        for (int e = t; e < G * (HD + 2); e += 256) {
+          const int gi = e / (HD + 2), o = e - gi * (HD + 2);
+          a.part[(((size_t)m * HQ + g * G + gi) * a.max_chunks + c) * PS + o] = pb[gi][o];
+        }
+      }
+      lx_sync();                                                 // D
+    }
+    lx_wait_stores();
+    if (!lx_xcd_barrier(fl, j, ep0 + 2, deadline, err0, a.err, &okf)) return;   // 7, 8
+    merge();
+    lx_sync();                                                   // 9
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MLP half of a layer.  Grid LX_WGS, block LX_NT.  XCD g owns inner indices
+// [g I/8, (g+1) I/8); workgroup j of it IW = I/256 of them, IPW per
+// exchange wave; the stream waves hold the down projection's rows.
+template <typename WL, int D, int I>
+__global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
+  constexpr int M = LX_M, VEC = WL::VEC, NV = D / (64 * VEC);
+  constexpr int IX = I / LX_XCDS, IW = IX / LX_PER;
+  constexpr int GUW = 4;
+  constexpr int IPW = IW / GUW;                       // inner indices per gate/up wave
+  constexpr int DROWS = D / LX_PER, DRW = DROWS / 4;  // down rows per workgroup / stream wave
+  constexpr int DE = lx_col_elems<WL>(IX);
+  using NL = LxCols<WL, DE>;
+  constexpr int DU = IX / (64 * DE);                  // column units per lane per down row
+  static_assert(IW % 4 == 0 && IPW * GUW == IW && IX % (64 * DE) == 0 && DRW * 4 == DROWS, "lx_mlp_kernel shape");
+
+  __shared__ __attribute__((aligned(16))) float xsh[M * D];
+  __shared__ __attribute__((aligned(16))) float gsh[D];
+  __shared__ float ssq[8];
+  __shared__ __attribute__((aligned(16))) float ash[M][IX];   // the XCD's slice
+  __shared__ int stsh[2][2];   // row 0: barrier epoch, error word (loaded by the stream waves)
+  __shared__ int okf;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lx_xcd(), j = blockIdx.x >> 3;
+  const unsigned long long deadline = __builtin_amdgcn_s_memrealtime() + a.spin_ticks;
+  unsigned* fl = a.flags + g * LX_FLAGS;
+  LxInput<D> in;
+  in.issue(a, tid);
+  const int i0 = g * IX + j * IW;                     // first inner index of this workgroup
+  auto gate_up = [&](int gw, float& act) {             // gate/up wave gw (0..GUW-1)
+    uint4 w[2 * IPW][NV];
+    const int ib = i0 + gw * IPW;
+#pragma unroll
+    for (int r = 0; r < IPW; ++r)
+#pragma unroll
+      for (int jj = 0; jj < NV; ++jj) {
+        w[2 * r][jj] = WL::raw(a.wg, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
+        w[2 * r + 1][jj] = WL::raw(a.wu, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
+      }
+    in.finish(xsh, gsh, ssq, tid, wave);
+    lx_sync();                                                   // 1
+    const float inv[M] = {lx_inv_rms<D>(ssq, 0, a.eps), lx_inv_rms<D>(ssq, 1, a.eps)};
+    float acc[2 * IPW][M];
+    lx_dots<D, 2 * IPW, WL>(w, xsh, gsh, inv, lane, acc);
+    // word (2 i + gate/up) M + m = 4 i + 2 gu + m: lanes [4 w, 4 w + 4); the
+    // up word of a gate word sits 8 lanes further on
+    static_assert(2 * IPW * M <= 16, "gate/up rows per wave");
+    const float x = lx_reduce<16, 2 * IPW>(acc, lane);
+    const float u = __shfl(x, (lane + 8) & 63, 64);
+    const int wd = lane >> 2;
+    act = x / (1.0f + expf(-x)) * u;   // valid in lanes with (wd & 2) == 0: i = wd >> 2, m = wd & 1
+  };
+
+  if (wave < 4) {
+    // ===================== exchange waves =====================
+    // (the two roles start with different scheduling barriers, so no code of
+    // either is hoisted above the branch and made to wait for the other's loads)
+    __builtin_amdgcn_sched_barrier(0);
+    float act;
+    gate_up(wave, act);
+    if (blockIdx.x == 0)
+      for (int e = tid * 4; e < M * D; e += 256 * 4)
+        *reinterpret_cast<float4*>(a.xout + e) = *reinterpret_cast<const float4*>(xsh + e);
+    {
+      const int wd = lane >> 2, i = wd >> 2, m = wd & 1;
+      if ((lane & 3) == 0 && (wd & 2) == 0 && i < IPW) a.act[(size_t)m * a.ld_act + i0 + wave * IPW + i] = act;
+    }
+    lx_wait_stores();
+    const unsigned ep0 = (unsigned)stsh[0][0], err0 = (unsigned)stsh[0][1];
+    if (!lx_xcd_barrier(fl, j, ep0 + 1, deadline, err0, a.err, &okf)) return;   // 2, 3
+    {
+      constexpr int PT = M * IX / 256;                           // loads per thread, all issued first
+      static_assert(M * IX % 256 == 0, "act slice per exchange thread");
+      float v[PT];
+#pragma unroll
+      for (int q = 0; q < PT; ++q) {
+        const int e = tid + 256 * q, m = e / IX, k = e - m * IX;
+        v[q] = lx_ld(a.act + (size_t)m * a.ld_act + g * IX + k);
+      }
+#pragma unroll
+      for (int q = 0; q < PT; ++q) {
+        const int e = tid + 256 * q, m = e / IX, k = e - m * IX;
+        ash[m][k] = v[q];
+      }
+    }
+    lx_sync();                                                   // 4
+  } else {
+    // ===================== stream waves =====================
+    __builtin_amdgcn_sched_barrier(1);
+    const int w4 = wave - 4;
+    // down rows of this wave, slice g's columns: issued after the gate/up
+    // stream so that it reaches HBM first
+    const int n0 = j * DROWS + w4 * DRW;
+    float wd[DRW][DU][DE];
+    {
+      const unsigned ep = fl[j], er = *a.err;
+      in.finish(xsh, gsh, ssq, tid, wave);
+      int* sd = stsh[tid == 256 ? 0 : 1];   // no branch to sink the loads into
+      sd[0] = (int)ep; sd[1] = (int)er;
+      lx_sync();                                                 // 1
+    }
+#pragma unroll
+    for (int r = 0; r < DRW; ++r)
+#pragma unroll
+      for (int u = 0; u < DU; ++u)
+        NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE, wd[r][u]);
+    lx_sync(); lx_sync();                                        // 2, 3 (barrier)
+    if (okf == 0) return;
+    lx_sync();                                                   // 4
+    float acc[DRW][M];
+#pragma unroll
+    for (int r = 0; r < DRW; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+#pragma unroll
+    for (int u = 0; u < DU; ++u) {
+      const int k0 = (u * 64 + lane) * DE;
+      float xv[M][DE];
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < DE; ++i) xv[m][i] = ash[m][k0 + i];
+#pragma unroll
+      for (int r = 0; r < DRW; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int i = 0; i < DE; ++i) acc[r][m] = fmaf(wd[r][u][i], xv[m][i], acc[r][m]);
+    }
+    static_assert(DRW * M == 16 || DRW * M == 32, "down rows per stream wave");
+#pragma unroll
+    for (int h = 0; h < DRW * M / 16; ++h) {
+      float part[8][M];
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) part[r][m] = acc[h * 8 + r][m];
+      const float v = lx_reduce<16, 8>(part, lane);   // word r * M + m in lanes [4 w, 4 w + 4)
+      const int wd = lane >> 2;
+      if ((lane & 3) == 0) a.pout[((size_t)g * M + (wd & 1)) * D + n0 + h * 8 + (wd >> 1)] = v;
+    }
+  }
+}
+
+}  // namespace
+}  // namespace sk

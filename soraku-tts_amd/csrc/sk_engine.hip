@@ -492,7 +492,7 @@ hipError_t launch_attn_stream(sk_engine* e, const AttnArgs& at) {
 bool lx_fits(const sk_engine* e) {
   const sk_config& c = e->c;
   return e->rows == LX_M && !e->wide && e->attn_splits == 0 && c.n_kv_heads == LX_HKV && c.n_q_heads == LX_HQ &&
-         c.head_dim == LX_HD && c.d_model == 1024 && c.trunk_inter == 3072;
+         c.head_dim == LX_HD && c.d_model == 1024 && c.trunk_inter == 3072 && e->max_chunks <= LX_MAXCH;
 }
 
 template <typename WL, typename KT>
@@ -1109,8 +1109,8 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   }
   if (he == hipSuccess && e->lx) {
     const size_t pe = (size_t)LX_XCDS * R * d;
-    he = dalloc(&e->lx_xl, R * d);
-    if (he == hipSuccess) he = dalloc(&e->lx_xm, R * d);
+    he = dalloc(&e->lx_xl, pe);   // one copy of the residual stream per XCD
+    if (he == hipSuccess) he = dalloc(&e->lx_xm, pe);
     if (he == hipSuccess) he = dalloc(&e->lx_opart, pe);
     if (he == hipSuccess) he = dalloc(&e->lx_dpart, pe);
     if (he == hipSuccess) he = dalloc(&e->lx_zero, pe);

@@ -58,6 +58,7 @@ constexpr int LX_M = 2, LX_HD = 128, LX_G = 2, LX_HKV = 8, LX_HQ = LX_G * LX_HKV
 // A barrier wait longer than this (50 ms of the 100 MHz real-time counter)
 // ends the launch with an error instead of waiting further.
 constexpr unsigned long long LX_SPIN_TICKS = 5000000ull;
+constexpr int LX_MAXCH = 128;                   // attention chunks per row (max_ctx <= 4096)
 
 struct LxArgs {
   const void* wq; const void* wk; const void* wv; const void* wo;   // [out][in], weight dtype
@@ -66,7 +67,7 @@ struct LxArgs {
   const float* q_norm; const float* k_norm;
   const float* xin;                  // [M][D] residual stream entering the launch
   const float* pin;                  // [8][M][D] partials to add (zeros for the first layer)
-  float* xout;                       // [M][D] xin + sum(pin), written by workgroup 0
+  float* xout;                       // [8][M][D] xin + sum(pin), one copy per XCD (copy 0 is read next)
   float* pout;                       // [8][M][D] this launch's partials
   float* qkv;                        // [M][(HQ + 2 HKV) HD] raw projections (exchanged)
   float* part;                       // [M][HQ][max_chunks][HD + 4] chunk partials (exchanged)
@@ -108,16 +109,17 @@ __device__ __forceinline__ void lx_wait_stores() {
 // against 0.96 us for agent-scope loads).
 __device__ __forceinline__ float lx_ld(const float* p) { return *p; }
 
-// The 32 workgroups of this XCD meet.  The exchange waves have waited for
-// their stores; wave 0 stores this workgroup's epoch and polls all 32.
-// Returns false (uniformly) on a timeout, or when err0 (the error word as the
-// launch found it) is set.
+// The 32 workgroups of this XCD meet.  The waves that stored the data being
+// exchanged have waited for their stores; wave `poller` (one with no load in
+// flight) stores this workgroup's epoch and polls all 32, the other waves
+// only pass the two LDS barriers.  Returns false (uniformly) on a timeout, or
+// when err0 (the error word as the launch found it) is set.
 __device__ __forceinline__ bool lx_xcd_barrier(unsigned* fl, int j, unsigned target, unsigned long long deadline,
-                                               unsigned err0, unsigned* err, int* okf) {
+                                               unsigned err0, unsigned* err, int* okf, int poller) {
   lx_sync();
   const int tid = threadIdx.x;
-  if (tid < 64) {
-    if (tid == 0) __hip_atomic_store(fl + j, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if ((tid >> 6) == poller) {
+    if ((tid & 63) == 0) __hip_atomic_store(fl + j, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     int good = 1;
     for (;;) {
       const unsigned v = __hip_atomic_load(fl + (tid & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -125,7 +127,7 @@ __device__ __forceinline__ bool lx_xcd_barrier(unsigned* fl, int j, unsigned tar
       if (__builtin_amdgcn_s_memrealtime() > deadline) { good = 0; break; }
     }
     if (err0 != 0u) good = 0;   // an earlier launch failed: leave at once
-    if (tid == 0) {
+    if ((tid & 63) == 0) {
       *okf = good;
       if (!good) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
@@ -134,66 +136,63 @@ __device__ __forceinline__ bool lx_xcd_barrier(unsigned* fl, int j, unsigned tar
   return *okf != 0;
 }
 
-// Input of a launch: x = xin + pin[0] + ... + pin[7] for both rows, EPT
-// consecutive elements per thread (a wave's elements lie in one row), and the
-// RMSNorm gain.  issue() only loads; finish() sums, stores x (pre-norm) and
-// the gain to LDS and each wave's sum of squares to ssq[wave].
+// Input of a launch, gathered by the stream waves (threads 256..511) of the
+// XCD's 32 workgroups together.  Workgroup j sums its 1/32 slice of
+// x = xin + pin[0] + ... + pin[7] (both rows, M D / 32 elements, in that
+// order) into the XCD's copy xout[g]; after an XCD barrier every workgroup
+// reads the whole copy from the L2 into LDS (xsh, before the norm) with each
+// stream wave's sum of squares (ssq[w4]), and the norm gain into gsh.  Per CU
+// that is ~10 KB of loads instead of the 9 whole vectors (74 KB at d = 1024)
+// a workgroup read when it summed alone, on the CU path its weight stream
+// uses too.  All 8 copies are equal; the next launch reads copy 0.
 template <int D>
 struct LxInput {
-  static constexpr int EPT = LX_M * D / LX_NT;   // 4 or 8
-  static constexpr int GPT = D / LX_NT;          // 2 or 4
-  static_assert(EPT % 4 == 0 && (GPT == 2 || GPT == 4) && (64 * EPT) <= D, "LxInput shape");
-  float4 v[9][EPT / 4];
-  float gv[GPT];
-  __device__ __forceinline__ void issue(const LxArgs& a, int tid) {
-    const size_t e0 = (size_t)tid * EPT;
+  static constexpr int SL = LX_M * D / LX_PER;   // slice elements per workgroup: 64 or 128
+  static constexpr int EPT = LX_M * D / 256;     // elements per stream thread in the whole copy
+  static constexpr int GPT = D / 256;            // gain elements per stream thread
+  static_assert(SL <= 256 && EPT % 4 == 0 && GPT % 4 == 0 && 64 * EPT <= D, "LxInput shape");
+  float sv[9];
+  float4 gv[GPT / 4];
+  __device__ __forceinline__ void issue(const LxArgs& a, int st, int j) {
+    const size_t e = (size_t)j * SL + min(st, SL - 1);   // threads past the slice re-read its last element
+    sv[0] = a.xin[e];
 #pragma unroll
-    for (int i = 0; i < EPT / 4; ++i) v[0][i] = *reinterpret_cast<const float4*>(a.xin + e0 + 4 * i);
+    for (int h = 0; h < 8; ++h) sv[1 + h] = a.pin[(size_t)h * LX_M * D + e];
 #pragma unroll
-    for (int h = 0; h < 8; ++h)
-#pragma unroll
-      for (int i = 0; i < EPT / 4; ++i)
-        v[1 + h][i] = *reinterpret_cast<const float4*>(a.pin + (size_t)h * LX_M * D + e0 + 4 * i);
-    if constexpr (GPT == 2) {
-      const float2 t = *reinterpret_cast<const float2*>(a.gain + tid * 2);
-      gv[0] = t.x; gv[1] = t.y;
-    } else {
-      const float4 t = *reinterpret_cast<const float4*>(a.gain + tid * 4);
-      gv[0] = t.x; gv[1] = t.y; gv[2] = t.z; gv[3] = t.w;
-    }
+    for (int i = 0; i < GPT / 4; ++i) gv[i] = *reinterpret_cast<const float4*>(a.gain + st * GPT + 4 * i);
   }
-  __device__ __forceinline__ void finish(float* xsh, float* gsh, float* ssq, int tid, int wave) {
-    // The loaded values enter the sums only here, inside each role's code: the
-    // compiler may not start the sums (and wait for these loads) above the
-    // role branch, ahead of the role's weight stream.
+  // the slice's sum to the XCD copy, the gain to LDS (nothing is held across
+  // the barrier that follows)
+  __device__ __forceinline__ void slice(const LxArgs& a, int g, int st, int j, float* gsh) {
 #pragma unroll
-    for (int h = 0; h < 9; ++h)
+    for (int i = 0; i < GPT / 4; ++i) *reinterpret_cast<float4*>(gsh + st * GPT + 4 * i) = gv[i];
+    float s = sv[0];
 #pragma unroll
-      for (int i = 0; i < EPT / 4; ++i) asm volatile("" : "+v"(v[h][i].x), "+v"(v[h][i].y), "+v"(v[h][i].z), "+v"(v[h][i].w));
+    for (int h = 1; h < 9; ++h) s = __fadd_rn(s, sv[h]);
+    // every thread stores (threads past the slice repeat its last element)
+    a.xout[(size_t)g * LX_M * D + (size_t)j * SL + min(st, SL - 1)] = s;
+  }
+  __device__ __forceinline__ void gather(const LxArgs& a, int g, int st, int w4, float* xsh, float* ssq) {
+    const float* src = a.xout + (size_t)g * LX_M * D + (size_t)st * EPT;
+    float4 v[EPT / 4];
+#pragma unroll
+    for (int i = 0; i < EPT / 4; ++i) v[i] = *reinterpret_cast<const float4*>(src + 4 * i);
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < EPT / 4; ++i) {
-      float4 s = v[0][i];
-#pragma unroll
-      for (int h = 1; h < 9; ++h) {
-        s.x = __fadd_rn(s.x, v[h][i].x); s.y = __fadd_rn(s.y, v[h][i].y);
-        s.z = __fadd_rn(s.z, v[h][i].z); s.w = __fadd_rn(s.w, v[h][i].w);
-      }
-      *reinterpret_cast<float4*>(xsh + tid * EPT + 4 * i) = s;
-      ss = fmaf(s.x, s.x, ss); ss = fmaf(s.y, s.y, ss); ss = fmaf(s.z, s.z, ss); ss = fmaf(s.w, s.w, ss);
+      *reinterpret_cast<float4*>(xsh + st * EPT + 4 * i) = v[i];
+      ss = fmaf(v[i].x, v[i].x, ss); ss = fmaf(v[i].y, v[i].y, ss);
+      ss = fmaf(v[i].z, v[i].z, ss); ss = fmaf(v[i].w, v[i].w, ss);
     }
-#pragma unroll
-    for (int i = 0; i < GPT; ++i) gsh[tid * GPT + i] = gv[i];
     ss = wave_sum_dpp(ss);
-    if ((tid & 63) == 0) ssq[wave] = ss;
+    if ((st & 63) == 0) ssq[w4] = ss;
   }
 };
 
-// 1 / rms of row m from the per-wave sums (waves 4m .. 4m+3 hold row m).
+// 1 / rms of row m from the stream waves' sums (stream waves 2m, 2m+1 hold row m).
 template <int D>
 __device__ __forceinline__ float lx_inv_rms(const float* ssq, int m, float eps) {
-  const float s = ((ssq[4 * m] + ssq[4 * m + 1]) + ssq[4 * m + 2]) + ssq[4 * m + 3];
-  return 1.0f / sqrtf(s / (float)D + eps);
+  return 1.0f / sqrtf((ssq[2 * m] + ssq[2 * m + 1]) / (float)D + eps);
 }
 
 // RW rows of a GEMV over K = D against the normalized input rows held in LDS:
@@ -311,6 +310,8 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
   __shared__ float qwn[HD], kwn[HD];
   __shared__ float2 csh[M][HD / 2];
   __shared__ int stsh[2][6];   // row 0: kv_len[0..1], active[0..1], barrier epoch, error word
+  __shared__ float mw[2 * G][LX_MAXCH];   // chunk weights of each (row, head) pair
+  __shared__ float mil[2 * G];
   __shared__ int okf;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -333,42 +334,53 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     nsl = nch0 + nch1;
     nit = (nsl + LX_PER - 1) / LX_PER;              // slots per workgroup (one bound for all)
   };
-  LxInput<D> in;
-  in.issue(a, tid);
-  // Chunk merge after the second barrier, by all 8 waves: thread t -> row
-  // t >> 8, head (t >> 7) & 1 of the pair, dim t & 127; up to 16 chunks'
-  // partials per batch of loads, merged in chunk order with a running max.
+  // Chunk merge after the third barrier, by all 8 waves: every thread issues
+  // its output's first 16 chunk partials (row tid >> 8, head (tid >> 7) & 1
+  // of the pair, dim tid & 127) while wave 0 turns each (row, head) pair's
+  // chunk maxima and sums into weights exp(m_c - M) and 1 / sum_c l_c
+  // exp(m_c - M) in LDS (mw, mil); then O = sum_c w_c o_c in chunk order.
   auto merge = [&]() {
-    const int m = tid >> 8, gi = (tid >> 7) & 1, d = tid & (HD - 1);
+    const int m = tid >> 8, gi = (tid >> 7) & 1, d = tid & (HD - 1), pr = 2 * m + gi;
     const int nch = m == 0 ? nch0 : nch1;
-    const float* pp = a.part + (((size_t)m * HQ + g * G + gi) * a.max_chunks) * PS;
-    float Mr = -INFINITY, L = 0.f, O = 0.f;
+    const float* pp = a.part + (((size_t)m * HQ + g * G + gi) * a.max_chunks) * PS + d;
     constexpr int CB = 16;
-    for (int c0 = 0; c0 < nch; c0 += CB) {
-      float2 ml[CB];
-      float ov[CB];
+    float ov[CB];
 #pragma unroll
-      for (int q = 0; q < CB; ++q) {
-        const float* pc = pp + (size_t)min(c0 + q, nch - 1) * PS;
-        ml[q] = *reinterpret_cast<const float2*>(pc + HD);
-        ov[q] = lx_ld(pc + d);
-      }
-      float Mb = Mr;
+    for (int q = 0; q < CB; ++q) ov[q] = lx_ld(pp + (size_t)min(q, max(nch - 1, 0)) * PS);
+    if (wave == 0) {   // lane = (pair p, chunk c within a block of 16)
+      const int p = lane >> 4, c = lane & 15, pm = p >> 1;
+      const int pn = pm == 0 ? nch0 : nch1, nmax = max(nch0, nch1);
+      const float* pq = a.part + (((size_t)pm * HQ + g * G + (p & 1)) * a.max_chunks) * PS + HD;
+      const float2 v0 = *reinterpret_cast<const float2*>(pq + (size_t)min(c, max(pn - 1, 0)) * PS);
+      float mx = c < pn ? v0.x : -INFINITY;
+      for (int c0 = CB; c0 < nmax; c0 += CB)
+        if (c0 + c < pn) mx = fmaxf(mx, lx_ld(pq + (size_t)(c0 + c) * PS));
 #pragma unroll
-      for (int q = 0; q < CB; ++q)
-        if (c0 + q < nch) Mb = fmaxf(Mb, ml[q].x);
-      const float rs = expf(Mr - Mb);   // 0 on the first block
-      L *= rs; O *= rs;
-#pragma unroll
-      for (int q = 0; q < CB; ++q)
-        if (c0 + q < nch) {
-          const float e = expf(ml[q].x - Mb);
-          L = fmaf(ml[q].y, e, L);
-          O = fmaf(ov[q], e, O);
+      for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      const float e0 = c < pn ? expf(v0.x - mx) : 0.f;
+      float l = v0.y * e0;
+      if (c < pn) mw[p][c] = e0;
+      for (int c0 = CB; c0 < nmax; c0 += CB)
+        if (c0 + c < pn) {
+          const float2 v = *reinterpret_cast<const float2*>(pq + (size_t)(c0 + c) * PS);
+          const float e = expf(v.x - mx);
+          l = fmaf(v.y, e, l);
+          mw[p][c0 + c] = e;
         }
-      Mr = Mb;
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+      if (c == 0) mil[p] = pn ? 1.0f / l : 0.f;
     }
-    ash[m][gi * HD + d] = nch ? O / L : 0.f;
+    lx_sync();
+    float O = 0.f;
+#pragma unroll
+    for (int q = 0; q < CB; ++q)
+      if (q < nch) O = fmaf(mw[pr][q], ov[q], O);
+    for (int c0 = CB; c0 < nch; c0 += CB)
+#pragma unroll
+      for (int q = 0; q < CB; ++q)
+        if (c0 + q < nch) O = fmaf(mw[pr][c0 + q], lx_ld(pp + (size_t)(c0 + q) * PS), O);
+    ash[m][gi * HD + d] = O * mil[pr];
   };
 
   if (wave >= 4) {
@@ -376,15 +388,21 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     __builtin_amdgcn_sched_barrier(1);
     const int w4 = wave - 4, st = tid - 256;
     const int tok = st / LPT, sub = st % LPT;
+    LxInput<D> in;
+    unsigned ep, er;
     {
       const int t0 = a.kv_len[0], t1 = a.kv_len[1], a0 = a.active[0], a1 = a.active[1];
-      const unsigned ep = fl[j], er = *a.err;
+      ep = fl[j]; er = *a.err;
+      in.issue(a, st, j);
       rows_state(t0, t1, a0, a1);
       // every stream thread writes (thread 0 to row 0, the rest to row 1):
       // no branch for the compiler to sink these loads into
       int* sd = stsh[st == 0 ? 0 : 1];
       sd[0] = t0; sd[1] = t1; sd[2] = a0; sd[3] = a1; sd[4] = (int)ep; sd[5] = (int)er;
     }
+    in.slice(a, g, st, j, gsh);
+    lx_wait_stores();
+    if (!lx_xcd_barrier(fl, j, ep + 1, deadline, er, a.err, &okf, 4)) return;   // input barrier
     // K/V of this workgroup's first slot (clamped into the cache when the
     // slot does not exist; then unused)
     const int s0 = j < nsl ? j : 0;
@@ -398,7 +416,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
 #pragma unroll
       for (int i = 0; i < NLD; ++i) { kraw[i] = kp[i]; vraw[i] = vp[i]; }
     };
-    in.finish(xsh, gsh, ssq, tid, wave);
+    in.gather(a, g, st, w4, xsh, ssq);
     lx_sync();                                                   // 1
     // The first slot's K/V, issued once the exchange waves' q/k/v weights
     // are in flight (the projections are on the critical path; the cache rows
@@ -565,16 +583,13 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     for (int r = 0; r < QRW; ++r)
 #pragma unroll
       for (int jj = 0; jj < NVQ; ++jj) w[r][jj] = WL::raw(wb, (size_t)(wrow + r) * D + (size_t)(jj * 64 + lane) * VEC);
-    in.finish(xsh, gsh, ssq, tid, wave);
+    if (!lx_xcd_barrier(fl, j, 0u, deadline, 0u, a.err, &okf, 4)) return;   // input barrier (stream wave 4 polls)
     if (trow == 0) { qwn[tr] = qw_r; kwn[tr] = kw_r; }
     if (tr < HD / 2) csh[trow][tr] = cs_r;
     lx_sync();                                                   // 1
     const unsigned ep0 = (unsigned)stsh[0][4], err0 = (unsigned)stsh[0][5];
     rows_state(stsh[0][0], stsh[0][1], stsh[0][2], stsh[0][3]);
     const float inv[M] = {lx_inv_rms<D>(ssq, 0, a.eps), lx_inv_rms<D>(ssq, 1, a.eps)};
-    if (blockIdx.x == 0)
-      for (int e = tid * 4; e < M * D; e += 256 * 4)
-        *reinterpret_cast<float4*>(a.xout + e) = *reinterpret_cast<const float4*>(xsh + e);
     float acc[QRW][M];
     lx_dots<D, QRW, WL>(w, xsh, gsh, inv, lane, acc);
     {
@@ -583,7 +598,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       if ((lane & 7) == 0) a.qkv[(size_t)(wd & 1) * (HQ + 2 * HKV) * HD + ocol + (wd >> 1)] = v;
     }
     lx_wait_stores();
-    if (!lx_xcd_barrier(fl, j, ep0 + 1, deadline, err0, a.err, &okf)) return;   // 2, 3
+    if (!lx_xcd_barrier(fl, j, ep0 + 2, deadline, err0, a.err, &okf, 0)) return;   // 2, 3
     // raw q (both rows, this head pair), new k and v
     {
       const int ldq = (HQ + 2 * HKV) * HD;
@@ -649,7 +664,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       lx_sync();                                                 // D
     }
     lx_wait_stores();
-    if (!lx_xcd_barrier(fl, j, ep0 + 2, deadline, err0, a.err, &okf)) return;   // 7, 8
+    if (!lx_xcd_barrier(fl, j, ep0 + 3, deadline, err0, a.err, &okf, 0)) return;   // 7, 8
     merge();
     lx_sync();                                                   // 9
   }
@@ -683,10 +698,11 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
   const int g = lx_xcd(), j = blockIdx.x >> 3;
   const unsigned long long deadline = __builtin_amdgcn_s_memrealtime() + a.spin_ticks;
   unsigned* fl = a.flags + g * LX_FLAGS;
-  LxInput<D> in;
-  in.issue(a, tid);
   const int i0 = g * IX + j * IW;                     // first inner index of this workgroup
-  auto gate_up = [&](int gw, float& act) {             // gate/up wave gw (0..GUW-1)
+  // gate/up wave gw (0..GUW-1): its weight rows are issued, then it joins
+  // the input barrier (stream wave 4 polls) and the LDS barrier after which
+  // the input is in LDS
+  auto gate_up = [&](int gw, float& act) {
     uint4 w[2 * IPW][NV];
     const int ib = i0 + gw * IPW;
 #pragma unroll
@@ -696,7 +712,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
         w[2 * r][jj] = WL::raw(a.wg, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
         w[2 * r + 1][jj] = WL::raw(a.wu, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
       }
-    in.finish(xsh, gsh, ssq, tid, wave);
+    if (!lx_xcd_barrier(fl, j, 0u, deadline, 0u, a.err, &okf, 4)) return false;   // input barrier
     lx_sync();                                                   // 1
     const float inv[M] = {lx_inv_rms<D>(ssq, 0, a.eps), lx_inv_rms<D>(ssq, 1, a.eps)};
     float acc[2 * IPW][M];
@@ -708,6 +724,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
     const float u = __shfl(x, (lane + 8) & 63, 64);
     const int wd = lane >> 2;
     act = x / (1.0f + expf(-x)) * u;   // valid in lanes with (wd & 2) == 0: i = wd >> 2, m = wd & 1
+    return true;
   };
 
   if (wave < 4) {
@@ -716,17 +733,14 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
     // either is hoisted above the branch and made to wait for the other's loads)
     __builtin_amdgcn_sched_barrier(0);
     float act;
-    gate_up(wave, act);
-    if (blockIdx.x == 0)
-      for (int e = tid * 4; e < M * D; e += 256 * 4)
-        *reinterpret_cast<float4*>(a.xout + e) = *reinterpret_cast<const float4*>(xsh + e);
+    if (!gate_up(wave, act)) return;
     {
       const int wd = lane >> 2, i = wd >> 2, m = wd & 1;
       if ((lane & 3) == 0 && (wd & 2) == 0 && i < IPW) a.act[(size_t)m * a.ld_act + i0 + wave * IPW + i] = act;
     }
     lx_wait_stores();
     const unsigned ep0 = (unsigned)stsh[0][0], err0 = (unsigned)stsh[0][1];
-    if (!lx_xcd_barrier(fl, j, ep0 + 1, deadline, err0, a.err, &okf)) return;   // 2, 3
+    if (!lx_xcd_barrier(fl, j, ep0 + 2, deadline, err0, a.err, &okf, 0)) return;   // 2, 3
     {
       constexpr int PT = M * IX / 256;                           // loads per thread, all issued first
       static_assert(M * IX % 256 == 0, "act slice per exchange thread");
@@ -752,10 +766,16 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
     const int n0 = j * DROWS + w4 * DRW;
     float wd[DRW][DU][DE];
     {
+      const int st = tid - 256;
+      LxInput<D> in;
       const unsigned ep = fl[j], er = *a.err;
-      in.finish(xsh, gsh, ssq, tid, wave);
-      int* sd = stsh[tid == 256 ? 0 : 1];   // no branch to sink the loads into
+      in.issue(a, st, j);
+      int* sd = stsh[st == 0 ? 0 : 1];   // no branch to sink the loads into
       sd[0] = (int)ep; sd[1] = (int)er;
+      in.slice(a, g, st, j, gsh);
+      lx_wait_stores();
+      if (!lx_xcd_barrier(fl, j, ep + 1, deadline, er, a.err, &okf, 4)) return;   // input barrier
+      in.gather(a, g, st, w4, xsh, ssq);
       lx_sync();                                                 // 1
     }
 #pragma unroll

@@ -183,6 +183,7 @@ struct sk_engine {
   // barrier epochs and the error word (nonzero: a barrier timed out).
   bool lx = false;
   float *lx_xl = nullptr, *lx_xm = nullptr, *lx_opart = nullptr, *lx_dpart = nullptr, *lx_zero = nullptr;
+  uint2 *lx_qkv = nullptr, *lx_act = nullptr;   // tagged exchange words (zeroed at creation)
   unsigned *lx_flags = nullptr, *lx_err = nullptr;
 
   // batched prefill activations, sized for the largest packed prefix so far
@@ -515,7 +516,7 @@ hipError_t enqueue_trunk_lx(sk_engine* e) {
     A.xin = l == 0 ? e->x : e->lx_xm;
     A.pin = l == 0 ? e->lx_zero : e->lx_dpart;
     A.xout = e->lx_xl; A.pout = e->lx_opart;
-    A.qkv = e->qkv; A.part = e->part; A.act = e->act; A.ld_act = e->inner_max;
+    A.qkv = e->lx_qkv; A.part = e->part; A.act = e->lx_act; A.ld_act = c.trunk_inter;
     A.kc = e->kc + (size_t)l * kv_layer_bytes(e);
     A.vc = e->vc + (size_t)l * kv_layer_bytes(e);
     A.rope = e->rope; A.kv_len = e->kv_len; A.active = e->active;
@@ -1116,6 +1117,11 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     if (he == hipSuccess) he = dalloc(&e->lx_zero, pe);
     if (he == hipSuccess) he = dalloc(&e->lx_flags, (size_t)LX_XCDS * LX_FLAGS);
     if (he == hipSuccess) he = dalloc(&e->lx_err, 1);
+    const size_t nqkv = (size_t)R * (c.n_q_heads + 2 * c.n_kv_heads) * c.head_dim, nact = (size_t)R * c.trunk_inter;
+    if (he == hipSuccess) he = dalloc(&e->lx_qkv, nqkv);
+    if (he == hipSuccess) he = dalloc(&e->lx_act, nact);
+    if (he == hipSuccess) he = hipMemset(e->lx_qkv, 0, nqkv * sizeof(uint2));
+    if (he == hipSuccess) he = hipMemset(e->lx_act, 0, nact * sizeof(uint2));
     if (he == hipSuccess) he = hipMemset(e->lx_zero, 0, pe * sizeof(float));
     if (he == hipSuccess) he = hipMemset(e->lx_flags, 0, (size_t)LX_XCDS * LX_FLAGS * sizeof(unsigned));
     if (he == hipSuccess) he = hipMemset(e->lx_err, 0, sizeof(unsigned));
@@ -1138,7 +1144,8 @@ int sk_destroy(sk_engine* e) {
                   e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->flag_ring, e->u_ring,
                   e->pf_mem, e->ptab, e->gbuf[0], e->gbuf[1],
-                  e->lx_xl, e->lx_xm, e->lx_opart, e->lx_dpart, e->lx_zero, e->lx_flags, e->lx_err,
+                  e->lx_xl, e->lx_xm, e->lx_opart, e->lx_dpart, e->lx_zero, e->lx_qkv, e->lx_act,
+                  e->lx_flags, e->lx_err,
                   e->p_row_start, e->p_rope,
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
   for (void* p : bufs)

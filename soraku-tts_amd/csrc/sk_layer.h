@@ -10,12 +10,12 @@
 // one XCD and pass through its L2:
 //
 //   lx_attn_kernel: x = x_in + sum_h part_in[h] (h = 0..7, fixed order) ->
-//     RMSNorm -> q/k/v rows of KV head g -> barrier -> QK-norm, RoPE, KV
+//     RMSNorm -> q/k/v rows of KV head g -> (tagged) -> QK-norm, RoPE, KV
 //     append, 32-token attention chunks of head g -> barrier -> chunk merge ->
 //     O[:, head g's 256 columns] . attn = this XCD's partial of the residual
 //     update, part_out[g];
 //   lx_mlp_kernel: x = x_in + sum_h part_in[h] -> RMSNorm -> gate/up rows of
-//     inner slice g -> SwiGLU -> barrier -> down[:, slice g] . act =
+//     inner slice g -> SwiGLU -> (tagged) -> down[:, slice g] . act =
 //     part_out[g].
 //
 // The next launch (or the final norm) adds the 8 partials in XCD order, so the
@@ -24,16 +24,18 @@
 // Barrier among the 32 workgroups of an XCD (lx_xcd_barrier): each workgroup
 // stores its epoch in its own word of the XCD's flag line and one wave polls
 // the 32 words with agent-scope loads, which read the L2 (0.5 us measured,
-// against 1.6 us for a kernel boundary).  Data exchanged through it is written
-// with plain stores whose completion the writer waits for, and read with
-// agent-scope loads.  On gfx9 one counter (vmcnt) covers loads and stores and
+// against 1.6 us for a kernel boundary).  Data exchanged through it (the input
+// sums, the chunk partials) is written with plain stores whose completion the
+// writer waits for, and read after it with plain loads; the q/k/v rows and the
+// SwiGLU output pass without a barrier, as tagged words (lx_put, lx_settle).
+// On gfx9 one counter (vmcnt) covers loads and stores and
 // retires in issue order, so waiting for a store also waits for every load
 // issued before it, and a load's data is usable only once every earlier load
 // of the wave has arrived.  Each workgroup therefore splits its 8 waves:
 //   * exchange waves (0-3) issue the first phase's weights, and do every
 //     exchange store, flag and agent-scope load; they hold no prefetch across
 //     a barrier;
-//   * stream waves (4-7) issue the later phases' K/V and weights at entry and
+//   * stream waves (4-7) issue the later phases' K/V and weights ahead of use and
 //     take their inputs from LDS, so nothing they wait for is behind a barrier.
 // Each role is straight-line code and both execute the same sequence of LDS
 // barriers (lx_sync); none of them waits for global loads.
@@ -69,9 +71,9 @@ struct LxArgs {
   const float* pin;                  // [8][M][D] partials to add (zeros for the first layer)
   float* xout;                       // [8][M][D] xin + sum(pin), one copy per XCD (copy 0 is read next)
   float* pout;                       // [8][M][D] this launch's partials
-  float* qkv;                        // [M][(HQ + 2 HKV) HD] raw projections (exchanged)
+  uint2* qkv;                        // [M][(HQ + 2 HKV) HD] raw projections, tagged (exchanged)
   float* part;                       // [M][HQ][max_chunks][HD + 4] chunk partials (exchanged)
-  float* act; int ld_act;            // [M][ld_act] SwiGLU output (exchanged)
+  uint2* act; int ld_act;            // [M][ld_act] SwiGLU output, tagged (exchanged)
   void* kc; void* vc;                // this layer's cache, [M][HKV][max_ctx][HD]
   const float2* rope;                // [M][HD / 2] (cos, sin) at each row's position
   const int* kv_len; const int* active;
@@ -108,6 +110,55 @@ __device__ __forceinline__ void lx_wait_stores() {
 // so the loads miss in L1 and read the XCD's L2 (0.36 us after a barrier,
 // against 0.96 us for agent-scope loads).
 __device__ __forceinline__ float lx_ld(const float* p) { return *p; }
+
+// Tagged exchange words (the q/k/v rows and the SwiGLU output): the value's
+// bits in the low half, the launch's tag in the high half, written with one
+// 8-byte store (naturally aligned 8-byte accesses are single-copy atomic), so
+// a reader that sees the tag sees the value.  The writer neither waits for its
+// stores nor raises a flag: the reader loads the words once with plain loads
+// (the lines are first touched then, so they miss in L1 and read the L2) and
+// reloads those whose tag is not yet the launch's with agent-scope loads,
+// which skip the L1 line the first load left.  The tag is the launch's input
+// barrier epoch, which grows with every launch, so a word from an earlier
+// launch never carries the current one.  (For the input sums, gathered by
+// every workgroup from all 32, the barrier with plain words measured faster:
+// 8 words per thread from writers up to microseconds apart make many reloads.)
+__device__ __forceinline__ void lx_put(uint2* p, float v, unsigned tag) {
+  const unsigned long long wv = (unsigned long long)__float_as_uint(v) | ((unsigned long long)tag << 32);
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ unsigned long long lx_get(const uint2* p) {
+  return *reinterpret_cast<const unsigned long long*>(p);
+}
+__device__ __forceinline__ float lx_val(unsigned long long v) { return __uint_as_float((unsigned)v); }
+// Reloads until every word of v carries tag; false if the deadline passes
+// first.  addr(i) is word i's address.
+template <int N, typename Addr>
+__device__ __forceinline__ bool lx_settle(unsigned long long (&v)[N], Addr addr, unsigned tag,
+                                          unsigned long long deadline) {
+  for (;;) {
+    bool miss = false;
+#pragma unroll
+    for (int i = 0; i < N; ++i) miss |= (unsigned)(v[i] >> 32) != tag;
+    if (!miss) return true;
+    if (__builtin_amdgcn_s_memrealtime() > deadline) return false;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if ((unsigned)(v[i] >> 32) != tag)
+        v[i] = __hip_atomic_load(reinterpret_cast<const unsigned long long*>(addr(i)), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+// A wave's verdict on its exchange (all lanes settled) into ok[w]; a failing
+// wave sets err bit 0.  Read back with lx_all_ok after the next LDS barrier.
+__device__ __forceinline__ void lx_report(bool good, int* ok, int w, unsigned* err) {
+  const bool all = __builtin_amdgcn_ballot_w64(!good) == 0ull;
+  if ((threadIdx.x & 63) == 0) {
+    ok[w] = all ? 1 : 0;
+    if (!all) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+__device__ __forceinline__ bool lx_all_ok(const int* ok) { return (ok[0] & ok[1] & ok[2] & ok[3]) != 0; }
 
 // The 32 workgroups of this XCD meet.  The waves that stored the data being
 // exchanged have waited for their stores; wave `poller` (one with no load in
@@ -313,6 +364,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
   __shared__ float mw[2 * G][LX_MAXCH];   // chunk weights of each (row, head) pair
   __shared__ float mil[2 * G];
   __shared__ int okf;
+  __shared__ int okq[4];   // per-wave verdicts on the q/k/v exchange
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -420,11 +472,12 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     lx_sync();                                                   // 1
     // The first slot's K/V, issued once the exchange waves' q/k/v weights
     // are in flight (the projections are on the critical path; the cache rows
-    // are needed only after the first barrier)
+    // are needed only after the q/k/v exchange)
     load_kv(m0, c0s);
-    lx_sync(); lx_sync();                                        // 2, 3 (barrier)
-    if (okf == 0) return;
+    lx_sync();                                                   // 4
+    if (!lx_all_ok(okq)) return;
     // this wave's W_o rows, head g's columns: needed only after the merge
+    // (issued before, they slow the q/k/v weight stream)
     const int n0 = j * OROWS + w4 * ORW;
     float wo[ORW][OU][OE];
 #pragma unroll
@@ -432,7 +485,6 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
 #pragma unroll
       for (int u = 0; u < OU; ++u)
         NL::load(a.wo, (size_t)(n0 + r) * (HQ * HD) + g * OCOL + (size_t)(u * 64 + lane) * OE, wo[r][u]);
-    lx_sync();                                                   // 4
     lx_sync();                                                   // 5
     lx_sync();                                                   // 6
     // One slot: scores, chunk softmax, partial (o, max, sum) into pb.
@@ -586,8 +638,8 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     if (!lx_xcd_barrier(fl, j, 0u, deadline, 0u, a.err, &okf, 4)) return;   // input barrier (stream wave 4 polls)
     if (trow == 0) { qwn[tr] = qw_r; kwn[tr] = kw_r; }
     if (tr < HD / 2) csh[trow][tr] = cs_r;
-    lx_sync();                                                   // 1
-    const unsigned ep0 = (unsigned)stsh[0][4], err0 = (unsigned)stsh[0][5];
+    lx_sync();                                                   // 1 (input in LDS)
+    const unsigned ep0 = (unsigned)stsh[0][4], err0 = (unsigned)stsh[0][5], tag = ep0 + 1;
     rows_state(stsh[0][0], stsh[0][1], stsh[0][2], stsh[0][3]);
     const float inv[M] = {lx_inv_rms<D>(ssq, 0, a.eps), lx_inv_rms<D>(ssq, 1, a.eps)};
     float acc[QRW][M];
@@ -595,22 +647,26 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     {
       const float v = lx_reduce<8, QRW>(acc, lane);   // word r * M + m in lanes [8 w, 8 w + 8)
       const int wd = lane >> 3;
-      if ((lane & 7) == 0) a.qkv[(size_t)(wd & 1) * (HQ + 2 * HKV) * HD + ocol + (wd >> 1)] = v;
+      if ((lane & 7) == 0) lx_put(a.qkv + (size_t)(wd & 1) * (HQ + 2 * HKV) * HD + ocol + (wd >> 1), v, tag);
     }
-    lx_wait_stores();
-    if (!lx_xcd_barrier(fl, j, ep0 + 2, deadline, err0, a.err, &okf, 0)) return;   // 2, 3
-    // raw q (both rows, this head pair), new k and v
+    // raw q (both rows, this head pair), new k and v, as their tags arrive
     {
       const int ldq = (HQ + 2 * HKV) * HD;
+      auto src = [&](int i) -> const uint2* {
+        return i < 2 ? a.qkv + (size_t)i * ldq + g * G * HD + t
+                     : a.qkv + (size_t)trow * ldq + (i == 2 ? HQ * HD : (HQ + HKV) * HD) + g * HD + tr;
+      };
+      unsigned long long v[4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int e = t + 256 * i, m = e >> 8, o = e & 255;
-        qs[m][o] = lx_ld(a.qkv + (size_t)m * ldq + g * G * HD + o);
-      }
-      kn[trow][tr] = lx_ld(a.qkv + (size_t)trow * ldq + HQ * HD + g * HD + tr);
-      vn[trow][tr] = lx_ld(a.qkv + (size_t)trow * ldq + (HQ + HKV) * HD + g * HD + tr);
+      for (int i = 0; i < 4; ++i) v[i] = lx_get(src(i));
+      lx_report(lx_settle(v, src, tag, deadline), okq, w4, a.err);
+      qs[0][t] = lx_val(v[0]);
+      qs[1][t] = lx_val(v[1]);
+      kn[trow][tr] = lx_val(v[2]);
+      vn[trow][tr] = lx_val(v[3]);
     }
     lx_sync();                                                   // 4
+    if (!lx_all_ok(okq)) return;
     // Qwen3 per-head RMSNorm, then rotate-half RoPE: vectors (row, q head 0,
     // q head 1, k) = 6, waves 0-3 take 0-3 and 4-5.  Lane l holds dims l and l + 64.
     for (int vi = w4; vi < 3 * M; vi += 4) {
@@ -664,7 +720,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       lx_sync();                                                 // D
     }
     lx_wait_stores();
-    if (!lx_xcd_barrier(fl, j, ep0 + 3, deadline, err0, a.err, &okf, 0)) return;   // 7, 8
+    if (!lx_xcd_barrier(fl, j, tag + 1, deadline, err0, a.err, &okf, 0)) return;   // 7, 8
     merge();
     lx_sync();                                                   // 9
   }
@@ -690,8 +746,9 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
   __shared__ __attribute__((aligned(16))) float gsh[D];
   __shared__ float ssq[8];
   __shared__ __attribute__((aligned(16))) float ash[M][IX];   // the XCD's slice
-  __shared__ int stsh[2][2];   // row 0: barrier epoch, error word (loaded by the stream waves)
+  __shared__ int stsh[2][2];   // row 0: epoch, error word (loaded by the stream waves)
   __shared__ int okf;
+  __shared__ int oka[4];   // per-wave verdicts on the SwiGLU exchange
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -713,7 +770,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
         w[2 * r + 1][jj] = WL::raw(a.wu, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
       }
     if (!lx_xcd_barrier(fl, j, 0u, deadline, 0u, a.err, &okf, 4)) return false;   // input barrier
-    lx_sync();                                                   // 1
+    lx_sync();                                                   // 1 (input in LDS)
     const float inv[M] = {lx_inv_rms<D>(ssq, 0, a.eps), lx_inv_rms<D>(ssq, 1, a.eps)};
     float acc[2 * IPW][M];
     lx_dots<D, 2 * IPW, WL>(w, xsh, gsh, inv, lane, acc);
@@ -734,26 +791,26 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     float act;
     if (!gate_up(wave, act)) return;
+    const unsigned tag = (unsigned)stsh[0][0] + 1;   // the input barrier's epoch
     {
       const int wd = lane >> 2, i = wd >> 2, m = wd & 1;
-      if ((lane & 3) == 0 && (wd & 2) == 0 && i < IPW) a.act[(size_t)m * a.ld_act + i0 + wave * IPW + i] = act;
+      if ((lane & 3) == 0 && (wd & 2) == 0 && i < IPW) lx_put(a.act + (size_t)m * a.ld_act + i0 + wave * IPW + i, act, tag);
     }
-    lx_wait_stores();
-    const unsigned ep0 = (unsigned)stsh[0][0], err0 = (unsigned)stsh[0][1];
-    if (!lx_xcd_barrier(fl, j, ep0 + 2, deadline, err0, a.err, &okf, 0)) return;   // 2, 3
     {
       constexpr int PT = M * IX / 256;                           // loads per thread, all issued first
       static_assert(M * IX % 256 == 0, "act slice per exchange thread");
-      float v[PT];
+      auto src = [&](int q) -> const uint2* {
+        const int e = tid + 256 * q, m = e / IX, k = e - m * IX;
+        return a.act + (size_t)m * a.ld_act + g * IX + k;
+      };
+      unsigned long long v[PT];
+#pragma unroll
+      for (int q = 0; q < PT; ++q) v[q] = lx_get(src(q));
+      lx_report(lx_settle(v, src, tag, deadline), oka, wave, a.err);
 #pragma unroll
       for (int q = 0; q < PT; ++q) {
         const int e = tid + 256 * q, m = e / IX, k = e - m * IX;
-        v[q] = lx_ld(a.act + (size_t)m * a.ld_act + g * IX + k);
-      }
-#pragma unroll
-      for (int q = 0; q < PT; ++q) {
-        const int e = tid + 256 * q, m = e / IX, k = e - m * IX;
-        ash[m][k] = v[q];
+        ash[m][k] = lx_val(v[q]);
       }
     }
     lx_sync();                                                   // 4
@@ -783,9 +840,8 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
 #pragma unroll
       for (int u = 0; u < DU; ++u)
         NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE, wd[r][u]);
-    lx_sync(); lx_sync();                                        // 2, 3 (barrier)
-    if (okf == 0) return;
     lx_sync();                                                   // 4
+    if (!lx_all_ok(oka)) return;
     float acc[DRW][M];
 #pragma unroll
     for (int r = 0; r < DRW; ++r)

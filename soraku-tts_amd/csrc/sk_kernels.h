@@ -2731,7 +2731,74 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
     const float* xr = x + (size_t)b * D;
     const size_t ro = (size_t)b * D;
     constexpr int PER = 16;              // D <= 4096 in registers, all loads issued at once
-    if (D <= NT * PER) {
+    const bool al16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(parts) |
+                        reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(w_in) |
+                        reinterpret_cast<uintptr_t>(hidden)) & 15u) == 0;
+    if (al16 && D % (4 * NT) == 0 && D <= NT * PER) {
+      // 16-byte loads: thread t holds elements 4 (t + i NT) .. + 3, so each
+      // thread issues 2 + 8 loads per 1024 elements (and one more with abuf)
+      constexpr int P4 = PER / 4;
+      const int n4 = D / (4 * NT);
+      const float4* x4 = reinterpret_cast<const float4*>(xr);
+      const float4* w4 = reinterpret_cast<const float4*>(w);
+      float4 xv[P4], wv[P4], gv[P4];
+#pragma unroll
+      for (int i = 0; i < P4; ++i) {
+        const int k4 = min((int)threadIdx.x + i * NT, D / 4 - 1);
+        xv[i] = x4[k4];
+        wv[i] = w4[k4];
+        gv[i] = abuf ? reinterpret_cast<const float4*>(w_in)[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      if (parts) {
+        const size_t ps = (size_t)gridDim.x * D;
+#pragma unroll
+        for (int i = 0; i < P4; ++i) {
+          const int k4 = min((int)threadIdx.x + i * NT, D / 4 - 1);
+          float4 pv[8];
+#pragma unroll
+          for (int h = 0; h < 8; ++h) pv[h] = reinterpret_cast<const float4*>(parts + h * ps + ro)[k4];
+#pragma unroll
+          for (int h = 0; h < 8; ++h) {
+            xv[i].x = __fadd_rn(xv[i].x, pv[h].x); xv[i].y = __fadd_rn(xv[i].y, pv[h].y);
+            xv[i].z = __fadd_rn(xv[i].z, pv[h].z); xv[i].w = __fadd_rn(xv[i].w, pv[h].w);
+          }
+        }
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < P4; ++i)
+        if (i < n4) s += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
+      const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
+      float s2 = 0.f;
+      float4* h4 = reinterpret_cast<float4*>(hidden + ro);
+#pragma unroll
+      for (int i = 0; i < P4; ++i) {
+        const float4 y = make_float4(wv[i].x * (xv[i].x * inv), wv[i].y * (xv[i].y * inv), wv[i].z * (xv[i].z * inv),
+                                     wv[i].w * (xv[i].w * inv));
+        xv[i] = y;
+        if (i < n4) {
+          h4[threadIdx.x + i * NT] = y;
+          s2 = fmaf(y.x, y.x, fmaf(y.y, y.y, fmaf(y.z, y.z, fmaf(y.w, y.w, s2))));
+        }
+      }
+      // Depth step 0's input: the prefix is zero at the start of a frame.
+      if (abuf) {
+        const float inv2 = 1.0f / sqrtf(block_sum(s2, red) / (float)D + eps_in);
+#pragma unroll
+        for (int i = 0; i < P4; ++i) {
+          if (i < n4) {
+            const int k = 4 * ((int)threadIdx.x + i * NT);
+            const float y[4] = {gv[i].x * (xv[i].x * inv2), gv[i].y * (xv[i].y * inv2), gv[i].z * (xv[i].z * inv2),
+                                gv[i].w * (xv[i].w * inv2)};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              abuf[ro + k + c] = y[c];
+              if (xs_abuf) xsplit_store(xs_abuf, b, k + c, y[c]);
+            }
+          }
+        }
+      }
+    } else if (D <= NT * PER) {
       float xv[PER], wv[PER], gv[PER];
 #pragma unroll
       for (int i = 0; i < PER; ++i) {

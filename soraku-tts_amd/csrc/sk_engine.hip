@@ -487,19 +487,25 @@ hipError_t launch_attn_stream(sk_engine* e, const AttnArgs& at) {
   return e->c.kv_dtype == SK_BF16 ? launch_attn_stream_kt<uint16_t>(e, at) : launch_attn_stream_kt<float>(e, at);
 }
 
-// XCD-resident layers (sk_layer.h): one utterance with CFG at the Qwen3-0.6B
-// trunk shape (d 1024, SwiGLU 3072, 16 q / 8 KV heads of 128), FP32 or BF16
-// weights and cache.
+// XCD-resident layers (sk_layer.h): one utterance with CFG, 16 q / 8 KV heads
+// of 128, at the Qwen3-0.6B trunk shape (d 1024, SwiGLU 3072) or the
+// Qwen3-1.7B one (d 2048, SwiGLU 6144), FP32 or BF16 weights and cache.
 bool lx_fits(const sk_engine* e) {
   const sk_config& c = e->c;
+  const bool shape = (c.d_model == 1024 && c.trunk_inter == 3072) || (c.d_model == 2048 && c.trunk_inter == 6144);
   return e->rows == LX_M && !e->wide && e->attn_splits == 0 && c.n_kv_heads == LX_HKV && c.n_q_heads == LX_HQ &&
-         c.head_dim == LX_HD && c.d_model == 1024 && c.trunk_inter == 3072 && e->max_chunks <= LX_MAXCH;
+         c.head_dim == LX_HD && shape && e->max_chunks <= LX_MAXCH;
 }
 
 template <typename WL, typename KT>
-hipError_t launch_lx(const LxArgs& A, const LxArgs& C, hipStream_t st) {
-  hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 1024>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
-  hipLaunchKernelGGL((lx_mlp_kernel<WL, 1024, 3072>), dim3(LX_WGS), dim3(LX_NT), 0, st, C);
+hipError_t launch_lx(int d, const LxArgs& A, const LxArgs& C, hipStream_t st) {
+  if (d == 1024) {
+    hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 1024>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
+    hipLaunchKernelGGL((lx_mlp_kernel<WL, 1024, 3072>), dim3(LX_WGS), dim3(LX_NT), 0, st, C);
+  } else {
+    hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 2048>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
+    hipLaunchKernelGGL((lx_mlp8_kernel<WL, 2048, 6144>), dim3(LX_WGS), dim3(LX_NT), 0, st, C);
+  }
   return hipGetLastError();
 }
 
@@ -528,8 +534,9 @@ hipError_t enqueue_trunk_lx(sk_engine* e) {
     C.wg = w.gate; C.wu = w.up; C.wd = w.down; C.gain = w.post_norm;
     C.xin = e->lx_xl; C.pin = e->lx_opart; C.xout = e->lx_xm; C.pout = e->lx_dpart;
     const bool wbf = c.weight_dtype == SK_BF16, kbf = c.kv_dtype == SK_BF16;
-    const hipError_t err = wbf ? (kbf ? launch_lx<WBF16, uint16_t>(A, C, e->stream) : launch_lx<WBF16, float>(A, C, e->stream))
-                               : (kbf ? launch_lx<WF32, uint16_t>(A, C, e->stream) : launch_lx<WF32, float>(A, C, e->stream));
+    const int d = c.d_model;
+    const hipError_t err = wbf ? (kbf ? launch_lx<WBF16, uint16_t>(d, A, C, e->stream) : launch_lx<WBF16, float>(d, A, C, e->stream))
+                               : (kbf ? launch_lx<WF32, uint16_t>(d, A, C, e->stream) : launch_lx<WF32, float>(d, A, C, e->stream));
     if (err != hipSuccess) return err;
   }
   return hipSuccess;

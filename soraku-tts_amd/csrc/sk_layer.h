@@ -300,25 +300,33 @@ __device__ __forceinline__ float lx_reduce(const float (&acc)[R][LX_M], int lane
 }
 
 // E consecutive elements of a weight row (the O and down projections' column
-// slices), widened to FP32: FP32 E = 2 (8 bytes); BF16 E = 4 (8 bytes) or 2
-// (4 bytes) when the slice is not a multiple of 256 columns.
+// slices): FP32 E = 2 (8 bytes); BF16 E = 4 (8 bytes) or 2 (4 bytes) when the
+// slice is not a multiple of 256 columns.  Held raw from the load and widened
+// to FP32 where multiplied, so no conversion waits for a prefetch.
 template <typename WL, int E> struct LxCols;
 template <> struct LxCols<WF32, 2> {
-  __device__ __forceinline__ static void load(const void* base, size_t off, float (&o)[2]) {
-    const float2 t = *reinterpret_cast<const float2*>(static_cast<const float*>(base) + off);
-    o[0] = t.x; o[1] = t.y;
+  using raw_t = uint2;
+  __device__ __forceinline__ static raw_t load(const void* base, size_t off) {
+    return *reinterpret_cast<const uint2*>(static_cast<const float*>(base) + off);
   }
+  __device__ __forceinline__ static void widen(raw_t t, float (&o)[2]) { o[0] = __uint_as_float(t.x); o[1] = __uint_as_float(t.y); }
 };
 template <> struct LxCols<WBF16, 4> {
-  __device__ __forceinline__ static void load(const void* base, size_t off, float (&o)[4]) {
-    const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+  using raw_t = uint2;
+  __device__ __forceinline__ static raw_t load(const void* base, size_t off) {
+    return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+  }
+  __device__ __forceinline__ static void widen(raw_t t, float (&o)[4]) {
     o[0] = __uint_as_float(t.x << 16); o[1] = __uint_as_float(t.x & 0xffff0000u);
     o[2] = __uint_as_float(t.y << 16); o[3] = __uint_as_float(t.y & 0xffff0000u);
   }
 };
 template <> struct LxCols<WBF16, 2> {
-  __device__ __forceinline__ static void load(const void* base, size_t off, float (&o)[2]) {
-    const uint32_t t = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(base) + off);
+  using raw_t = uint32_t;
+  __device__ __forceinline__ static raw_t load(const void* base, size_t off) {
+    return *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(base) + off);
+  }
+  __device__ __forceinline__ static void widen(raw_t t, float (&o)[2]) {
     o[0] = __uint_as_float(t << 16); o[1] = __uint_as_float(t & 0xffff0000u);
   }
 };
@@ -479,12 +487,12 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     // this wave's W_o rows, head g's columns: needed only after the merge
     // (issued before, they slow the q/k/v weight stream)
     const int n0 = j * OROWS + w4 * ORW;
-    float wo[ORW][OU][OE];
+    typename NL::raw_t wo[ORW][OU];
 #pragma unroll
     for (int r = 0; r < ORW; ++r)
 #pragma unroll
       for (int u = 0; u < OU; ++u)
-        NL::load(a.wo, (size_t)(n0 + r) * (HQ * HD) + g * OCOL + (size_t)(u * 64 + lane) * OE, wo[r][u]);
+        wo[r][u] = NL::load(a.wo, (size_t)(n0 + r) * (HQ * HD) + g * OCOL + (size_t)(u * 64 + lane) * OE);
     lx_sync();                                                   // 5
     lx_sync();                                                   // 6
     // One slot: scores, chunk softmax, partial (o, max, sum) into pb.
@@ -589,11 +597,14 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
 #pragma unroll
         for (int i = 0; i < OE; ++i) xv[m][i] = ash[m][k0 + i];
 #pragma unroll
-      for (int r = 0; r < ORW; ++r)
+      for (int r = 0; r < ORW; ++r) {
+        float wf[OE];
+        NL::widen(wo[r][u], wf);
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
-          for (int i = 0; i < OE; ++i) acc[r][m] = fmaf(wo[r][u][i], xv[m][i], acc[r][m]);
+          for (int i = 0; i < OE; ++i) acc[r][m] = fmaf(wf[i], xv[m][i], acc[r][m]);
+      }
     }
     static_assert(ORW * M == 16 || ORW * M == 32, "O rows per stream wave");
     if constexpr (ORW * M == 16) {
@@ -821,7 +832,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
     // down rows of this wave, slice g's columns: issued after the gate/up
     // stream so that it reaches HBM first
     const int n0 = j * DROWS + w4 * DRW;
-    float wd[DRW][DU][DE];
+    typename NL::raw_t wd[DRW][DU];
     {
       const int st = tid - 256;
       LxInput<D> in;
@@ -839,7 +850,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
     for (int r = 0; r < DRW; ++r)
 #pragma unroll
       for (int u = 0; u < DU; ++u)
-        NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE, wd[r][u]);
+        wd[r][u] = NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE);
     lx_sync();                                                   // 4
     if (!lx_all_ok(oka)) return;
     float acc[DRW][M];
@@ -856,11 +867,14 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
 #pragma unroll
         for (int i = 0; i < DE; ++i) xv[m][i] = ash[m][k0 + i];
 #pragma unroll
-      for (int r = 0; r < DRW; ++r)
+      for (int r = 0; r < DRW; ++r) {
+        float wf[DE];
+        NL::widen(wd[r][u], wf);
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
-          for (int i = 0; i < DE; ++i) acc[r][m] = fmaf(wd[r][u][i], xv[m][i], acc[r][m]);
+          for (int i = 0; i < DE; ++i) acc[r][m] = fmaf(wf[i], xv[m][i], acc[r][m]);
+      }
     }
     static_assert(DRW * M == 16 || DRW * M == 32, "down rows per stream wave");
 #pragma unroll
@@ -875,6 +889,134 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
       if ((lane & 3) == 0) a.pout[((size_t)g * M + (wd & 1)) * D + n0 + h * 8 + (wd >> 1)] = v;
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// MLP half for the wider shape (Qwen3-1.7B: d 2048, SwiGLU 6144): 24 inner
+// indices per workgroup are 48 gate/up rows of 4 KB (BF16), more than 4 waves
+// can hold, so all 8 waves take 3 inner indices each and then 8 down rows
+// each.  The stream waves (4-7) also sum the input (their store wait before
+// the input barrier then includes their own gate/up rows, which the dots after
+// it need anyway); the down rows are issued once a wave's gate/up rows are
+// multiplied, and the SwiGLU output is exchanged as tagged words behind them.
+template <typename WL, int D, int I>
+__global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
+  constexpr int M = LX_M, VEC = WL::VEC, NV = D / (64 * VEC);
+  constexpr int IX = I / LX_XCDS, IW = IX / LX_PER;
+  constexpr int IPW = IW / 8;                         // inner indices per wave
+  constexpr int DROWS = D / LX_PER, DRW = DROWS / 8;  // down rows per workgroup / wave
+  constexpr int DE = lx_col_elems<WL>(IX);
+  using NL = LxCols<WL, DE>;
+  constexpr int DU = IX / (64 * DE);                  // column units per lane per down row
+  constexpr int PT = M * IX / LX_NT;                  // SwiGLU outputs per thread in the exchange
+  static_assert(IPW * 8 == IW && 2 * IPW * M <= 16 && DRW * 8 == DROWS && DRW * M == 16, "lx_mlp8_kernel shape");
+  static_assert(IX % (64 * DE) == 0 && M * IX % LX_NT == 0, "lx_mlp8_kernel shape");
+
+  __shared__ __attribute__((aligned(16))) float xsh[M * D];
+  __shared__ __attribute__((aligned(16))) float gsh[D];
+  __shared__ float ssq[8];
+  __shared__ __attribute__((aligned(16))) float ash[M][IX];   // the XCD's slice
+  __shared__ int stsh[2][2];   // row 0: barrier epoch, error word (loaded by the stream waves)
+  __shared__ int okf;
+  __shared__ int oka[8];       // per-wave verdicts on the SwiGLU exchange
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lx_xcd(), j = blockIdx.x >> 3;
+  const unsigned long long deadline = __builtin_amdgcn_s_memrealtime() + a.spin_ticks;
+  unsigned* fl = a.flags + g * LX_FLAGS;
+  const int i0 = g * IX + j * IW;                     // first inner index of this workgroup
+  const int ib = i0 + wave * IPW;
+  uint4 w[2 * IPW][NV];
+#pragma unroll
+  for (int r = 0; r < IPW; ++r)
+#pragma unroll
+    for (int jj = 0; jj < NV; ++jj) {
+      w[2 * r][jj] = WL::raw(a.wg, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
+      w[2 * r + 1][jj] = WL::raw(a.wu, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
+    }
+  if (wave < 4) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (!lx_xcd_barrier(fl, j, 0u, deadline, 0u, a.err, &okf, 4)) return;   // input barrier (stream wave 4 polls)
+    lx_sync();                                                   // 1
+  } else {
+    __builtin_amdgcn_sched_barrier(1);
+    const int st = tid - 256, w4 = wave - 4;
+    LxInput<D> in;
+    const unsigned ep = fl[j], er = *a.err;
+    in.issue(a, st, j);
+    int* sd = stsh[st == 0 ? 0 : 1];   // no branch to sink the loads into
+    sd[0] = (int)ep; sd[1] = (int)er;
+    in.slice(a, g, st, j, gsh);
+    lx_wait_stores();
+    if (!lx_xcd_barrier(fl, j, ep + 1, deadline, er, a.err, &okf, 4)) return;   // input barrier
+    in.gather(a, g, st, w4, xsh, ssq);
+    lx_sync();                                                   // 1
+  }
+  const unsigned tag = (unsigned)stsh[0][0] + 1;                 // the input barrier's epoch
+  {
+    const float inv[M] = {lx_inv_rms<D>(ssq, 0, a.eps), lx_inv_rms<D>(ssq, 1, a.eps)};
+    float acc[2 * IPW][M];
+    lx_dots<D, 2 * IPW, WL>(w, xsh, gsh, inv, lane, acc);
+    // word (2 i + gate/up) M + m = 4 i + 2 gu + m: lanes [4 w, 4 w + 4); the
+    // up word of a gate word sits 8 lanes further on
+    const float x = lx_reduce<16, 2 * IPW>(acc, lane);
+    const float u = __shfl(x, (lane + 8) & 63, 64);
+    const int wd = lane >> 2, i = wd >> 2, m = wd & 1;
+    const float act = x / (1.0f + expf(-x)) * u;
+    if ((lane & 3) == 0 && (wd & 2) == 0 && i < IPW) lx_put(a.act + (size_t)m * a.ld_act + ib + i, act, tag);
+  }
+  // this wave's down rows, slice g's columns
+  const int n0 = j * DROWS + wave * DRW;
+  typename NL::raw_t wdn[DRW][DU];
+#pragma unroll
+  for (int r = 0; r < DRW; ++r)
+#pragma unroll
+    for (int u = 0; u < DU; ++u)
+      wdn[r][u] = NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE);
+  {
+    auto src = [&](int q) -> const uint2* {
+      const int e = tid + LX_NT * q, m = e / IX, k = e - m * IX;
+      return a.act + (size_t)m * a.ld_act + g * IX + k;
+    };
+    unsigned long long v[PT];
+#pragma unroll
+    for (int q = 0; q < PT; ++q) v[q] = lx_get(src(q));
+    lx_report(lx_settle(v, src, tag, deadline), oka, wave, a.err);
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+      const int e = tid + LX_NT * q, m = e / IX, k = e - m * IX;
+      ash[m][k] = lx_val(v[q]);
+    }
+  }
+  lx_sync();                                                     // 2
+  if (!(lx_all_ok(oka) && lx_all_ok(oka + 4))) return;
+  float acc[DRW][M];
+#pragma unroll
+  for (int r = 0; r < DRW; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+#pragma unroll
+  for (int u = 0; u < DU; ++u) {
+    const int k0 = (u * 64 + lane) * DE;
+    float xv[M][DE];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int i = 0; i < DE; ++i) xv[m][i] = ash[m][k0 + i];
+#pragma unroll
+    for (int r = 0; r < DRW; ++r) {
+      float wf[DE];
+      NL::widen(wdn[r][u], wf);
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < DE; ++i) acc[r][m] = fmaf(wf[i], xv[m][i], acc[r][m]);
+    }
+  }
+  const float v = lx_reduce<16, DRW>(acc, lane);   // word r * M + m in lanes [4 w, 4 w + 4)
+  const int wd = lane >> 2;
+  if ((lane & 3) == 0) a.pout[((size_t)g * M + (wd & 1)) * D + n0 + (wd >> 1)] = v;
 }
 
 }  // namespace

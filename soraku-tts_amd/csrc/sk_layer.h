@@ -897,8 +897,8 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
 // can hold, so all 8 waves take 3 inner indices each and then 8 down rows
 // each.  The stream waves (4-7) also sum the input (their store wait before
 // the input barrier then includes their own gate/up rows, which the dots after
-// it need anyway); the down rows are issued once a wave's gate/up rows are
-// multiplied, and the SwiGLU output is exchanged as tagged words behind them.
+// it need anyway); the SwiGLU output is exchanged as tagged words behind the
+// down rows.
 template <typename WL, int D, int I>
 __global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
   constexpr int M = LX_M, VEC = WL::VEC, NV = D / (64 * VEC);
@@ -935,8 +935,21 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
       w[2 * r][jj] = WL::raw(a.wg, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
       w[2 * r + 1][jj] = WL::raw(a.wu, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
     }
+  // this wave's down rows, slice g's columns: the exchange waves issue them
+  // behind their gate/up rows, the stream waves once the input is in LDS
+  // (ahead of it they would hold back the input barrier)
+  const int n0 = j * DROWS + wave * DRW;
+  typename NL::raw_t wdn[DRW][DU];
+  auto load_down = [&]() {
+#pragma unroll
+    for (int r = 0; r < DRW; ++r)
+#pragma unroll
+      for (int u = 0; u < DU; ++u)
+        wdn[r][u] = NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE);
+  };
   if (wave < 4) {
     __builtin_amdgcn_sched_barrier(0);
+    load_down();
     if (!lx_xcd_barrier(fl, j, 0u, deadline, 0u, a.err, &okf, 4)) return;   // input barrier (stream wave 4 polls)
     lx_sync();                                                   // 1
   } else {
@@ -952,6 +965,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
     if (!lx_xcd_barrier(fl, j, ep + 1, deadline, er, a.err, &okf, 4)) return;   // input barrier
     in.gather(a, g, st, w4, xsh, ssq);
     lx_sync();                                                   // 1
+    load_down();
   }
   const unsigned tag = (unsigned)stsh[0][0] + 1;                 // the input barrier's epoch
   {
@@ -966,14 +980,6 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
     const float act = x / (1.0f + expf(-x)) * u;
     if ((lane & 3) == 0 && (wd & 2) == 0 && i < IPW) lx_put(a.act + (size_t)m * a.ld_act + ib + i, act, tag);
   }
-  // this wave's down rows, slice g's columns
-  const int n0 = j * DROWS + wave * DRW;
-  typename NL::raw_t wdn[DRW][DU];
-#pragma unroll
-  for (int r = 0; r < DRW; ++r)
-#pragma unroll
-    for (int u = 0; u < DU; ++u)
-      wdn[r][u] = NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE);
   {
     auto src = [&](int q) -> const uint2* {
       const int e = tid + LX_NT * q, m = e / IX, k = e - m * IX;

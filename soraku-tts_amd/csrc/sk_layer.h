@@ -668,6 +668,10 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
                      : a.qkv + (size_t)trow * ldq + (i == 2 ? HQ * HD : (HQ + HKV) * HD) + g * HD + tr;
       };
       unsigned long long v[4];
+      // ~0.3 us before the first load: loaded right after the own store,
+      // most words were not yet there and each reload is an L2 round trip
+      // (0.6B frame -8 us; 5 or 20 instead of 10: -5 us, 30: 0)
+      __builtin_amdgcn_s_sleep(10);
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = lx_get(src(i));
       lx_report(lx_settle(v, src, tag, deadline), okq, w4, a.err);
@@ -815,6 +819,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
         return a.act + (size_t)m * a.ld_act + g * IX + k;
       };
       unsigned long long v[PT];
+      __builtin_amdgcn_s_sleep(10);   // as before the q/k/v loads
 #pragma unroll
       for (int q = 0; q < PT; ++q) v[q] = lx_get(src(q));
       lx_report(lx_settle(v, src, tag, deadline), oka, wave, a.err);

@@ -179,6 +179,13 @@ int sk_synchronize(sk_engine* e);
 /* The engine's stream (hipStream_t) and frame counter. */
 void* sk_stream(sk_engine* e);
 int32_t sk_frames_done(sk_engine* e);
+/* Diagnostic with no counterpart in the reference (which has one decode
+ * path): 1 when the engine runs its trunk as XCD-resident layers (two
+ * launches per layer; one utterance with CFG at the Qwen3-0.6B or, with BF16
+ * weights, Qwen3-1.7B shape, on a device of 256 CUs, unless
+ * SORAKU_XCD_LAYERS=0 was set at sk_create), 0 when it runs the per-op layer
+ * kernels, -1 for a NULL engine.  For tests and profiling. */
+int32_t sk_xcd_layers(sk_engine* e);
 
 /* ---- operator API (tilelang_kernels.py counterparts) ------------------
  * All pointers are device pointers, all tensors contiguous row-major.

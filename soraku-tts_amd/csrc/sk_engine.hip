@@ -1549,5 +1549,6 @@ int sk_synchronize(sk_engine* e) {
 void* sk_stream(sk_engine* e) { return e ? (void*)e->stream : nullptr; }
 
 int32_t sk_frames_done(sk_engine* e) { return e ? e->fc_host : -1; }
+int32_t sk_xcd_layers(sk_engine* e) { return e ? (e->lx ? 1 : 0) : -1; }
 
 }  // extern "C"

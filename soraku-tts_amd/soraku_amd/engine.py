@@ -327,3 +327,8 @@ class GraphFrameEngine:
     @property
     def frames_done(self) -> int:
         return int(lib().sk_frames_done(self._h))
+
+    @property
+    def xcd_layers(self) -> bool:
+        """True when the trunk runs as XCD-resident layers (two launches per layer)."""
+        return int(lib().sk_xcd_layers(self._h)) == 1

@@ -89,6 +89,7 @@ def test_null_handles_are_rejected(L):
     assert L.sk_step_frame(None, 0, None, None, None, None) == SK_EINVAL
     assert L.sk_bind_weight(None, b"trunk.norm.weight", None, 0, None, 0) == SK_EINVAL
     assert L.sk_frames_done(None) == -1
+    assert L.sk_xcd_layers(None) == -1
     assert L.sk_prefill_refill(None) == SK_EINVAL
     assert L.sk_retire_row(None, 0) == SK_EINVAL
     assert L.sk_reset_frames(None) == SK_EINVAL

@@ -10,6 +10,8 @@ reference's vectors and the oracle.
 * Qwen3-0.6B with 543 / 448 cached positions: decode attention crosses a
   32-token chunk edge and merges more than 16 chunks (contexts above 512).
 * Qwen3-1.7B, BF16 weights, 240-position prefix, sampled.
+* The XCD-resident trunk layers (the path these two-row engines take)
+  against the per-op layer kernels, at both shapes.
 * An untied classifier head bound through ``GraphFrameEngine(model=...)``.
 
 Tolerance: logits within 1e-3 of the reference / oracle, relative to the
@@ -123,6 +125,7 @@ def test_c3_prefix_teacher_forced_matches_reference(hip_device):
     text, uncond, prompt = _c3_inputs(f)
     g = {k: gen[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
     e = _engine(s, w, hip_device, text, uncond, prompt, 260, **g)
+    assert e.xcd_layers   # two decode rows at the 0.6B shape: the XCD-resident trunk layers
     hid = e.hidden()
     assert np.abs(hid - f["hidden"][0]).max() / np.abs(f["hidden"][0]).max() < 1e-4
     got = []
@@ -204,11 +207,56 @@ def test_q17b_c5_prefix_sampled(hip_device):
     m = OracleModel(s, w, np.float64)
     states = start_states(m, text, prompt, uncond, C3["cfg_scale"], 260)
     e = _engine(s, w, hip_device, text, uncond, prompt, 260, bf16=True, **C3)
+    assert e.xcd_layers   # two decode rows at the 1.7B shape, BF16: the XCD-resident trunk layers
     u = np.random.default_rng(241).random((4, s.n_codebooks))
     done, worst = _free_running_vs_oracle(e, m, states, s, u, C3, text, prompt, uncond)
     e.close()
     print(f"1.7B BF16 at 240/146 positions: {done} frames equal, max logit error {worst:.3e}")
     assert done >= 3
+
+
+@pytest.mark.parametrize("model", ["q06b", "q17b"])
+def test_xcd_layers_match_per_op_layers(hip_device, monkeypatch, model):
+    """The XCD-resident trunk layers (two launches per layer, projections
+    summed as 8 per-XCD partials) against the per-op layer kernels
+    (SORAKU_XCD_LAYERS=0) on the same weights and prefix: teacher-forced
+    masked logits of every depth step within 1e-4 row-relative (two FP32
+    summation orders of the same projections; measured 7e-7 at 0.6B, 3e-6 at
+    1.7B), 4 frames, at the C3 (0.6B FP32) and C5 (1.7B BF16) prefixes."""
+    if model == "q06b":
+        f, s, _ = load_golden("q06b_sampled")
+        w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                              bias_std=float(f["bias_std"]))
+        text, uncond, prompt = _c3_inputs(f)
+        bf16 = False
+    else:
+        from test_gpu_engine import _device_weights
+
+        s = dataclasses.replace(QWEN3_17B, text_vocab=4096)
+        w = _device_weights(s, 240, hip_device)
+        rng = np.random.default_rng(240)
+        text = rng.integers(0, s.text_vocab, 95)
+        prompt = rng.integers(0, s.codebook_size, (144, s.n_codebooks))
+        uncond = np.array([11])
+        bf16 = True
+    g = {k: C3[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
+    e = _engine(s, w, hip_device, text, uncond, prompt, 260, bf16=bf16, **g)
+    monkeypatch.setenv("SORAKU_XCD_LAYERS", "0")
+    r = _engine(s, w, hip_device, text, uncond, prompt, 260, bf16=bf16, **g)
+    monkeypatch.delenv("SORAKU_XCD_LAYERS")
+    assert e.xcd_layers and not r.xcd_layers
+    codes = np.random.default_rng(7).integers(0, s.codebook_size, (4, s.n_codebooks))
+    worst = 0.0
+    for fi in range(codes.shape[0]):
+        step = dict(mask_eos_q0=True, uniforms=np.zeros(s.n_codebooks), forced_codes=codes[fi], return_logits=True)
+        _, a = e.step_frame(**step)
+        _, b = r.step_frame(**step)
+        rel = _rowwise_rel(np.asarray(a[0]), np.asarray(b[0]))
+        worst = max(worst, rel)
+        assert rel < 1e-4, (fi, rel)
+    e.close()
+    r.close()
+    print(f"{model}: XCD-resident vs per-op layers, max row-relative logit difference {worst:.3e}")
 
 
 def test_untied_head_through_model_binding(hip_device):

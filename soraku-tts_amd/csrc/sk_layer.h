@@ -369,8 +369,6 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
   __shared__ float qwn[HD], kwn[HD];
   __shared__ float2 csh[M][HD / 2];
   __shared__ int stsh[2][6];   // row 0: kv_len[0..1], active[0..1], barrier epoch, error word
-  __shared__ float mw[2 * G][LX_MAXCH];   // chunk weights of each (row, head) pair
-  __shared__ float mil[2 * G];
   __shared__ int okf;
   __shared__ int okq[4];   // per-wave verdicts on the q/k/v exchange
 
@@ -394,53 +392,52 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     nsl = nch0 + nch1;
     nit = (nsl + LX_PER - 1) / LX_PER;              // slots per workgroup (one bound for all)
   };
-  // Chunk merge after the third barrier, by all 8 waves: every thread issues
-  // its output's first 16 chunk partials (row tid >> 8, head (tid >> 7) & 1
-  // of the pair, dim tid & 127) while wave 0 turns each (row, head) pair's
-  // chunk maxima and sums into weights exp(m_c - M) and 1 / sum_c l_c
-  // exp(m_c - M) in LDS (mw, mil); then O = sum_c w_c o_c in chunk order.
+  // Chunk merge after the chunk barrier, by all 8 waves; each wave serves one
+  // (row, head) pair (row tid >> 8, head (tid >> 7) & 1 of the pair, dim
+  // tid & 127).  Every thread issues its output's first 16 chunk partials,
+  // lanes c = lane & 15 the pair's chunk maxima and sums; the wave turns them
+  // into weights exp(m_c - M) and 1 / sum_c l_c exp(m_c - M) with 16-lane
+  // shuffle trees and hands weight c to every lane by a shuffle, so no wave
+  // waits for another; then O = sum_c w_c o_c in chunk order.
   auto merge = [&]() {
-    const int m = tid >> 8, gi = (tid >> 7) & 1, d = tid & (HD - 1), pr = 2 * m + gi;
-    const int nch = m == 0 ? nch0 : nch1;
-    const float* pp = a.part + (((size_t)m * HQ + g * G + gi) * a.max_chunks) * PS + d;
+    const int m = tid >> 8, gi = (tid >> 7) & 1, d = tid & (HD - 1);
+    const int nch = m == 0 ? nch0 : nch1;   // uniform in the wave
+    const float* pp = a.part + (((size_t)m * HQ + g * G + gi) * a.max_chunks) * PS;
     constexpr int CB = 16;
     float ov[CB];
 #pragma unroll
-    for (int q = 0; q < CB; ++q) ov[q] = lx_ld(pp + (size_t)min(q, max(nch - 1, 0)) * PS);
-    if (wave == 0) {   // lane = (pair p, chunk c within a block of 16)
-      const int p = lane >> 4, c = lane & 15, pm = p >> 1;
-      const int pn = pm == 0 ? nch0 : nch1, nmax = max(nch0, nch1);
-      const float* pq = a.part + (((size_t)pm * HQ + g * G + (p & 1)) * a.max_chunks) * PS + HD;
-      const float2 v0 = *reinterpret_cast<const float2*>(pq + (size_t)min(c, max(pn - 1, 0)) * PS);
-      float mx = c < pn ? v0.x : -INFINITY;
-      for (int c0 = CB; c0 < nmax; c0 += CB)
-        if (c0 + c < pn) mx = fmaxf(mx, lx_ld(pq + (size_t)(c0 + c) * PS));
+    for (int q = 0; q < CB; ++q) ov[q] = lx_ld(pp + (size_t)min(q, max(nch - 1, 0)) * PS + d);
+    const int c = lane & 15;
+    const float2 v0 = *reinterpret_cast<const float2*>(pp + (size_t)min(c, max(nch - 1, 0)) * PS + HD);
+    float mx = c < nch ? v0.x : -INFINITY;
+    for (int c0 = CB; c0 < nch; c0 += CB)
+      if (c0 + c < nch) mx = fmaxf(mx, lx_ld(pp + (size_t)(c0 + c) * PS + HD));
 #pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-      const float e0 = c < pn ? expf(v0.x - mx) : 0.f;
-      float l = v0.y * e0;
-      if (c < pn) mw[p][c] = e0;
-      for (int c0 = CB; c0 < nmax; c0 += CB)
-        if (c0 + c < pn) {
-          const float2 v = *reinterpret_cast<const float2*>(pq + (size_t)(c0 + c) * PS);
-          const float e = expf(v.x - mx);
-          l = fmaf(v.y, e, l);
-          mw[p][c0 + c] = e;
-        }
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
-      if (c == 0) mil[p] = pn ? 1.0f / l : 0.f;
-    }
-    lx_sync();
+    for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const float e0 = c < nch ? expf(v0.x - mx) : 0.f;
+    float l = v0.y * e0;
     float O = 0.f;
 #pragma unroll
-    for (int q = 0; q < CB; ++q)
-      if (q < nch) O = fmaf(mw[pr][q], ov[q], O);
-    for (int c0 = CB; c0 < nch; c0 += CB)
+    for (int q = 0; q < CB; ++q) {
+      const float w = __shfl(e0, q, 64);
+      if (q < nch) O = fmaf(w, ov[q], O);
+    }
+    for (int c0 = CB; c0 < nch; c0 += CB) {
+      float e = 0.f;
+      if (c0 + c < nch) {
+        const float2 v = *reinterpret_cast<const float2*>(pp + (size_t)(c0 + c) * PS + HD);
+        e = expf(v.x - mx);
+        l = fmaf(v.y, e, l);
+      }
 #pragma unroll
-      for (int q = 0; q < CB; ++q)
-        if (c0 + q < nch) O = fmaf(mw[pr][c0 + q], lx_ld(pp + (size_t)(c0 + q) * PS), O);
-    ash[m][gi * HD + d] = O * mil[pr];
+      for (int q = 0; q < CB; ++q) {
+        const float w = __shfl(e, q, 64);
+        if (c0 + q < nch) O = fmaf(w, lx_ld(pp + (size_t)(c0 + q) * PS + d), O);
+      }
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+    ash[m][gi * HD + d] = O * (nch ? 1.0f / l : 0.f);
   };
 
   if (wave >= 4) {

@@ -14,9 +14,9 @@
 //     append, 32-token attention chunks of head g -> barrier -> chunk merge ->
 //     O[:, head g's 256 columns] . attn = this XCD's partial of the residual
 //     update, part_out[g];
-//   lx_mlp_kernel: x = x_in + sum_h part_in[h] -> RMSNorm -> gate/up rows of
-//     inner slice g -> SwiGLU -> (tagged) -> down[:, slice g] . act =
-//     part_out[g].
+//   lx_mlp_kernel (lx_mlp8_kernel at the 1.7B shape): x = x_in +
+//     sum_h part_in[h] -> RMSNorm -> gate/up rows of inner slice g -> SwiGLU
+//     -> (tagged) -> down[:, slice g] . act = part_out[g].
 //
 // The next launch (or the final norm) adds the 8 partials in XCD order, so the
 // projections' sums are taken in a fixed order and replays stay bitwise equal.
@@ -32,11 +32,13 @@
 // retires in issue order, so waiting for a store also waits for every load
 // issued before it, and a load's data is usable only once every earlier load
 // of the wave has arrived.  Each workgroup therefore splits its 8 waves:
-//   * exchange waves (0-3) issue the first phase's weights, and do every
-//     exchange store, flag and agent-scope load; they hold no prefetch across
-//     a barrier;
-//   * stream waves (4-7) issue the later phases' K/V and weights ahead of use and
-//     take their inputs from LDS, so nothing they wait for is behind a barrier.
+//   * exchange waves (0-3) issue the first phase's weights and do the q/k/v
+//     or SwiGLU exchange and the chunk partials' barrier; they hold no
+//     prefetch across an exchange;
+//   * stream waves (4-7) sum the input (their workgroup's slice, the input
+//     barrier, the gather), then issue the later phases' K/V and weights ahead
+//     of use and take their inputs from LDS, so nothing they wait for is
+//     behind an exchange.
 // Each role is straight-line code and both execute the same sequence of LDS
 // barriers (lx_sync); none of them waits for global loads.
 //

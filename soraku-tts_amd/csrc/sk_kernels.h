@@ -2064,6 +2064,23 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   float xr[VPT];
   merge_mask<VPT>(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, a.flag_cur, ut, q != 0, temp,
                   P.record_logits ? a.dbg + ((size_t)ut * a.Q + q) * a.V : nullptr, xr);
+  // The last codebook's frame embedding: the table rows of codebooks
+  // 0 .. Q-2 do not depend on the draw, so they are in flight during it
+  // (issued once the logits are in, so the sampler does not wait for them).
+  constexpr int EI = 4, EQ = 16;        // d <= EI * SNT, 2 <= Q <= EQ
+  const bool early = last && a.d <= EI * SNT && a.Q >= 2 && a.Q <= EQ;
+  const size_t row_stride = (size_t)a.V * a.d;
+  float te[EI][EQ - 1];
+  if (early) {
+#pragma unroll
+    for (int i = 0; i < EI; ++i)
+#pragma unroll
+      for (int j = 0; j < EQ - 1; ++j) {
+        const int dd = min((int)threadIdx.x + i * SNT, a.d - 1), jj = min(j, a.Q - 2);
+        const int cj = a.codes_cur[(size_t)ut * a.Q + jj];
+        te[i][j] = TL::get(a.table, (size_t)jj * row_stride + (size_t)cj * a.d + dd);
+      }
+  }
   int code = sample_core<VPT>(xr, a.V, temp, topk, topp, u, ck, sk, W, s);
   const size_t uoff = ((size_t)slot * a.n_utts + ut) * a.Q + q;
   if (threadIdx.x == 0) {
@@ -2082,7 +2099,28 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   }
 
   __syncthreads();
-  const size_t row_stride = (size_t)a.V * a.d;
+  if (early) {
+    const int cq = codes_l[q];
+    float tq[EI];
+#pragma unroll
+    for (int i = 0; i < EI; ++i)
+      tq[i] = TL::get(a.table, (size_t)q * row_stride + (size_t)cq * a.d + min((int)threadIdx.x + i * SNT, a.d - 1));
+#pragma unroll
+    for (int i = 0; i < EI; ++i) {
+      const int dd = threadIdx.x + i * SNT;
+      if (dd >= a.d) continue;
+      float e = te[i][0];                 // codebooks in order: the same fold as below
+#pragma unroll
+      for (int j = 1; j < EQ - 1; ++j)
+        if (j < a.Q - 1) e = __fadd_rn(e, te[i][j]);
+      e = __fmul_rn(__fadd_rn(e, tq[i]), a.scale);
+      for (int rr = 0; rr < a.rows_per_utt; ++rr) {
+        a.xnext[(size_t)(r0 + rr) * a.d + dd] = e;
+        a.prefix[(size_t)(r0 + rr) * a.d + dd] = 0.f;
+      }
+    }
+    return;
+  }
   for (int dd = threadIdx.x; dd < a.d; dd += SNT) {
     float e = 0.f;
     for (int j0 = 0; j0 < a.Q; j0 += 16) {

@@ -366,7 +366,6 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
   __shared__ float sc[G][ATT_CHUNK];
   __shared__ float stt[G][2];
   __shared__ __attribute__((aligned(16))) float vs[ATT_CHUNK * HD];
-  __shared__ float pb[G][HD + 2];
   __shared__ __attribute__((aligned(16))) float ash[M][OCOL];
   __shared__ float qwn[HD], kwn[HD];
   __shared__ float2 csh[M][HD / 2];
@@ -560,16 +559,18 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
         if (lane == 0) { stt[w4][0] = mx; stt[w4][1] = l; }
       }
       lx_sync();                                                 // B
-      {
+      {   // the chunk's partial (o, max, sum) straight to the XCD's L2
         const int gi = st / HD, d = st - gi * HD;
         float o = 0.f;
 #pragma unroll 8
         for (int tl = 0; tl < ATT_CHUNK; ++tl) o = fmaf(sc[gi][tl], vs[(size_t)tl * HD + d], o);
-        pb[gi][d] = o;
-        if (d < 2) pb[gi][HD + d] = stt[gi][d];
+        if (live) {
+          float* dst = a.part + (((size_t)m * HQ + g * G + gi) * a.max_chunks + c) * PS;
+          dst[d] = o;
+          if (d < 2) dst[HD + d] = stt[gi][d];
+        }
       }
-      lx_sync();                                                 // C
-      lx_sync();                                                 // D
+      lx_sync();                                                 // C: sc, vs free for the next slot
     };
     attend(0);   // the first slot apart, so waiting for its K/V does not wait for W_o
     for (int it = 1; it < nit; ++it) {
@@ -578,8 +579,10 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       load_kv(live ? (s < nch0 ? 0 : 1) : 0, live ? (s < nch0 ? s : s - nch0) : 0);
       attend(it);
     }
-    lx_sync(); lx_sync();                                        // 7, 8 (barrier)
-    if (okf == 0) return;
+    // the partials are out once this wave's stores are (its K/V and W_o
+    // loads, issued before them, are in by now); stream wave 4 polls
+    lx_wait_stores();
+    if (!lx_xcd_barrier(fl, j, ep + 2, deadline, er, a.err, &okf, 4)) return;   // 7, 8
     merge();
     lx_sync();                                                   // 9
     float acc[ORW][M];
@@ -722,19 +725,9 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     for (int it = 0; it < nit; ++it) {
       lx_sync();                                                 // A: scores, V in LDS
       lx_sync();                                                 // B: softmax
-      lx_sync();                                                 // C: partials in pb
-      const int s = j + it * LX_PER;
-      if (s < nsl) {
-        const int m = s < nch0 ? 0 : 1, c = s < nch0 ? s : s - nch0;
-        for (int e = t; e < G * (HD + 2); e += 256) {
-          const int gi = e / (HD + 2), o = e - gi * (HD + 2);
-          a.part[(((size_t)m * HQ + g * G + gi) * a.max_chunks + c) * PS + o] = pb[gi][o];
-        }
-      }
-      lx_sync();                                                 // D
+      lx_sync();                                                 // C: partials stored
     }
-    lx_wait_stores();
-    if (!lx_xcd_barrier(fl, j, tag + 1, deadline, err0, a.err, &okf, 0)) return;   // 7, 8
+    if (!lx_xcd_barrier(fl, j, tag + 1, deadline, err0, a.err, &okf, 4)) return;   // 7, 8 (stream wave 4 polls)
     merge();
     lx_sync();                                                   // 9
   }

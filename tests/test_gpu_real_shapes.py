@@ -215,14 +215,15 @@ def test_q17b_c5_prefix_sampled(hip_device):
     assert done >= 3
 
 
-@pytest.mark.parametrize("model", ["q06b", "q17b"])
+@pytest.mark.parametrize("model", ["q06b", "q17b", "q17b_f32"])
 def test_xcd_layers_match_per_op_layers(hip_device, monkeypatch, model):
     """The XCD-resident trunk layers (two launches per layer, projections
     summed as 8 per-XCD partials) against the per-op layer kernels
     (SORAKU_XCD_LAYERS=0) on the same weights and prefix: teacher-forced
     masked logits of every depth step within 1e-4 row-relative (two FP32
     summation orders of the same projections; measured 7e-7 at 0.6B, 3e-6 at
-    1.7B), 4 frames, at the C3 (0.6B FP32) and C5 (1.7B BF16) prefixes."""
+    1.7B), 4 frames, at the C3 (0.6B FP32) and C5 (1.7B BF16, and the same
+    BF16-valued weights held as FP32) prefixes."""
     if model == "q06b":
         f, s, _ = load_golden("q06b_sampled")
         w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
@@ -238,7 +239,7 @@ def test_xcd_layers_match_per_op_layers(hip_device, monkeypatch, model):
         text = rng.integers(0, s.text_vocab, 95)
         prompt = rng.integers(0, s.codebook_size, (144, s.n_codebooks))
         uncond = np.array([11])
-        bf16 = True
+        bf16 = model == "q17b"
     g = {k: C3[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
     e = _engine(s, w, hip_device, text, uncond, prompt, 260, bf16=bf16, **g)
     monkeypatch.setenv("SORAKU_XCD_LAYERS", "0")

@@ -11,7 +11,8 @@ reference's vectors and the oracle.
   32-token chunk edge and merges more than 16 chunks (contexts above 512).
 * Qwen3-1.7B, BF16 weights, 240-position prefix, sampled.
 * The XCD-resident trunk layers (the path these two-row engines take)
-  against the per-op layer kernels, at both shapes.
+  against the per-op layer kernels, at both shapes, and with more chunk slots
+  than an XCD has workgroups.
 * An untied classifier head bound through ``GraphFrameEngine(model=...)``.
 
 Tolerance: logits within 1e-3 of the reference / oracle, relative to the
@@ -258,6 +259,39 @@ def test_xcd_layers_match_per_op_layers(hip_device, monkeypatch, model):
     e.close()
     r.close()
     print(f"{model}: XCD-resident vs per-op layers, max row-relative logit difference {worst:.3e}")
+
+
+def test_xcd_layers_two_slots_per_workgroup(hip_device, monkeypatch):
+    """Cond row 657 cached positions, uncond 562: 21 + 18 = 39 chunk slots, more
+    than the 32 workgroups of an XCD, so some take a second slot (the
+    attention half's slot loop, which the C5 frames past ~512 positions use).
+    Teacher-forced masked logits of the XCD-resident layers against the per-op
+    layer kernels within 1e-4 row-relative, 3 frames."""
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)
+    w = synthetic_weights(s, 21, norm_gain_std=0.1, bias_std=0.02)
+    rng = np.random.default_rng(21)
+    text = rng.integers(0, s.text_vocab, 96)
+    prompt = rng.integers(0, s.codebook_size, (560, s.n_codebooks))
+    uncond = np.array([5])
+    assert text.size + 1 + prompt.shape[0] == 657 and uncond.size + 1 + prompt.shape[0] == 562
+    g = {k: C3[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
+    e = _engine(s, w, hip_device, text, uncond, prompt, 700, **g)
+    monkeypatch.setenv("SORAKU_XCD_LAYERS", "0")
+    r = _engine(s, w, hip_device, text, uncond, prompt, 700, **g)
+    monkeypatch.delenv("SORAKU_XCD_LAYERS")
+    assert e.xcd_layers and not r.xcd_layers
+    codes = np.random.default_rng(22).integers(0, s.codebook_size, (3, s.n_codebooks))
+    worst = 0.0
+    for fi in range(codes.shape[0]):
+        step = dict(mask_eos_q0=True, uniforms=np.zeros(s.n_codebooks), forced_codes=codes[fi], return_logits=True)
+        _, a = e.step_frame(**step)
+        _, b = r.step_frame(**step)
+        rel = _rowwise_rel(np.asarray(a[0]), np.asarray(b[0]))
+        worst = max(worst, rel)
+        assert rel < 1e-4, (fi, rel)
+    e.close()
+    r.close()
+    print(f"two slots per workgroup (657/562 positions): max row-relative logit difference {worst:.3e}")
 
 
 def test_untied_head_through_model_binding(hip_device):

@@ -2763,9 +2763,37 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
                                                         const float* w_in, float eps_in, float* abuf,
                                                         uint16_t* xs_abuf) {
   __shared__ float red[WAVES];
-  const int b = blockIdx.x;
-  const int p0 = pos[b];                 // read by every thread before the barrier in block_sum
-  if (active[b]) {
+  const int b = blockIdx.x, tx = threadIdx.x;
+  // The bookkeeping's loads (step counters, the RoPE table row, the next
+  // frame's draws and flags) are issued before the row's stores and held in
+  // registers: issued where they are used, after those stores, each waited
+  // for the stores and for the load before it.  The table row, draws and
+  // flags are loaded right behind the row's loads (book()), unconditionally
+  // at clamped indices (a load under a branch makes the join wait for it), so
+  // rope_tab, u_ring and flag_ring must be valid buffers; only the stores are
+  // conditional.  The frame counter is a vector load (opaque zero offset):
+  // the first use of a scalar load waits for every scalar load in flight, and
+  // the compiler puts that use ahead of the row's loads.  The asm statement
+  // follows the scalar loads, since loads after it become vector loads too.
+  // Every thread reads pos, kv_len and the counter before thread 0 writes
+  // them (after the barriers in block_sum, or the one below); every
+  // workgroup loads the counter, only workgroup 0 uses it.
+  const int p0 = pos[b], kv0 = kv_len[b], np = p0 + 1;
+  const bool act = active[b] != 0;
+  int zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  const int cnt = counter[zero];   // the frame counter; the next frame is cnt + 1
+  int f0 = 0;
+  double u0 = 0.0;
+  float2 rp = make_float2(0.f, 0.f);
+  auto book = [&]() {
+    const int nx = min(cnt + 1, max_frames - 1);
+    rp = rope_tab[(size_t)min(np, tab_n - 1) * half + min(tx, half - 1)];
+    u0 = u_ring[(size_t)nx * nq + min(tx, nq - 1)];
+    f0 = flag_ring[2 * nx + min(tx, 1)];
+  };
+  if (!act) book();
+  if (act) {
     const float* xr = x + (size_t)b * D;
     const size_t ro = (size_t)b * D;
     constexpr int PER = 16;              // D <= 4096 in registers, all loads issued at once
@@ -2773,34 +2801,36 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
                         reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(w_in) |
                         reinterpret_cast<uintptr_t>(hidden)) & 15u) == 0;
     if (al16 && D % (4 * NT) == 0 && D <= NT * PER) {
-      // 16-byte loads: thread t holds elements 4 (t + i NT) .. + 3, so each
-      // thread issues 2 + 8 loads per 1024 elements (and one more with abuf)
+      // 16-byte loads: thread t holds elements 4 (t + i NT) .. + 3
       constexpr int P4 = PER / 4;
       const int n4 = D / (4 * NT);
       const float4* x4 = reinterpret_cast<const float4*>(xr);
       const float4* w4 = reinterpret_cast<const float4*>(w);
-      float4 xv[P4], wv[P4], gv[P4];
+      const size_t ps = (size_t)gridDim.x * D;
+      float4 xv[P4], wv[P4], gv[P4], pv[P4][8];
+      // every load first, then the bookkeeping's, then the sums; chunks past
+      // n4 re-read the last element (no branch, so no wait between the
+      // chunks' loads) and are discarded
 #pragma unroll
       for (int i = 0; i < P4; ++i) {
-        const int k4 = min((int)threadIdx.x + i * NT, D / 4 - 1);
+        const int k4 = min(tx + i * NT, D / 4 - 1);
         xv[i] = x4[k4];
         wv[i] = w4[k4];
         gv[i] = abuf ? reinterpret_cast<const float4*>(w_in)[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (parts) {
+#pragma unroll
+          for (int h = 0; h < 8; ++h) pv[i][h] = reinterpret_cast<const float4*>(parts + h * ps + ro)[k4];
+        }
       }
+      book();
       if (parts) {
-        const size_t ps = (size_t)gridDim.x * D;
 #pragma unroll
-        for (int i = 0; i < P4; ++i) {
-          const int k4 = min((int)threadIdx.x + i * NT, D / 4 - 1);
-          float4 pv[8];
-#pragma unroll
-          for (int h = 0; h < 8; ++h) pv[h] = reinterpret_cast<const float4*>(parts + h * ps + ro)[k4];
+        for (int i = 0; i < P4; ++i)
 #pragma unroll
           for (int h = 0; h < 8; ++h) {
-            xv[i].x = __fadd_rn(xv[i].x, pv[h].x); xv[i].y = __fadd_rn(xv[i].y, pv[h].y);
-            xv[i].z = __fadd_rn(xv[i].z, pv[h].z); xv[i].w = __fadd_rn(xv[i].w, pv[h].w);
+            xv[i].x = __fadd_rn(xv[i].x, pv[i][h].x); xv[i].y = __fadd_rn(xv[i].y, pv[i][h].y);
+            xv[i].z = __fadd_rn(xv[i].z, pv[i][h].z); xv[i].w = __fadd_rn(xv[i].w, pv[i][h].w);
           }
-        }
       }
       float s = 0.f;
 #pragma unroll
@@ -2857,6 +2887,7 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
           for (int h = 0; h < 8; ++h) xv[i] = __fadd_rn(xv[i], pv[h]);
         }
       }
+      book();
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < PER; ++i)
@@ -2886,6 +2917,7 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
         }
       }
     } else {   // (parts are only used with D <= NT * PER)
+      book();
       float s = 0.f;
       for (int k = threadIdx.x; k < D; k += NT) s += xr[k] * xr[k];
       const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
@@ -2904,20 +2936,20 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
         }
       }
     }
-    if (threadIdx.x == 0) { kv_len[b] += 1; pos[b] = p0 + 1; }
-    // (cos, sin) of the new position: from the per-position table (one load),
-    // computed only for positions past it
-    const int np = p0 + 1;
-    for (int t = threadIdx.x; t < half; t += NT)
-      rope[(size_t)b * half + t] = np < tab_n ? rope_tab[(size_t)np * half + t] : rope_cs(np, inv_freq[t]);
+    if (tx == 0) { kv_len[b] = kv0 + 1; pos[b] = np; }
+    // (cos, sin) of the new position: from the per-position table, computed
+    // only for positions past it
+    for (int t = tx; t < half; t += NT)
+      rope[(size_t)b * half + t] = np < tab_n ? (t == tx ? rp : rope_tab[(size_t)np * half + t])
+                                              : rope_cs(np, inv_freq[t]);
   }
   if (b == 0) {
-    const int next = *counter + 1;
     __syncthreads();
-    if (threadIdx.x == 0) *counter = next;
-    if (u_ring && next < max_frames) {
-      for (int i = threadIdx.x; i < nq; i += NT) u_cur[i] = u_ring[(size_t)next * nq + i];
-      if (threadIdx.x < 2) flag_cur[threadIdx.x] = flag_ring[2 * next + threadIdx.x];
+    const int next = cnt + 1;
+    if (tx == 0) *counter = next;
+    if (next < max_frames) {
+      for (int i = tx; i < nq; i += NT) u_cur[i] = i == tx ? u0 : u_ring[(size_t)next * nq + i];
+      if (tx < 2) flag_cur[tx] = f0;
     }
   }
 }

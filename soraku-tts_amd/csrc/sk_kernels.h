@@ -2770,8 +2770,9 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
   // for the stores and for the load before it.  The table row, draws and
   // flags are loaded right behind the row's loads (book()), unconditionally
   // at clamped indices (a load under a branch makes the join wait for it), so
-  // rope_tab, u_ring and flag_ring must be valid buffers; only the stores are
-  // conditional.  The frame counter is a vector load (opaque zero offset):
+  // rope_tab, u_ring and flag_ring must be valid buffers, and max_frames,
+  // half, tab_n and nq at least 1 (the engine's config checks ensure both);
+  // only the stores are conditional.  The frame counter is a vector load (opaque zero offset):
   // the first use of a scalar load waits for every scalar load in flight, and
   // the compiler puts that use ahead of the row's loads.  The asm statement
   // follows the scalar loads, since loads after it become vector loads too.

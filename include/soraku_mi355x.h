@@ -101,8 +101,10 @@ int sk_prefill_row(sk_engine* e, int32_t row, const int64_t* text_ids, int32_t n
  * Every row must be staged; the frame counter starts over. */
 int sk_prefill_run(sk_engine* e);
 /* sk_prefill_run that allocates no device memory.  No counterpart in the
- * reference: for callers that cannot allocate (code under HIP graph capture,
- * serving loops that must not stall on hipMalloc).  The prefill's activation
+ * reference: for callers that cannot allocate (serving loops that must not
+ * stall on hipMalloc, harnesses that forbid it).  It copies small host-side
+ * tables and waits for the engine's stream, so it cannot be recorded into a
+ * graph: on a capturing stream it returns SK_ESTATE.  The prefill's activation
  * buffers come from a scratch array of SK_NOALLOC_SCRATCH_BYTES in the
  * library's device code (one per GPU, held until the process ends) instead
  * of the engine's lazily grown buffers; a packed prefix that needs more
@@ -186,6 +188,15 @@ int32_t sk_frames_done(sk_engine* e);
  * SORAKU_XCD_LAYERS=0 was set at sk_create), 0 when it runs the per-op layer
  * kernels, -1 for a NULL engine.  For tests and profiling. */
 int32_t sk_xcd_layers(sk_engine* e);
+/* Test hook with no counterpart in the reference: the bound, in ticks of the
+ * 100 MHz real-time counter, of every wait inside the XCD-resident layers
+ * (barriers and tagged exchanges; default and maximum 5,000,000 = 50 ms).
+ * Set before sk_capture (SK_ESTATE after).  A wait that passes it makes the
+ * layer kernels leave the frame early and the next sk_step_frame /
+ * sk_synchronize / sk_read_codes return SK_EHIP; 0 makes nearly every wait
+ * give up at once, which is how a test forces that error path while every
+ * kernel still exits normally.  The engine must then be recreated. */
+int sk_debug_set_spin_ticks(sk_engine* e, uint64_t ticks);
 
 /* ---- operator API (tilelang_kernels.py counterparts) ------------------
  * All pointers are device pointers, all tensors contiguous row-major.

@@ -3,9 +3,7 @@
     python soraku-tts_amd/build.py [--jobs N]
 
 Compiles each ``csrc/*.hip`` to an object with ``hipcc --offload-arch=gfx950``
-and links them into ``soraku_amd/libsoraku_mi355x.so``; then builds
-``soraku_amd/sk_frame_driver`` (driver/frame_driver.hip), a plain executable
-that runs the engine through the C ABI.  Packed-FP32 VALU ops
+and links them into ``soraku_amd/libsoraku_mi355x.so``.  Packed-FP32 VALU ops
 are disabled for all device code (-packed-fp32-ops).
 """
 
@@ -22,8 +20,6 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "soraku_amd")
 LIB = os.path.join(OUT_DIR, "libsoraku_mi355x.so")
-DRIVER_SRC = os.path.join(HERE, "driver", "frame_driver.hip")
-DRIVER = os.path.join(OUT_DIR, "sk_frame_driver")
 OBJ_DIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -59,13 +55,6 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
-    # Stand-alone driver (C ABI only) for profilers that attach to a plain process.
-    cmd = [HIPCC, *FLAGS, DRIVER_SRC, "-L" + OUT_DIR, "-lsoraku_mi355x", "-Wl,-rpath,$ORIGIN",
-           "-o", DRIVER + ".tmp"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"driver build failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(DRIVER + ".tmp", DRIVER)
     if verbose:
         print(f"built {LIB}")
     return LIB

@@ -182,6 +182,7 @@ struct sk_engine {
   // launches' per-XCD partials, a zero block for the first layer's input,
   // barrier epochs and the error word (nonzero: a barrier timed out).
   bool lx = false;
+  unsigned long long spin_ticks = LX_SPIN_TICKS;   // bound of every barrier / exchange wait, in 10 ns ticks
   float *lx_xl = nullptr, *lx_xm = nullptr, *lx_opart = nullptr, *lx_dpart = nullptr, *lx_zero = nullptr;
   uint2 *lx_qkv = nullptr, *lx_act = nullptr;   // tagged exchange words (zeroed at creation)
   unsigned *lx_flags = nullptr, *lx_err = nullptr;
@@ -529,7 +530,7 @@ hipError_t enqueue_trunk_lx(sk_engine* e) {
     A.flags = e->lx_flags; A.err = e->lx_err;
     A.max_ctx = c.max_ctx; A.max_chunks = e->max_chunks;
     A.eps = c.trunk_eps; A.scale = 1.0f / sqrtf((float)c.head_dim);
-    A.spin_ticks = LX_SPIN_TICKS;
+    A.spin_ticks = e->spin_ticks;
     LxArgs C = A;
     C.wg = w.gate; C.wu = w.up; C.wd = w.down; C.gain = w.post_norm;
     C.xin = e->lx_xl; C.pin = e->lx_opart; C.xout = e->lx_xm; C.pout = e->lx_dpart;
@@ -1129,7 +1130,10 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     if (he == hipSuccess) he = dalloc(&e->lx_act, nact);
     if (he == hipSuccess) he = hipMemset(e->lx_qkv, 0, nqkv * sizeof(uint2));
     if (he == hipSuccess) he = hipMemset(e->lx_act, 0, nact * sizeof(uint2));
-    if (he == hipSuccess) he = hipMemset(e->lx_zero, 0, pe * sizeof(float));
+    // all zero at creation, so a frame whose layer launches left early (a
+    // barrier timeout) still reads finite values
+    for (float* z : {e->lx_zero, e->lx_xl, e->lx_xm, e->lx_opart, e->lx_dpart})
+      if (he == hipSuccess) he = hipMemset(z, 0, pe * sizeof(float));
     if (he == hipSuccess) he = hipMemset(e->lx_flags, 0, (size_t)LX_XCDS * LX_FLAGS * sizeof(unsigned));
     if (he == hipSuccess) he = hipMemset(e->lx_err, 0, sizeof(unsigned));
   }
@@ -1327,6 +1331,11 @@ int sk_prefill_run(sk_engine* e) {
 
 int sk_prefill_run_noalloc(sk_engine* e) {
   SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  // The prefill copies host-side tables and waits for its stream: it cannot
+  // be recorded into a graph.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  SK_HIP(hipStreamIsCapturing(e->stream, &cs));
+  SK_CHECK(cs == hipStreamCaptureStatusNone, SK_ESTATE, "sk_prefill_run_noalloc on a capturing stream");
   return prefill_staged(e, true, true);
 }
 
@@ -1406,6 +1415,14 @@ int sk_set_sampling(sk_engine* e, float cfg_scale, float temperature, int32_t to
   SK_HIP(hipStreamSynchronize(e->stream));
   SK_HIP(hipMemcpy(e->params, &p, sizeof(SkParams), hipMemcpyHostToDevice));
   e->p_host = p;
+  return SK_OK;
+}
+
+int sk_debug_set_spin_ticks(sk_engine* e, uint64_t ticks) {
+  SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
+  SK_CHECK(e->exec == nullptr, SK_ESTATE, "the spin limit is set before sk_capture");
+  SK_CHECK(ticks <= LX_SPIN_TICKS, SK_EINVAL, "spin limit above %llu ticks", LX_SPIN_TICKS);
+  e->spin_ticks = ticks;
   return SK_OK;
 }
 

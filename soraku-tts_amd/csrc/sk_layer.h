@@ -45,7 +45,11 @@
 // Every spin is bounded (spin_ticks of the 100 MHz real-time counter): a
 // workgroup that times out sets err bit 0 and leaves the launch (so would a
 // dispatch that gave an XCD other than 32 of the workgroups).  The host
-// reports err after a frame; a set bit makes every later barrier exit at once.
+// reports err after a frame.  A set bit ends the barrier waits that see it
+// (a long wait reads the error word every 64th poll), and every barrier of a
+// later launch, which finds it set at entry, returns at once without polling:
+// a failed frame costs at most about one spin limit, and the frames queued
+// behind it run through without waiting.
 #pragma once
 
 #include "sk_kernels.h"
@@ -165,22 +169,29 @@ __device__ __forceinline__ bool lx_all_ok(const int* ok) { return (ok[0] & ok[1]
 // The 32 workgroups of this XCD meet.  The waves that stored the data being
 // exchanged have waited for their stores; wave `poller` (one with no load in
 // flight) stores this workgroup's epoch and polls all 32, the other waves
-// only pass the two LDS barriers.  Returns false (uniformly) on a timeout, or
-// when err0 (the error word as the launch found it) is set.
+// only pass the two LDS barriers.  Returns false (uniformly) on a timeout,
+// when the error word is seen set during a long wait (it is read every 64th
+// poll, ~30 us apart, so the fast path polls the epochs alone), or at once,
+// without polling, when err0 (the error word as the launch found it) is set.
+// The epoch is stored in every case, so the XCD's other workgroups are not
+// held by this one.
 __device__ __forceinline__ bool lx_xcd_barrier(unsigned* fl, int j, unsigned target, unsigned long long deadline,
                                                unsigned err0, unsigned* err, int* okf, int poller) {
   lx_sync();
   const int tid = threadIdx.x;
   if ((tid >> 6) == poller) {
-    if ((tid & 63) == 0) __hip_atomic_store(fl + j, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    int good = 1;
-    for (;;) {
-      const unsigned v = __hip_atomic_load(fl + (tid & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int lane = tid & 63;
+    if (lane == 0) __hip_atomic_store(fl + j, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    int good = err0 == 0u;
+    for (unsigned it = 1; good; ++it) {
+      const unsigned v = __hip_atomic_load(fl + (lane & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (__builtin_amdgcn_ballot_w64((int)(v - target) < 0) == 0ull) break;
-      if (__builtin_amdgcn_s_memrealtime() > deadline) { good = 0; break; }
+      if (__builtin_amdgcn_s_memrealtime() > deadline)
+        good = 0;
+      else if ((it & 63u) == 0u && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+        good = 0;
     }
-    if (err0 != 0u) good = 0;   // an earlier launch failed: leave at once
-    if ((tid & 63) == 0) {
+    if (lane == 0) {
       *okf = good;
       if (!good) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }

@@ -78,6 +78,7 @@ PROTOTYPES = {
     "sk_stream": (_P, [_P]),
     "sk_frames_done": (_I, [_P]),
     "sk_xcd_layers": (_I, [_P]),
+    "sk_debug_set_spin_ticks": (_I, [_P, C.c_uint64]),
     "sk_op_add_rmsnorm": (_I, [_P, _I, _I, _F, _P, _P, _P, _P]),
     "sk_op_rmsnorm": (_I, [_P, _I, _I, _F, _P, _P, _P]),
     "sk_op_swiglu_gemv": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),

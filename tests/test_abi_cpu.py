@@ -90,6 +90,8 @@ def test_null_handles_are_rejected(L):
     assert L.sk_bind_weight(None, b"trunk.norm.weight", None, 0, None, 0) == SK_EINVAL
     assert L.sk_frames_done(None) == -1
     assert L.sk_xcd_layers(None) == -1
+    assert L.sk_debug_set_spin_ticks(None, 0) == SK_EINVAL
+    assert L.sk_prefill_run_noalloc(None) == SK_EINVAL
     assert L.sk_prefill_refill(None) == SK_EINVAL
     assert L.sk_retire_row(None, 0) == SK_EINVAL
     assert L.sk_reset_frames(None) == SK_EINVAL

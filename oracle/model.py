@@ -198,9 +198,9 @@ def attend(q, k, v, scale):
     rep = q.shape[0] // k.shape[0]
     kk = np.repeat(k, rep, axis=0)
     vv = np.repeat(v, rep, axis=0)
-    s = np.einsum("hd,htd->ht", q, kk) * scale
+    s = np.matmul(kk, q[:, :, None])[..., 0] * scale          # [Hq, ctx]
     p = softmax(s, -1)
-    return np.einsum("ht,htd->hd", p, vv)
+    return np.matmul(p[:, None, :], vv)[:, 0, :]
 
 
 # --------------------------------------------------------------------- model
@@ -300,9 +300,9 @@ class OracleModel:
             st.v[i, :, p0:ctx] = self._kv_store(v.transpose(1, 0, 2))
             kk = np.repeat(st.k[i, :, :ctx], rep, axis=0)
             vv = np.repeat(st.v[i, :, :ctx], rep, axis=0)
-            sc = np.einsum("nhd,htd->hnt", q, kk) * self.scale_attn
+            sc = np.matmul(q.transpose(1, 0, 2), kk.transpose(0, 2, 1)) * self.scale_attn   # [Hq, n, ctx]
             sc = np.where(causal[None], -np.inf, sc)
-            o = np.einsum("hnt,htd->nhd", softmax(sc, -1), vv).reshape(n, -1)
+            o = np.matmul(softmax(sc, -1), vv).transpose(1, 0, 2).reshape(n, -1)
             h = h + o @ self._lw(i, "self_attn.o_proj.weight").T
             h = self._mlp(i, h)
         st.kv_len = ctx

@@ -504,21 +504,35 @@ def test_batched_prefill_matches_oracle(hip_device, kv_bf16):
 
 
 def _many_utterance_case(s, w, n_utts, seed, hip_device, bf16=False, frames=2, max_len=64, text_len=(5, 30),
-                         kv_bf16=False):
+                         kv_bf16=False, prefix=None):
     """n_utts utterances with ragged prefixes, teacher-forced for `frames`
     frames through one engine; per utterance, the engine's masked merged
     logits and the oracle's for the same prefix and codes.  With kv_bf16 the
     engine and the oracle keep BF16 caches, and the result is the pair
-    (engine vs FP64 oracle, FP32 oracle vs FP64 oracle)."""
+    (engine vs FP64 oracle, FP32 oracle vs FP64 oracle).
+
+    ``prefix=(lo, hi)`` (or one such pair per utterance): the throughput
+    batch's prefixes instead of short ones -- each utterance's cond prefix
+    has P positions, P uniform in [lo, hi]: round(0.6 P) prompt frames after
+    the BOS frame, the rest text ids; its uncond row is one text id + the BOS
+    frame + the same prompt frames (runtime.py:143, model.py:632-653)."""
     from soraku_amd import GraphFrameEngine
 
     rng = np.random.default_rng(seed)
     items, codes = [], []
-    for _ in range(n_utts):
-        nt = int(rng.integers(*text_len))
+    for ui in range(n_utts):
+        if prefix is None:
+            nt, npr = int(rng.integers(*text_len)), int(rng.integers(0, 4))
+        else:
+            lo, hi = prefix[ui] if isinstance(prefix, list) else prefix
+            plen = int(rng.integers(lo, hi + 1))
+            npr = int(0.6 * plen + 0.5)
+            nt = plen - 1 - npr
         items.append((rng.integers(0, s.text_vocab, nt), np.array([int(rng.integers(0, s.text_vocab))]),
-                      rng.integers(0, s.codebook_size, (int(rng.integers(0, 4)), s.n_codebooks))))
+                      rng.integers(0, s.codebook_size, (npr, s.n_codebooks))))
         codes.append(rng.integers(0, s.codebook_size, (frames, s.n_codebooks)))
+    lens = [(t.size + 1 + p.shape[0], 2 + p.shape[0]) for t, _, p in items]
+    print(f"{n_utts} utterances, cond/uncond positions {lens}", flush=True)
     codes = np.stack(codes)                       # [utts, frames, Q]
     cfg = 1.5
     e = GraphFrameEngine(device=hip_device, max_cache_len=max_len, cfg_scale=cfg, batch=2, state_dict=w,
@@ -538,6 +552,7 @@ def _many_utterance_case(s, w, n_utts, seed, hip_device, bf16=False, frames=2, m
     m = OracleModel(s, w, np.float64, kv_bf16=kv_bf16)
     m32 = OracleModel(s, w, np.float32, kv_bf16=True) if kv_bf16 else None
     for u, (text, uncond, prompt) in enumerate(items):
+        print(f"oracle, utterance {u}", flush=True)
         ref = _oracle_forced_logits(m, s, text, prompt, uncond, codes[u], cfg)
         worst = max(worst, _rowwise_rel(got[u].reshape(-1, got.shape[-1]), ref))
         if kv_bf16:
@@ -614,6 +629,63 @@ def test_sixteen_utterances_q06b_bf16_kv(hip_device):
     rel, spread = _many_utterance_case(s, w, 16, 5, hip_device, bf16=True, frames=2, kv_bf16=True)
     print(f"q06b BF16 weights + BF16 KV, 16 utterances: engine {rel:.3e}, oracle FP32 vs FP64 {spread:.3e}")
     assert rel < max(LOGIT_TOL, 2 * spread)
+
+
+def test_sixteen_utterances_q06b_real_prefixes(hip_device):
+    """The throughput batch at its own workload: 16 utterances x CFG at the
+    Qwen3-0.6B shape, BF16 weights and BF16 KV cache, ragged cond prefixes of
+    120-240 positions from the batched prefill, KV capacity 512, 3
+    teacher-forced frames.  The streaming attention runs one split per (row,
+    kv head) here, 64 single-token slots of 8 lanes, so every slot holds 2-4
+    tokens of these contexts and runs its own online softmax over them
+    (model.py:658-676 attends over each branch's own history;
+    fast_generate.py:232-328 batches the rows).  Held to max(1e-3, 2 x the
+    oracle's own FP32-vs-FP64 spread with the same BF16 cache)."""
+    import dataclasses
+
+    from oracle.model import QWEN3_06B
+
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)
+    w = _device_weights(s, 18, hip_device)
+    rel, spread = _many_utterance_case(s, w, 16, 6, hip_device, bf16=True, frames=3, kv_bf16=True,
+                                       max_len=512, prefix=(120, 240))
+    print(f"q06b BF16 + BF16 KV, 16 utterances, 120-240-position prefixes: engine {rel:.3e}, "
+          f"oracle FP32 vs FP64 {spread:.3e}")
+    assert rel < max(LOGIT_TOL, 2 * spread)
+
+
+def test_sixteen_utterances_q06b_near_kv_capacity(hip_device):
+    """16 utterances x CFG at the Qwen3-0.6B shape, BF16 weights, FP32 KV
+    cache of 512 positions per row: six utterances with cond prefixes of
+    440-505 positions (uncond 266-305; 7-8 tokens per attention slot, and the
+    3 frames append up to position 508), ten of 120-240; FP64 oracle within
+    1e-3."""
+    import dataclasses
+
+    from oracle.model import QWEN3_06B
+
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)
+    w = _device_weights(s, 19, hip_device)
+    prefix = [(440, 505)] * 6 + [(120, 240)] * 10
+    rel = _many_utterance_case(s, w, 16, 8, hip_device, bf16=True, frames=3, max_len=512, prefix=prefix)
+    print(f"q06b BF16, 16 utterances, six with 440-505-position prefixes: max row-relative logit error {rel:.3e}")
+    assert rel < LOGIT_TOL
+
+
+def test_sixteen_utterances_tiny_long_contexts(hip_device):
+    """Tiny shape (head_dim 16: a slot is one lane, 512 slots per workgroup),
+    16 utterances x CFG: 4 splits per (row, kv head), so a slot's tokens are
+    2,048 apart.  Four utterances have cond prefixes of 2,600-3,000
+    positions (uncond 1,560-1,800), so a quarter to a half of their cond
+    rows' slots hold 2 tokens, the rest one; twelve have 20-60.  FP32
+    weights and cache against the FP64 oracle within 1e-3."""
+    from oracle.model import TINY
+
+    w = synthetic_weights(TINY, 33, norm_gain_std=0.1, bias_std=0.02)
+    prefix = [(2600, 3000)] * 4 + [(20, 60)] * 12
+    rel = _many_utterance_case(TINY, w, 16, 10, hip_device, frames=2, max_len=3072, prefix=prefix)
+    print(f"tiny, 16 utterances, four with 2,600-3,000-position prefixes: max row-relative logit error {rel:.3e}")
+    assert rel < LOGIT_TOL
 
 
 def test_generate_batch_per_utterance_equals_oracle(hip_device):

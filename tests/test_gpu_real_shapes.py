@@ -294,6 +294,124 @@ def test_xcd_layers_two_slots_per_workgroup(hip_device, monkeypatch):
     print(f"two slots per workgroup (657/562 positions): max row-relative logit difference {worst:.3e}")
 
 
+def _teacher_forced_vs_oracle(e, m, states, s, text, prompt, uncond, codes, cfg):
+    """Masked merged logits of every depth step, teacher-forced on `codes`,
+    engine against the oracle from its prefilled `states`; the largest
+    row-relative error."""
+    from test_gpu_engine import _engine_forced_logits, _oracle_forced_logits
+
+    ref = _oracle_forced_logits(m, s, text, prompt, uncond, codes, cfg, states=states)
+    got = _engine_forced_logits(e, s, codes)
+    return _rowwise_rel(got, ref)
+
+
+def _long_prefix_vs_oracle(s, w, hip_device, text, uncond, prompt, max_ctx, bf16, seed):
+    """Teacher-forced logits over 3 frames, then sampled codes over 4 frames
+    (each on its own engine) against the float64 oracle at a long prefix."""
+    import copy
+
+    m = OracleModel(s, w, np.float64)
+    states = start_states(m, text, prompt, uncond, C3["cfg_scale"], max_ctx)
+    g = {k: C3[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
+    e = _engine(s, w, hip_device, text, uncond, prompt, max_ctx, bf16=bf16, **g)
+    assert e.xcd_layers
+    codes = np.random.default_rng(seed).integers(0, s.codebook_size, (3, s.n_codebooks))
+    rel = _teacher_forced_vs_oracle(e, m, copy.deepcopy(states), s, text, prompt, uncond, codes, C3["cfg_scale"])
+    e.close()
+    print(f"teacher-forced, 3 frames: max row-relative logit error {rel:.3e}", flush=True)
+    assert rel < LOGIT_TOL
+    e = _engine(s, w, hip_device, text, uncond, prompt, max_ctx, bf16=bf16, **C3)
+    u = np.random.default_rng(seed + 1).random((4, s.n_codebooks))
+    done, worst = _free_running_vs_oracle(e, m, states, s, u, C3, text, prompt, uncond)
+    e.close()
+    print(f"sampled: {done} frames equal, max logit error {worst:.3e}")
+    assert done >= 3
+    return rel, worst
+
+
+def test_q06b_two_slots_per_workgroup_vs_oracle(hip_device):
+    """Qwen3-0.6B FP32 with 657 / 562 cached positions: 21 + 18 = 39 chunk
+    slots of the XCD-resident attention half, more than the 32 workgroups
+    of an XCD, so workgroups 0-6 take a second slot (K/V loads after the
+    first slot's barrier, the merge over more than 16 chunks); teacher-forced
+    logits and sampled codes against the float64 oracle."""
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)
+    w = synthetic_weights(s, 21, norm_gain_std=0.1, bias_std=0.02)
+    rng = np.random.default_rng(21)
+    text = rng.integers(0, s.text_vocab, 96)
+    prompt = rng.integers(0, s.codebook_size, (560, s.n_codebooks))
+    uncond = np.array([5])
+    assert text.size + 1 + prompt.shape[0] == 657 and uncond.size + 1 + prompt.shape[0] == 562
+    _long_prefix_vs_oracle(s, w, hip_device, text, uncond, prompt, 680, False, 23)
+
+
+def test_q17b_late_frame_contexts_vs_oracle(hip_device):
+    """Qwen3-1.7B shape, BF16 weights, FP32 KV, at the contexts the last of
+    C5's 480 frames reach: cond 720 positions (95 text ids + BOS frame + 624
+    prompt frames, through the batched prefill), uncond 626.  That is 23 + 20
+    = 43 chunk slots at d = 2048, so every XCD's workgroups 0-10 take a
+    second slot; teacher-forced logits (3 frames) and sampled codes (4
+    frames) against the float64 oracle on the same BF16-rounded weights
+    (model.py:567-612, graph_frame.py:247-270)."""
+    from test_gpu_engine import _device_weights
+
+    s = dataclasses.replace(QWEN3_17B, text_vocab=4096)
+    w = _device_weights(s, 720, hip_device)
+    rng = np.random.default_rng(720)
+    text = rng.integers(0, s.text_vocab, 95)
+    prompt = rng.integers(0, s.codebook_size, (624, s.n_codebooks))
+    uncond = np.array([13])
+    assert text.size + 1 + prompt.shape[0] == 720 and uncond.size + 1 + prompt.shape[0] == 626
+    _long_prefix_vs_oracle(s, w, hip_device, text, uncond, prompt, 740, True, 721)
+
+
+def test_barrier_timeout_reports_error_and_fresh_engine_decodes(hip_device):
+    """The XCD-resident layers' bounded waits, forced to give up from the
+    host (sk_debug_set_spin_ticks(e, 0): every barrier or exchange wait that
+    does not find its data at the first look ends): every kernel still
+    exits, sk_step_frame returns SK_EHIP with its message soon after, and a
+    freshly created engine on the same weights then decodes the C3 prefix's
+    first teacher-forced frame as the reference did."""
+    import time
+
+    from soraku_amd._lib import SK_EHIP, SK_ESTATE, SkError, check, lib
+
+    f, s, gen = load_golden("q06b_sampled")
+    w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                          bias_std=float(f["bias_std"]))
+    text, uncond, prompt = _c3_inputs(f)
+    g = {k: gen[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
+    from soraku_amd import GraphFrameEngine
+
+    e = GraphFrameEngine(device=hip_device, max_cache_len=260, cfg_scale=g["cfg_scale"], batch=2, state_dict=w,
+                         shape=_shape(s))
+    e.set_temperature(g["temperature"])
+    e.set_sampling(sampled=True, top_k=g["top_k"], top_p=g["top_p"])
+    e.prefill(text, uncond, prompt)
+    check(lib().sk_debug_set_spin_ticks(e._h, 0))
+    e.capture()
+    assert e.xcd_layers
+    with pytest.raises(SkError) as ei:
+        check(lib().sk_debug_set_spin_ticks(e._h, 0))
+    assert ei.value.code == SK_ESTATE   # only before capture
+    t0 = time.time()
+    with pytest.raises(SkError) as ei:
+        e.step_frame(mask_eos_q0=True, uniforms=np.zeros(s.n_codebooks), forced_codes=f["codes"][0])
+    dt = time.time() - t0
+    print(f"forced timeout: {ei.value} after {dt:.3f} s", flush=True)
+    assert ei.value.code == SK_EHIP and "barrier timed out" in str(ei.value)
+    assert dt < 5.0
+    e.close()
+    e = _engine(s, w, hip_device, text, uncond, prompt, 260, **g)
+    _, lg = e.step_frame(mask_eos_q0=True, uniforms=np.zeros(s.n_codebooks), forced_codes=f["codes"][0],
+                         return_logits=True)
+    e.synchronize()
+    e.close()
+    rel = _rowwise_rel(lg[0], f["sample_logits"][: s.n_codebooks])
+    print(f"fresh engine after the timeout: row-relative logit error vs reference {rel:.3e}")
+    assert rel < LOGIT_TOL
+
+
 def test_untied_head_through_model_binding(hip_device):
     """GraphFrameEngine(model) with a SorakuTTSv2-like module whose config has
     tie_audio_head=False binds depth_head.out_proj as the classifier

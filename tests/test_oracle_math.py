@@ -324,7 +324,7 @@ def test_attention_closed_forms():
     np.testing.assert_allclose(out, np.repeat(v1[:, 0], 2, 0), rtol=1e-14)   # one token -> v
     keq = np.repeat(rng.standard_normal((Hkv, 1, hd)), 9, axis=1)             # equal keys -> mean of V
     v = rng.standard_normal((Hkv, 9, hd))
-    np.testing.assert_allclose(attend(q, keq, v, 0.25), np.repeat(v.mean(1), 2, 0), rtol=1e-12)
+    np.testing.assert_allclose(attend(q, keq, v, 0.25), np.repeat(v.mean(1), 2, 0), rtol=1e-12, atol=1e-15)
     k = rng.standard_normal((Hkv, 9, hd))
     # GQA: q head h reads kv head h // (Hq / Hkv); brute force per head
     for h in range(Hq):

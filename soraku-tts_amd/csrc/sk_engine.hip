@@ -178,12 +178,12 @@ struct sk_engine {
   float* gbuf[2] = {nullptr, nullptr};
 
   // XCD-resident trunk layers (lx_attn_kernel + lx_mlp_kernel per layer, one
-  // utterance with CFG, 8 KV heads): residual stream after each launch, the
-  // launches' per-XCD partials, a zero block for the first layer's input,
-  // barrier epochs and the error word (nonzero: a barrier timed out).
+  // utterance with CFG, 8 KV heads): the residual stream's three rotating
+  // fixed-point accumulators, barrier epochs and the error word (nonzero: a
+  // barrier timed out).
   bool lx = false;
   unsigned long long spin_ticks = LX_SPIN_TICKS;   // bound of every barrier / exchange wait, in 10 ns ticks
-  float *lx_xl = nullptr, *lx_xm = nullptr, *lx_opart = nullptr, *lx_dpart = nullptr, *lx_zero = nullptr;
+  unsigned long long* lx_acc = nullptr;   // [3][rows][d], 2^-32 units
   uint2 *lx_qkv = nullptr, *lx_act = nullptr;   // tagged exchange words (zeroed at creation)
   unsigned *lx_flags = nullptr, *lx_err = nullptr;
 
@@ -499,30 +499,42 @@ bool lx_fits(const sk_engine* e) {
 }
 
 template <typename WL, typename KT>
-hipError_t launch_lx(int d, const LxArgs& A, const LxArgs& C, hipStream_t st) {
+hipError_t launch_lx(int d, bool first, const LxArgs& A, const LxArgs& C, hipStream_t st) {
   if (d == 1024) {
-    hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 1024>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
+    if (first) hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 1024, false>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
+    else hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 1024, true>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
     hipLaunchKernelGGL((lx_mlp_kernel<WL, 1024, 3072>), dim3(LX_WGS), dim3(LX_NT), 0, st, C);
   } else {
-    hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 2048>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
+    if (first) hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 2048, false>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
+    else hipLaunchKernelGGL((lx_attn_kernel<WL, KT, 2048, true>), dim3(LX_WGS), dim3(LX_NT), 0, st, A);
     hipLaunchKernelGGL((lx_mlp8_kernel<WL, 2048, 6144>), dim3(LX_WGS), dim3(LX_NT), 0, st, C);
   }
   return hipGetLastError();
 }
 
-// Each layer as two launches: attention half (x + partials -> q/k/v ->
-// attention -> O partials) and MLP half (x + O partials -> SwiGLU -> down
-// partials); the final norm adds the last layer's down partials.
+// Fixed-point accumulator k % 3 of the XCD-resident layers (sk_layer.h).
+unsigned long long* lx_acc(const sk_engine* e, int k) {
+  return e->lx_acc + (size_t)(k % 3) * e->rows * e->c.d_model;
+}
+
+// Each layer as two launches: attention half (x -> q/k/v -> attention -> O
+// partials) and MLP half (x -> SwiGLU -> down partials).  Launch i = 2 l + h
+// reads accumulator i (the first one the FP32 frame embedding), adds x and
+// its partials into accumulator i + 1 and clears accumulator i + 2; the final
+// norm reads accumulator 2 L and clears accumulator 1, the first launch's
+// target of the next frame.
 hipError_t enqueue_trunk_lx(sk_engine* e) {
   const sk_config& c = e->c;
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerW& w = e->L[l];
+    const int i = 2 * l;
     LxArgs A{};
     A.wq = w.q; A.wk = w.k; A.wv = w.v; A.wo = w.o;
     A.gain = w.in_norm; A.q_norm = w.q_norm; A.k_norm = w.k_norm;
-    A.xin = l == 0 ? e->x : e->lx_xm;
-    A.pin = l == 0 ? e->lx_zero : e->lx_dpart;
-    A.xout = e->lx_xl; A.pout = e->lx_opart;
+    A.xin = e->x;
+    A.acc_in = reinterpret_cast<const long long*>(lx_acc(e, i));
+    A.acc_out = lx_acc(e, i + 1);
+    A.acc_clear = lx_acc(e, i + 2);
     A.qkv = e->lx_qkv; A.part = e->part; A.act = e->lx_act; A.ld_act = c.trunk_inter;
     A.kc = e->kc + (size_t)l * kv_layer_bytes(e);
     A.vc = e->vc + (size_t)l * kv_layer_bytes(e);
@@ -533,11 +545,16 @@ hipError_t enqueue_trunk_lx(sk_engine* e) {
     A.spin_ticks = e->spin_ticks;
     LxArgs C = A;
     C.wg = w.gate; C.wu = w.up; C.wd = w.down; C.gain = w.post_norm;
-    C.xin = e->lx_xl; C.pin = e->lx_opart; C.xout = e->lx_xm; C.pout = e->lx_dpart;
+    C.acc_in = reinterpret_cast<const long long*>(lx_acc(e, i + 1));
+    C.acc_out = lx_acc(e, i + 2);
+    C.acc_clear = lx_acc(e, i + 3);
     const bool wbf = c.weight_dtype == SK_BF16, kbf = c.kv_dtype == SK_BF16;
     const int d = c.d_model;
-    const hipError_t err = wbf ? (kbf ? launch_lx<WBF16, uint16_t>(d, A, C, e->stream) : launch_lx<WBF16, float>(d, A, C, e->stream))
-                               : (kbf ? launch_lx<WF32, uint16_t>(d, A, C, e->stream) : launch_lx<WF32, float>(d, A, C, e->stream));
+    const bool first = l == 0;
+    const hipError_t err = wbf ? (kbf ? launch_lx<WBF16, uint16_t>(d, first, A, C, e->stream)
+                                      : launch_lx<WBF16, float>(d, first, A, C, e->stream))
+                               : (kbf ? launch_lx<WF32, uint16_t>(d, first, A, C, e->stream)
+                                      : launch_lx<WF32, float>(d, first, A, C, e->stream));
     if (err != hipSuccess) return err;
   }
   return hipSuccess;
@@ -761,8 +778,9 @@ hipError_t enqueue_tail(sk_engine* e) {
   const int d = c.d_model, M = e->rows;
   hipError_t err;
   if ((err = enqueue_trunk(e)) != hipSuccess) return err;
-  hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->lx ? e->lx_xm : e->x,
-                     e->lx ? e->lx_dpart : nullptr, e->final_norm,
+  hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x,
+                     e->lx ? reinterpret_cast<const long long*>(lx_acc(e, 2 * c.n_layers)) : nullptr,
+                     e->lx ? lx_acc(e, 1) : nullptr, e->final_norm,
                      c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->fc, e->u_ring,
                      e->flag_ring, e->u_cur, e->flag_cur, c.n_utts * c.n_codebooks, c.max_frames,
                      e->inv_freq, c.head_dim / 2, e->rope, (const float2*)e->p_rope, c.max_ctx + 1,
@@ -1117,12 +1135,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     e->lx = he == hipSuccess && mapped;
   }
   if (he == hipSuccess && e->lx) {
-    const size_t pe = (size_t)LX_XCDS * R * d;
-    he = dalloc(&e->lx_xl, pe);   // one copy of the residual stream per XCD
-    if (he == hipSuccess) he = dalloc(&e->lx_xm, pe);
-    if (he == hipSuccess) he = dalloc(&e->lx_opart, pe);
-    if (he == hipSuccess) he = dalloc(&e->lx_dpart, pe);
-    if (he == hipSuccess) he = dalloc(&e->lx_zero, pe);
+    he = dalloc(&e->lx_acc, 3 * (size_t)R * d);
     if (he == hipSuccess) he = dalloc(&e->lx_flags, (size_t)LX_XCDS * LX_FLAGS);
     if (he == hipSuccess) he = dalloc(&e->lx_err, 1);
     const size_t nqkv = (size_t)R * (c.n_q_heads + 2 * c.n_kv_heads) * c.head_dim, nact = (size_t)R * c.trunk_inter;
@@ -1130,10 +1143,10 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     if (he == hipSuccess) he = dalloc(&e->lx_act, nact);
     if (he == hipSuccess) he = hipMemset(e->lx_qkv, 0, nqkv * sizeof(uint2));
     if (he == hipSuccess) he = hipMemset(e->lx_act, 0, nact * sizeof(uint2));
-    // all zero at creation, so a frame whose layer launches left early (a
-    // barrier timeout) still reads finite values
-    for (float* z : {e->lx_zero, e->lx_xl, e->lx_xm, e->lx_opart, e->lx_dpart})
-      if (he == hipSuccess) he = hipMemset(z, 0, pe * sizeof(float));
+    // all zero at creation: the first frame's first launch adds into
+    // accumulator 1 (and a frame whose layer launches left early, after a
+    // barrier timeout, still reads finite values)
+    if (he == hipSuccess) he = hipMemset(e->lx_acc, 0, 3 * (size_t)R * d * sizeof(unsigned long long));
     if (he == hipSuccess) he = hipMemset(e->lx_flags, 0, (size_t)LX_XCDS * LX_FLAGS * sizeof(unsigned));
     if (he == hipSuccess) he = hipMemset(e->lx_err, 0, sizeof(unsigned));
   }
@@ -1155,7 +1168,7 @@ int sk_destroy(sk_engine* e) {
                   e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->flag_ring, e->u_ring,
                   e->pf_mem, e->ptab, e->gbuf[0], e->gbuf[1],
-                  e->lx_xl, e->lx_xm, e->lx_opart, e->lx_dpart, e->lx_zero, e->lx_qkv, e->lx_act,
+                  e->lx_acc, e->lx_qkv, e->lx_act,
                   e->lx_flags, e->lx_err,
                   e->p_row_start, e->p_rope,
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};

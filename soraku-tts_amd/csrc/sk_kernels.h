@@ -2751,9 +2751,11 @@ __global__ __launch_bounds__(NT) void rope_rows_kernel(const int* pos, const flo
 // are copied from the ring to the fixed current-frame slots.  With abuf set it
 // also writes depth step 0's input, RMSNorm_in(hidden) (the codebook prefix is
 // zero when a frame starts), and its split form when xs_abuf is set.  With
-// parts set the trunk's last layer left its residual update as 8 per-XCD
-// partials [8][rows][D]: x + parts[0] + ... + parts[7] is normed, in that order.
-__global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const float* parts, const float* w, float eps,
+// xfix set the input row is the XCD-resident layers' fixed-point residual
+// stream [rows][D] (2^-32 units) instead of x, and fix_clear (set with it) is
+// the accumulator whose row this workgroup zeroes once the input is read.
+__global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const long long* xfix,
+                                                        unsigned long long* fix_clear, const float* w, float eps,
                                                         int D, float* hidden, int* kv_len, int* pos,
                                                         const int* active, int* counter,
                                                         const double* u_ring, const int* flag_ring,
@@ -2798,7 +2800,7 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
     const float* xr = x + (size_t)b * D;
     const size_t ro = (size_t)b * D;
     constexpr int PER = 16;              // D <= 4096 in registers, all loads issued at once
-    const bool al16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(parts) |
+    const bool al16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(xfix) |
                         reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(w_in) |
                         reinterpret_cast<uintptr_t>(hidden)) & 15u) == 0;
     if (al16 && D % (4 * NT) == 0 && D <= NT * PER) {
@@ -2807,37 +2809,45 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
       const int n4 = D / (4 * NT);
       const float4* x4 = reinterpret_cast<const float4*>(xr);
       const float4* w4 = reinterpret_cast<const float4*>(w);
-      const size_t ps = (size_t)gridDim.x * D;
-      float4 xv[P4], wv[P4], gv[P4], pv[P4][8];
+      const ulonglong2* f2 = xfix ? reinterpret_cast<const ulonglong2*>(xfix + ro) : nullptr;
+      float4 xv[P4], wv[P4], gv[P4];
+      ulonglong2 fv[P4][2];
       // every load first, then the bookkeeping's, then the sums; chunks past
       // n4 re-read the last element (no branch, so no wait between the
       // chunks' loads) and are discarded
 #pragma unroll
       for (int i = 0; i < P4; ++i) {
         const int k4 = min(tx + i * NT, D / 4 - 1);
-        xv[i] = x4[k4];
+        if (xfix) {
+          fv[i][0] = f2[2 * k4];
+          fv[i][1] = f2[2 * k4 + 1];
+        } else {
+          xv[i] = x4[k4];
+        }
         wv[i] = w4[k4];
         gv[i] = abuf ? reinterpret_cast<const float4*>(w_in)[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (parts) {
-#pragma unroll
-          for (int h = 0; h < 8; ++h) pv[i][h] = reinterpret_cast<const float4*>(parts + h * ps + ro)[k4];
-        }
       }
       book();
-      if (parts) {
+      if (xfix) {   // the XCD-resident layers' fixed-point residual stream (2^-32 units)
 #pragma unroll
         for (int i = 0; i < P4; ++i)
-#pragma unroll
-          for (int h = 0; h < 8; ++h) {
-            xv[i].x = __fadd_rn(xv[i].x, pv[i][h].x); xv[i].y = __fadd_rn(xv[i].y, pv[i][h].y);
-            xv[i].z = __fadd_rn(xv[i].z, pv[i][h].z); xv[i].w = __fadd_rn(xv[i].w, pv[i][h].w);
-          }
+          xv[i] = make_float4((float)(long long)fv[i][0].x * 0x1p-32f, (float)(long long)fv[i][0].y * 0x1p-32f,
+                              (float)(long long)fv[i][1].x * 0x1p-32f, (float)(long long)fv[i][1].y * 0x1p-32f);
       }
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < P4; ++i)
         if (i < n4) s += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
       const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
+      if (fix_clear) {   // every thread's loads are consumed: the row may be the one read
+        ulonglong2* c2 = reinterpret_cast<ulonglong2*>(fix_clear + ro);
+#pragma unroll
+        for (int i = 0; i < P4; ++i)
+          if (i < n4) {
+            c2[2 * (tx + i * NT)] = make_ulonglong2(0ull, 0ull);
+            c2[2 * (tx + i * NT) + 1] = make_ulonglong2(0ull, 0ull);
+          }
+      }
       float s2 = 0.f;
       float4* h4 = reinterpret_cast<float4*>(hidden + ro);
 #pragma unroll
@@ -2872,21 +2882,9 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int k = min((int)threadIdx.x + i * NT, D - 1);
-        xv[i] = xr[k];
+        xv[i] = xfix ? (float)xfix[ro + k] * 0x1p-32f : xr[k];
         wv[i] = w[k];
         gv[i] = abuf ? w_in[k] : 0.f;
-      }
-      if (parts) {
-        const size_t ps = (size_t)gridDim.x * D;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-          const int k = min((int)threadIdx.x + i * NT, D - 1);
-          float pv[8];
-#pragma unroll
-          for (int h = 0; h < 8; ++h) pv[h] = parts[h * ps + ro + k];
-#pragma unroll
-          for (int h = 0; h < 8; ++h) xv[i] = __fadd_rn(xv[i], pv[h]);
-        }
       }
       book();
       float s = 0.f;
@@ -2894,6 +2892,11 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
       for (int i = 0; i < PER; ++i)
         if ((int)threadIdx.x + i * NT < D) s += xv[i] * xv[i];
       const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + eps);
+      if (fix_clear) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+          if ((int)threadIdx.x + i * NT < D) fix_clear[ro + threadIdx.x + i * NT] = 0ull;
+      }
       float s2 = 0.f;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
@@ -2917,7 +2920,7 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const fl
           }
         }
       }
-    } else {   // (parts are only used with D <= NT * PER)
+    } else {   // (the fixed-point input is only used with D <= NT * PER)
       book();
       float s = 0.f;
       for (int k = threadIdx.x; k < D; k += NT) s += xr[k] * xr[k];

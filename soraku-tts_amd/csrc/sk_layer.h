@@ -9,25 +9,33 @@
 // dimension -- gate/up rows -> those columns of the down projection -- stay on
 // one XCD and pass through its L2:
 //
-//   lx_attn_kernel: x = x_in + sum_h part_in[h] (h = 0..7, fixed order) ->
-//     RMSNorm -> q/k/v rows of KV head g -> (tagged) -> QK-norm, RoPE, KV
-//     append, 32-token attention chunks of head g -> barrier -> chunk merge ->
-//     O[:, head g's 256 columns] . attn = this XCD's partial of the residual
-//     update, part_out[g];
-//   lx_mlp_kernel (lx_mlp8_kernel at the 1.7B shape): x = x_in +
-//     sum_h part_in[h] -> RMSNorm -> gate/up rows of inner slice g -> SwiGLU
-//     -> (tagged) -> down[:, slice g] . act = part_out[g].
+//   lx_attn_kernel: x -> RMSNorm -> q/k/v rows of KV head g -> (tagged) ->
+//     QK-norm, RoPE, KV append, 32-token attention chunks of head g ->
+//     barrier -> chunk merge -> O[:, head g's 256 columns] . attn = this
+//     XCD's partial of the residual update;
+//   lx_mlp_kernel (lx_mlp8_kernel at the 1.7B shape): x -> RMSNorm ->
+//     gate/up rows of inner slice g -> SwiGLU -> (tagged) -> down[:, slice
+//     g] . act = this XCD's partial.
 //
-// The next launch (or the final norm) adds the 8 partials in XCD order, so the
-// projections' sums are taken in a fixed order and replays stay bitwise equal.
+// The residual stream between the launches is 64-bit fixed point (2^-32
+// units): each launch reads x whole from one accumulator and adds its
+// partials (XCD 0 also adds x itself) into the next with integer atomics,
+// which commute, so the sum is exact and replays stay bitwise equal.  Every
+// launch thus reads its input in one load, with no exchange before its first
+// projection.  Three accumulators rotate: launch i reads acc[i % 3] (the
+// first layer reads the FP32 frame embedding), adds into acc[(i + 1) % 3] and
+// clears acc[(i + 2) % 3], which launch i - 1 read; the final norm reads the
+// last one and clears the first layer's target for the next frame.
 //
 // Barrier among the 32 workgroups of an XCD (lx_xcd_barrier): each workgroup
 // stores its epoch in its own word of the XCD's flag line and one wave polls
 // the 32 words with agent-scope loads, which read the L2 (0.5 us measured,
-// against 1.6 us for a kernel boundary).  Data exchanged through it (the input
-// sums, the chunk partials) is written with plain stores whose completion the
-// writer waits for, and read after it with plain loads; the q/k/v rows and the
+// against 1.6 us for a kernel boundary).  Data exchanged through it (the
+// chunk partials) is written with plain stores whose completion the writer
+// waits for, and read after it with plain loads; the q/k/v rows and the
 // SwiGLU output pass without a barrier, as tagged words (lx_put, lx_settle).
+// The epochs advance by one per launch (the attention half's chunk barrier,
+// or a plain store in the MLP half), and the tags are the launch's epoch.
 // On gfx9 one counter (vmcnt) covers loads and stores and
 // retires in issue order, so waiting for a store also waits for every load
 // issued before it, and a load's data is usable only once every earlier load
@@ -35,10 +43,9 @@
 //   * exchange waves (0-3) issue the first phase's weights and do the q/k/v
 //     or SwiGLU exchange and the chunk partials' barrier; they hold no
 //     prefetch across an exchange;
-//   * stream waves (4-7) sum the input (their workgroup's slice, the input
-//     barrier, the gather), then issue the later phases' K/V and weights ahead
-//     of use and take their inputs from LDS, so nothing they wait for is
-//     behind an exchange.
+//   * stream waves (4-7) load the input into LDS, then issue the later
+//     phases' K/V and weights ahead of use and take their inputs from LDS,
+//     so nothing they wait for is behind an exchange.
 // Each role is straight-line code and both execute the same sequence of LDS
 // barriers (lx_sync); none of them waits for global loads.
 //
@@ -73,10 +80,10 @@ struct LxArgs {
   const void* wg; const void* wu; const void* wd;
   const float* gain;                 // RMSNorm gain of the launch's input (in_norm / post_norm)
   const float* q_norm; const float* k_norm;
-  const float* xin;                  // [M][D] residual stream entering the launch
-  const float* pin;                  // [8][M][D] partials to add (zeros for the first layer)
-  float* xout;                       // [8][M][D] xin + sum(pin), one copy per XCD (copy 0 is read next)
-  float* pout;                       // [8][M][D] this launch's partials
+  const float* xin;                  // [M][D] FP32 input (the first layer: the frame embedding)
+  const long long* acc_in;           // [M][D] fixed-point input (every later launch)
+  unsigned long long* acc_out;       // [M][D] accumulator this launch adds x + its partials into
+  unsigned long long* acc_clear;     // [M][D] accumulator this launch clears
   uint2* qkv;                        // [M][(HQ + 2 HKV) HD] raw projections, tagged (exchanged)
   float* part;                       // [M][HQ][max_chunks][HD + 4] chunk partials (exchanged)
   uint2* act; int ld_act;            // [M][ld_act] SwiGLU output, tagged (exchanged)
@@ -200,53 +207,78 @@ __device__ __forceinline__ bool lx_xcd_barrier(unsigned* fl, int j, unsigned tar
   return *okf != 0;
 }
 
-// Input of a launch, gathered by the stream waves (threads 256..511) of the
-// XCD's 32 workgroups together.  Workgroup j sums its 1/32 slice of
-// x = xin + pin[0] + ... + pin[7] (both rows, M D / 32 elements, in that
-// order) into the XCD's copy xout[g]; after an XCD barrier every workgroup
-// reads the whole copy from the L2 into LDS (xsh, before the norm) with each
-// stream wave's sum of squares (ssq[w4]), and the norm gain into gsh.  Per CU
-// that is ~10 KB of loads instead of the 9 whole vectors (74 KB at d = 1024)
-// a workgroup read when it summed alone, on the CU path its weight stream
-// uses too.  All 8 copies are equal; the next launch reads copy 0.
-template <int D>
-struct LxInput {
-  static constexpr int SL = LX_M * D / LX_PER;   // slice elements per workgroup: 64 or 128
-  static constexpr int EPT = LX_M * D / 256;     // elements per stream thread in the whole copy
+// Fixed-point residual stream: value * 2^32 in a 64-bit integer.  FP32 to
+// fixed point drops only bits below 2^-32; fixed point to FP32 rounds once.
+constexpr float LX_FIX_ONE = 4294967296.0f;
+__device__ __forceinline__ long long lx_fix(float v) { return (long long)(v * LX_FIX_ONE); }
+__device__ __forceinline__ float lx_unfix(long long q) { return (float)q * (1.0f / LX_FIX_ONE); }
+// Partial v of output (m, n), plus x (fixed point) on XCD 0, into the next
+// accumulator.
+__device__ __forceinline__ void lx_accum(unsigned long long* acc, size_t idx, float v, long long x) {
+  __hip_atomic_fetch_add(acc + idx, (unsigned long long)(lx_fix(v) + x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Input of a launch, loaded by the stream waves (threads 256..511): stream
+// thread st holds elements st * EPT .. st * EPT + EPT - 1 of x [M][D] (so
+// stream waves 2m and 2m + 1 hold row m), fixed point (FIX) or FP32 (the
+// first layer), and its 1/256 share of the norm gain.  finish() writes x to
+// LDS as FP32 with each stream wave's sum of squares (ssq[w4]) and the gain
+// to gsh.  clear() zeroes this workgroup's 1/256 share of acc_clear.  xo()
+// is x[m][n] in fixed point, for the XCD-0 workgroups' accumulation.
+template <int D, bool FIX>
+struct LxIn {
+  static constexpr int EPT = LX_M * D / 256;     // elements per stream thread
   static constexpr int GPT = D / 256;            // gain elements per stream thread
-  static_assert(SL <= 256 && EPT % 4 == 0 && GPT % 4 == 0 && 64 * EPT <= D, "LxInput shape");
-  float sv[9];
+  static constexpr int CPW = LX_M * D / LX_WGS;  // accumulator entries each workgroup clears
+  static_assert(EPT % 4 == 0 && GPT % 4 == 0 && CPW % 2 == 0 && 64 * EPT <= D, "LxIn shape");
+  ulonglong2 xq[FIX ? EPT / 2 : 1];
+  float4 xf[FIX ? 1 : EPT / 4];
   float4 gv[GPT / 4];
-  __device__ __forceinline__ void issue(const LxArgs& a, int st, int j) {
-    const size_t e = (size_t)j * SL + min(st, SL - 1);   // threads past the slice re-read its last element
-    sv[0] = a.xin[e];
+  __device__ __forceinline__ void issue(const LxArgs& a, int st) {
+    if constexpr (FIX) {
+      const ulonglong2* src = reinterpret_cast<const ulonglong2*>(a.acc_in + (size_t)st * EPT);
 #pragma unroll
-    for (int h = 0; h < 8; ++h) sv[1 + h] = a.pin[(size_t)h * LX_M * D + e];
+      for (int i = 0; i < EPT / 2; ++i) xq[i] = src[i];
+    } else {
+      const float4* src = reinterpret_cast<const float4*>(a.xin + (size_t)st * EPT);
+#pragma unroll
+      for (int i = 0; i < EPT / 4; ++i) xf[i] = src[i];
+    }
 #pragma unroll
     for (int i = 0; i < GPT / 4; ++i) gv[i] = *reinterpret_cast<const float4*>(a.gain + st * GPT + 4 * i);
   }
-  // the slice's sum to the XCD copy, the gain to LDS (nothing is held across
-  // the barrier that follows)
-  __device__ __forceinline__ void slice(const LxArgs& a, int g, int st, int j, float* gsh) {
+  __device__ __forceinline__ static long long xo(const LxArgs& a, int m, int n) {
+    if constexpr (FIX) return a.acc_in[(size_t)m * D + n];
+    else return lx_fix(a.xin[(size_t)m * D + n]);
+  }
+  // by wave 0 before its first load (lanes past the share repeat its last
+  // store): its first wait, for its weights, comes long after the store is
+  // done.  (Issued by the stream waves after their input loads, the stores
+  // made the compiler spill the gain to scratch.)
+  __device__ __forceinline__ static void clear(const LxArgs& a, int wave, int lane) {
+    if (wave == 0)
+      reinterpret_cast<ulonglong2*>(a.acc_clear + (size_t)blockIdx.x * CPW)[min(lane, CPW / 2 - 1)] =
+          make_ulonglong2(0ull, 0ull);
+  }
+  __device__ __forceinline__ void finish(int st, int w4, float* xsh, float* gsh, float* ssq) {
 #pragma unroll
     for (int i = 0; i < GPT / 4; ++i) *reinterpret_cast<float4*>(gsh + st * GPT + 4 * i) = gv[i];
-    float s = sv[0];
+    float v[EPT];
 #pragma unroll
-    for (int h = 1; h < 9; ++h) s = __fadd_rn(s, sv[h]);
-    // every thread stores (threads past the slice repeat its last element)
-    a.xout[(size_t)g * LX_M * D + (size_t)j * SL + min(st, SL - 1)] = s;
-  }
-  __device__ __forceinline__ void gather(const LxArgs& a, int g, int st, int w4, float* xsh, float* ssq) {
-    const float* src = a.xout + (size_t)g * LX_M * D + (size_t)st * EPT;
-    float4 v[EPT / 4];
-#pragma unroll
-    for (int i = 0; i < EPT / 4; ++i) v[i] = *reinterpret_cast<const float4*>(src + 4 * i);
+    for (int i = 0; i < EPT / 4; ++i) {
+      if constexpr (FIX) {
+        v[4 * i] = lx_unfix((long long)xq[2 * i].x); v[4 * i + 1] = lx_unfix((long long)xq[2 * i].y);
+        v[4 * i + 2] = lx_unfix((long long)xq[2 * i + 1].x); v[4 * i + 3] = lx_unfix((long long)xq[2 * i + 1].y);
+      } else {
+        v[4 * i] = xf[i].x; v[4 * i + 1] = xf[i].y; v[4 * i + 2] = xf[i].z; v[4 * i + 3] = xf[i].w;
+      }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < EPT / 4; ++i) {
-      *reinterpret_cast<float4*>(xsh + st * EPT + 4 * i) = v[i];
-      ss = fmaf(v[i].x, v[i].x, ss); ss = fmaf(v[i].y, v[i].y, ss);
-      ss = fmaf(v[i].z, v[i].z, ss); ss = fmaf(v[i].w, v[i].w, ss);
+      *reinterpret_cast<float4*>(xsh + st * EPT + 4 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ss = fmaf(v[4 * i + k], v[4 * i + k], ss);
     }
     ss = wave_sum_dpp(ss);
     if ((st & 63) == 0) ssq[w4] = ss;
@@ -351,7 +383,7 @@ __host__ __device__ constexpr int lx_col_elems(int ncols) {
 // ---------------------------------------------------------------------------
 // Attention half of a layer.  Grid LX_WGS, block LX_NT.
 // KT: KV cache element (float or uint16_t BF16 bits).
-template <typename WL, typename KT, int D>
+template <typename WL, typename KT, int D, bool FIX>
 __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
   constexpr int M = LX_M, HD = LX_HD, G = LX_G, HQ = LX_HQ, HKV = LX_HKV;
   constexpr int VEC = WL::VEC, NVQ = D / (64 * VEC);
@@ -457,21 +489,25 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     __builtin_amdgcn_sched_barrier(1);
     const int w4 = wave - 4, st = tid - 256;
     const int tok = st / LPT, sub = st % LPT;
-    LxInput<D> in;
+    // this wave's W_o rows; lanes with (lane & 3) == 0 own outputs
+    // (m, n) = (wd & 1, n0 + 8 h + (wd >> 1)), wd = lane >> 2, h < OH
+    const int n0 = j * OROWS + w4 * ORW, wd = lane >> 2;
+    constexpr int OH = ORW * M / 16;
+    LxIn<D, FIX> in;
     unsigned ep, er;
+    long long xo[OH];
     {
       const int t0 = a.kv_len[0], t1 = a.kv_len[1], a0 = a.active[0], a1 = a.active[1];
       ep = fl[j]; er = *a.err;
-      in.issue(a, st, j);
+      in.issue(a, st);
+#pragma unroll
+      for (int h = 0; h < OH; ++h) xo[h] = LxIn<D, FIX>::xo(a, wd & 1, n0 + 8 * h + (wd >> 1));
       rows_state(t0, t1, a0, a1);
       // every stream thread writes (thread 0 to row 0, the rest to row 1):
       // no branch for the compiler to sink these loads into
       int* sd = stsh[st == 0 ? 0 : 1];
       sd[0] = t0; sd[1] = t1; sd[2] = a0; sd[3] = a1; sd[4] = (int)ep; sd[5] = (int)er;
     }
-    in.slice(a, g, st, j, gsh);
-    lx_wait_stores();
-    if (!lx_xcd_barrier(fl, j, ep + 1, deadline, er, a.err, &okf, 4)) return;   // input barrier
     // K/V of this workgroup's first slot (clamped into the cache when the
     // slot does not exist; then unused)
     const int s0 = j < nsl ? j : 0;
@@ -485,7 +521,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
 #pragma unroll
       for (int i = 0; i < NLD; ++i) { kraw[i] = kp[i]; vraw[i] = vp[i]; }
     };
-    in.gather(a, g, st, w4, xsh, ssq);
+    in.finish(st, w4, xsh, gsh, ssq);
     lx_sync();                                                   // 1
     // The first slot's K/V, issued once the exchange waves' q/k/v weights
     // are in flight (the projections are on the critical path; the cache rows
@@ -495,7 +531,6 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     if (!lx_all_ok(okq)) return;
     // this wave's W_o rows, head g's columns: needed only after the merge
     // (issued before, they slow the q/k/v weight stream)
-    const int n0 = j * OROWS + w4 * ORW;
     typename NL::raw_t wo[ORW][OU];
 #pragma unroll
     for (int r = 0; r < ORW; ++r)
@@ -593,7 +628,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     // the partials are out once this wave's stores are (its K/V and W_o
     // loads, issued before them, are in by now); stream wave 4 polls
     lx_wait_stores();
-    if (!lx_xcd_barrier(fl, j, ep + 2, deadline, er, a.err, &okf, 4)) return;   // 7, 8
+    if (!lx_xcd_barrier(fl, j, ep + 1, deadline, er, a.err, &okf, 4)) return;   // 7, 8
     merge();
     lx_sync();                                                   // 9
     float acc[ORW][M];
@@ -620,22 +655,15 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       }
     }
     static_assert(ORW * M == 16 || ORW * M == 32, "O rows per stream wave");
-    if constexpr (ORW * M == 16) {
-      const float v = lx_reduce<16, ORW>(acc, lane);   // word r * M + m in lanes [4 w, 4 w + 4)
-      const int wd = lane >> 2;
-      if ((lane & 3) == 0) a.pout[((size_t)g * M + (wd & 1)) * D + n0 + (wd >> 1)] = v;
-    } else {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        float part[ORW / 2][M];
+    for (int h = 0; h < OH; ++h) {
+      float part[8][M];
 #pragma unroll
-        for (int r = 0; r < ORW / 2; ++r)
+      for (int r = 0; r < 8; ++r)
 #pragma unroll
-          for (int m = 0; m < M; ++m) part[r][m] = acc[h * (ORW / 2) + r][m];
-        const float v = lx_reduce<16, ORW / 2>(part, lane);
-        const int wd = lane >> 2;
-        if ((lane & 3) == 0) a.pout[((size_t)g * M + (wd & 1)) * D + n0 + h * (ORW / 2) + (wd >> 1)] = v;
-      }
+        for (int m = 0; m < M; ++m) part[r][m] = acc[h * 8 + r][m];
+      const float v = lx_reduce<16, 8>(part, lane);   // word r * M + m in lanes [4 w, 4 w + 4)
+      if ((lane & 3) == 0) lx_accum(a.acc_out, (size_t)(wd & 1) * D + n0 + 8 * h + (wd >> 1), v, g == 0 ? xo[h] : 0ll);
     }
   } else {
     // ===================== exchange waves =====================
@@ -643,6 +671,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     // either is hoisted above the branch and made to wait for the other's loads)
     __builtin_amdgcn_sched_barrier(0);
     const int w4 = wave;
+    LxIn<D, FIX>::clear(a, wave, lane);
     // norm gains and RoPE entries (needed after the q/k/v exchange)
     const int t = tid, tr = t & 127, trow = t >> 7;
     const float qw_r = a.q_norm[tr], kw_r = a.k_norm[tr];
@@ -659,7 +688,6 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     for (int r = 0; r < QRW; ++r)
 #pragma unroll
       for (int jj = 0; jj < NVQ; ++jj) w[r][jj] = WL::raw(wb, (size_t)(wrow + r) * D + (size_t)(jj * 64 + lane) * VEC);
-    if (!lx_xcd_barrier(fl, j, 0u, deadline, 0u, a.err, &okf, 4)) return;   // input barrier (stream wave 4 polls)
     if (trow == 0) { qwn[tr] = qw_r; kwn[tr] = kw_r; }
     if (tr < HD / 2) csh[trow][tr] = cs_r;
     lx_sync();                                                   // 1 (input in LDS)
@@ -738,7 +766,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       lx_sync();                                                 // B: softmax
       lx_sync();                                                 // C: partials stored
     }
-    if (!lx_xcd_barrier(fl, j, tag + 1, deadline, err0, a.err, &okf, 4)) return;   // 7, 8 (stream wave 4 polls)
+    if (!lx_xcd_barrier(fl, j, tag, deadline, err0, a.err, &okf, 4)) return;   // 7, 8 (stream wave 4 polls)
     merge();
     lx_sync();                                                   // 9
   }
@@ -750,6 +778,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
 // exchange wave; the stream waves hold the down projection's rows.
 template <typename WL, int D, int I>
 __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
+  constexpr bool FIX = true;
   constexpr int M = LX_M, VEC = WL::VEC, NV = D / (64 * VEC);
   constexpr int IX = I / LX_XCDS, IW = IX / LX_PER;
   constexpr int GUW = 4;
@@ -764,8 +793,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
   __shared__ __attribute__((aligned(16))) float gsh[D];
   __shared__ float ssq[8];
   __shared__ __attribute__((aligned(16))) float ash[M][IX];   // the XCD's slice
-  __shared__ int stsh[2][2];   // row 0: epoch, error word (loaded by the stream waves)
-  __shared__ int okf;
+  __shared__ int stsh[2];   // [0]: the epoch (loaded by the stream waves)
   __shared__ int oka[4];   // per-wave verdicts on the SwiGLU exchange
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -774,9 +802,8 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
   const unsigned long long deadline = __builtin_amdgcn_s_memrealtime() + a.spin_ticks;
   unsigned* fl = a.flags + g * LX_FLAGS;
   const int i0 = g * IX + j * IW;                     // first inner index of this workgroup
-  // gate/up wave gw (0..GUW-1): its weight rows are issued, then it joins
-  // the input barrier (stream wave 4 polls) and the LDS barrier after which
-  // the input is in LDS
+  // gate/up wave gw (0..GUW-1): its weight rows are issued, then it waits
+  // at the LDS barrier after which the input is in LDS
   auto gate_up = [&](int gw, float& act) {
     uint4 w[2 * IPW][NV];
     const int ib = i0 + gw * IPW;
@@ -787,7 +814,6 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
         w[2 * r][jj] = WL::raw(a.wg, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
         w[2 * r + 1][jj] = WL::raw(a.wu, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
       }
-    if (!lx_xcd_barrier(fl, j, 0u, deadline, 0u, a.err, &okf, 4)) return false;   // input barrier
     lx_sync();                                                   // 1 (input in LDS)
     const float inv[M] = {lx_inv_rms<D>(ssq, 0, a.eps), lx_inv_rms<D>(ssq, 1, a.eps)};
     float acc[2 * IPW][M];
@@ -807,9 +833,13 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
     // (the two roles start with different scheduling barriers, so no code of
     // either is hoisted above the branch and made to wait for the other's loads)
     __builtin_amdgcn_sched_barrier(0);
+    LxIn<D, FIX>::clear(a, wave, lane);
     float act;
     if (!gate_up(wave, act)) return;
-    const unsigned tag = (unsigned)stsh[0][0] + 1;   // the input barrier's epoch
+    const unsigned tag = (unsigned)stsh[0] + 1;   // this launch's epoch
+    // stored for the next launch (no barrier here); every lane of wave 0
+    // stores the same word, so the store needs no per-lane branch
+    if (wave == 0) __hip_atomic_store(fl + j, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     {
       const int wd = lane >> 2, i = wd >> 2, m = wd & 1;
       if ((lane & 3) == 0 && (wd & 2) == 0 && i < IPW) lx_put(a.act + (size_t)m * a.ld_act + i0 + wave * IPW + i, act, tag);
@@ -837,28 +867,33 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
     // ===================== stream waves =====================
     __builtin_amdgcn_sched_barrier(1);
     const int w4 = wave - 4;
-    // down rows of this wave, slice g's columns: issued after the gate/up
-    // stream so that it reaches HBM first
-    const int n0 = j * DROWS + w4 * DRW;
+    // down rows of this wave, slice g's columns; lanes with (lane & 3) == 0
+    // own outputs (m, n) = (wo & 1, n0 + 8 h + (wo >> 1)), wo = lane >> 2
+    const int n0 = j * DROWS + w4 * DRW, wo = lane >> 2;
+    constexpr int OH = DRW * M / 16;
     typename NL::raw_t wd[DRW][DU];
+    auto load_down = [&]() {
+#pragma unroll
+      for (int r = 0; r < DRW; ++r)
+#pragma unroll
+        for (int u = 0; u < DU; ++u)
+          wd[r][u] = NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE);
+    };
+    long long xo[OH];
     {
       const int st = tid - 256;
-      LxInput<D> in;
-      const unsigned ep = fl[j], er = *a.err;
-      in.issue(a, st, j);
-      int* sd = stsh[st == 0 ? 0 : 1];   // no branch to sink the loads into
-      sd[0] = (int)ep; sd[1] = (int)er;
-      in.slice(a, g, st, j, gsh);
-      lx_wait_stores();
-      if (!lx_xcd_barrier(fl, j, ep + 1, deadline, er, a.err, &okf, 4)) return;   // input barrier
-      in.gather(a, g, st, w4, xsh, ssq);
+      LxIn<D, FIX> in;
+      const unsigned ep = fl[j];
+      in.issue(a, st);
+#pragma unroll
+      for (int h = 0; h < OH; ++h) xo[h] = LxIn<D, FIX>::xo(a, wo & 1, n0 + 8 * h + (wo >> 1));
+      stsh[st == 0 ? 0 : 1] = (int)ep;   // no branch to sink the loads into
+      in.finish(st, w4, xsh, gsh, ssq);
       lx_sync();                                                 // 1
     }
-#pragma unroll
-    for (int r = 0; r < DRW; ++r)
-#pragma unroll
-      for (int u = 0; u < DU; ++u)
-        wd[r][u] = NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE);
+    // issued at entry, beside the gate/up rows, they slowed the 0.6B frame
+    // by 22 us (they share the HBM queues with the rows the dots wait for)
+    load_down();
     lx_sync();                                                   // 4
     if (!lx_all_ok(oka)) return;
     float acc[DRW][M];
@@ -893,8 +928,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
 #pragma unroll
         for (int m = 0; m < M; ++m) part[r][m] = acc[h * 8 + r][m];
       const float v = lx_reduce<16, 8>(part, lane);   // word r * M + m in lanes [4 w, 4 w + 4)
-      const int wd = lane >> 2;
-      if ((lane & 3) == 0) a.pout[((size_t)g * M + (wd & 1)) * D + n0 + h * 8 + (wd >> 1)] = v;
+      if ((lane & 3) == 0) lx_accum(a.acc_out, (size_t)(wo & 1) * D + n0 + 8 * h + (wo >> 1), v, g == 0 ? xo[h] : 0ll);
     }
   }
 }
@@ -909,6 +943,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
 // down rows.
 template <typename WL, int D, int I>
 __global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
+  constexpr bool FIX = true;
   constexpr int M = LX_M, VEC = WL::VEC, NV = D / (64 * VEC);
   constexpr int IX = I / LX_XCDS, IW = IX / LX_PER;
   constexpr int IPW = IW / 8;                         // inner indices per wave
@@ -924,8 +959,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
   __shared__ __attribute__((aligned(16))) float gsh[D];
   __shared__ float ssq[8];
   __shared__ __attribute__((aligned(16))) float ash[M][IX];   // the XCD's slice
-  __shared__ int stsh[2][2];   // row 0: barrier epoch, error word (loaded by the stream waves)
-  __shared__ int okf;
+  __shared__ int stsh[2];      // [0]: the epoch (loaded by the stream waves)
   __shared__ int oka[8];       // per-wave verdicts on the SwiGLU exchange
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -936,17 +970,18 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
   const int i0 = g * IX + j * IW;                     // first inner index of this workgroup
   const int ib = i0 + wave * IPW;
   uint4 w[2 * IPW][NV];
+  auto load_gate_up = [&]() {
 #pragma unroll
-  for (int r = 0; r < IPW; ++r)
+    for (int r = 0; r < IPW; ++r)
 #pragma unroll
-    for (int jj = 0; jj < NV; ++jj) {
-      w[2 * r][jj] = WL::raw(a.wg, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
-      w[2 * r + 1][jj] = WL::raw(a.wu, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
-    }
-  // this wave's down rows, slice g's columns: the exchange waves issue them
-  // behind their gate/up rows, the stream waves once the input is in LDS
-  // (ahead of it they would hold back the input barrier)
-  const int n0 = j * DROWS + wave * DRW;
+      for (int jj = 0; jj < NV; ++jj) {
+        w[2 * r][jj] = WL::raw(a.wg, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
+        w[2 * r + 1][jj] = WL::raw(a.wu, (size_t)(ib + r) * D + (size_t)(jj * 64 + lane) * VEC);
+      }
+  };
+  // this wave's down rows, slice g's columns; lanes with (lane & 3) == 0
+  // own outputs (m, n) = (wo & 1, n0 + (wo >> 1)), wo = lane >> 2
+  const int n0 = j * DROWS + wave * DRW, wo = lane >> 2;
   typename NL::raw_t wdn[DRW][DU];
   auto load_down = [&]() {
 #pragma unroll
@@ -955,27 +990,34 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
       for (int u = 0; u < DU; ++u)
         wdn[r][u] = NL::load(a.wd, (size_t)(n0 + r) * I + g * IX + (size_t)(u * 64 + lane) * DE);
   };
+  long long xo;
   if (wave < 4) {
+    // gate/up rows, then the down rows behind them
     __builtin_amdgcn_sched_barrier(0);
+    LxIn<D, FIX>::clear(a, wave, lane);
+    xo = LxIn<D, FIX>::xo(a, wo & 1, n0 + (wo >> 1));
+    load_gate_up();
     load_down();
-    if (!lx_xcd_barrier(fl, j, 0u, deadline, 0u, a.err, &okf, 4)) return;   // input barrier (stream wave 4 polls)
     lx_sync();                                                   // 1
   } else {
+    // the input first (so waiting for it waits for nothing else), then the
+    // gate/up rows, then the down rows
     __builtin_amdgcn_sched_barrier(1);
     const int st = tid - 256, w4 = wave - 4;
-    LxInput<D> in;
-    const unsigned ep = fl[j], er = *a.err;
-    in.issue(a, st, j);
-    int* sd = stsh[st == 0 ? 0 : 1];   // no branch to sink the loads into
-    sd[0] = (int)ep; sd[1] = (int)er;
-    in.slice(a, g, st, j, gsh);
-    lx_wait_stores();
-    if (!lx_xcd_barrier(fl, j, ep + 1, deadline, er, a.err, &okf, 4)) return;   // input barrier
-    in.gather(a, g, st, w4, xsh, ssq);
+    LxIn<D, FIX> in;
+    const unsigned ep = fl[j];
+    in.issue(a, st);
+    xo = LxIn<D, FIX>::xo(a, wo & 1, n0 + (wo >> 1));
+    load_gate_up();
+    stsh[st == 0 ? 0 : 1] = (int)ep;   // no branch to sink the loads into
+    in.finish(st, w4, xsh, gsh, ssq);
     lx_sync();                                                   // 1
     load_down();
   }
-  const unsigned tag = (unsigned)stsh[0][0] + 1;                 // the input barrier's epoch
+  const unsigned tag = (unsigned)stsh[0] + 1;                 // this launch's epoch
+  // stored for the next launch (no barrier here); every lane of wave 0 stores
+  // the same word, so the store needs no per-lane branch
+  if (wave == 0) __hip_atomic_store(fl + j, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   {
     const float inv[M] = {lx_inv_rms<D>(ssq, 0, a.eps), lx_inv_rms<D>(ssq, 1, a.eps)};
     float acc[2 * IPW][M];
@@ -1029,8 +1071,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp8_kernel(LxArgs a) {
     }
   }
   const float v = lx_reduce<16, DRW>(acc, lane);   // word r * M + m in lanes [4 w, 4 w + 4)
-  const int wd = lane >> 2;
-  if ((lane & 3) == 0) a.pout[((size_t)g * M + (wd & 1)) * D + n0 + (wd >> 1)] = v;
+  if ((lane & 3) == 0) lx_accum(a.acc_out, (size_t)(wo & 1) * D + n0 + (wo >> 1), v, g == 0 ? xo : 0ll);
 }
 
 }  // namespace

@@ -538,7 +538,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       for (int u = 0; u < OU; ++u)
         wo[r][u] = NL::load(a.wo, (size_t)(n0 + r) * (HQ * HD) + g * OCOL + (size_t)(u * 64 + lane) * OE);
     lx_sync();                                                   // 5
-    lx_sync();                                                   // 6
+    if constexpr (KBF) lx_sync();                                // 6 (the rounded new token)
     // One slot: scores, chunk softmax, partial (o, max, sum) into pb.
     auto attend = [&](int it) {
       const int s = j + it * LX_PER;
@@ -760,7 +760,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
         vn[m][d] = bf16_round(vn[m][d]);
       }
     }
-    lx_sync();                                                   // 6
+    if constexpr (KBF) lx_sync();                                // 6 (the rounded new token)
     for (int it = 0; it < nit; ++it) {
       lx_sync();                                                 // A: scores, V in LDS
       lx_sync();                                                 // B: softmax

@@ -2375,23 +2375,26 @@ __device__ __forceinline__ float wave_reduce_words(float (&w)[N], int lane) {
 //   W_gu a_q = r_q * (G_q + scale * P_{q-1}[c]),   G_q = W_gu (w_in * x_{q-1}),
 //                                                  P_j[c] = W_gu (w_in * table[j][c]),
 //
-// where G_q is computed by the previous step (it does not depend on c) and
-// P_j is a weight-only table of every code's contribution, built when the
-// frame is captured.  Once c is known every workgroup forms the whole SwiGLU
-// output elementwise, so codebook q-1's sampler, the prefix advance, the
-// SwiGLU, the down projection with its residual (y_q = a_q + W_d act_q,
-// model.py:163-170) and the next step's G_{q+1} fit one launch, and the
-// classifier follows.  Launches per codebook: two instead of three.
+// where P_j is a weight-only table of every code's contribution, built when
+// the frame is captured, and G_q, by the same linearity, is G_1 plus the table
+// entries of the codes drawn so far: G_{q+1} = G_q + scale * P_{q-1}[c], the
+// very sum the SwiGLU input scales.  Only G_1 = W_gu (w_in * hidden) is a
+// GEMV.  Once c is known every workgroup forms the whole SwiGLU output
+// elementwise, so codebook q-1's sampler, the prefix advance, the SwiGLU, the
+// down projection with its residual (y_q = a_q + W_d act_q, model.py:163-170)
+// and G_{q+1} fit one launch, and the classifier follows.  Launches per
+// codebook: two instead of three.
 //
-// Work of one launch (256 workgroups of SNT threads): each wave owns RWG gate
-// rows and the same RWG up rows of W_gu (whole rows, K = KD) for G_{q+1}, and
-// for the down projection the workgroup owns RD = KD / 256 output rows while
-// its 8 waves split the inner dimension KI into 8 chunks of 64 * VEC (one
-// 16-byte weight load per lane and row).  Every weight load is issued before
-// the sampler runs.
+// Work of one launch (256 workgroups of SNT threads): for G_1 each wave owns
+// RWG gate rows and the same RWG up rows of W_gu (whole rows, K = KD); for the
+// down projection the workgroup owns RD = KD / 256 output rows while its 8
+// waves split the inner dimension KI into 8 chunks of 64 * VEC (one 16-byte
+// weight load per lane and row).  Every weight load is issued before the
+// sampler runs.
 //   MODE 0: G_1 = W_gu (w_in * hidden) only (x_0 = hidden; no sampler).
 //   MODE 1: codebook 0's SwiGLU + down: act_0 = SwiGLU(r_0 G_1), y_0.
-//   MODE 2: codebooks 1 .. Q-2: sampler of q-1, prefix, act_q, y_q, G_{q+1}.
+//   MODE 2: codebooks 1 .. Q-2: sampler of q-1, prefix, act_q, y_q, and
+//           G_{q+1} = G_q + scale P_{q-1}[c] (workgroup 0 stores it).
 //   MODE 3: codebook Q-1: as MODE 2 without G_{q+1}.
 struct DepthArgs {
   const void* w_gate; const void* w_up;    // [KI][KD]
@@ -2400,7 +2403,7 @@ struct DepthArgs {
   const float* prefix_in; float* prefix_out;   // [M][KD] before / after code q-1 (MODE 2, 3)
   const float* norm_w; float eps;          // norm_in gain [KD], FLT_EPSILON
   const float* g_in;                       // [M][2 KI] G_q (gate | up), MODE 1-3
-  float* g_out;                            // [M][2 KI] G_{q+1}, MODE 0 and 2
+  float* g_out;                            // [M][2 KI] G_1 (MODE 0) or G_{q+1} (MODE 2)
   const float* ptab;                       // [Q-1][V][2 KI] code tables, MODE 2 and 3
   float* y;                                // [M][KD] depth MLP output, MODE 1-3
   float scale;                             // frame scale 1/sqrt(Q)
@@ -2413,7 +2416,7 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
   double* W = reinterpret_cast<double*>(raw);
   unsigned long long* ck = reinterpret_cast<unsigned long long*>(W + a.V);
   unsigned long long* sk = ck + pow2_ceil(a.V);
-  constexpr bool SAMPLE = MODE >= 2, GPART = MODE == 0 || MODE == 2, DPART = MODE >= 1;
+  constexpr bool SAMPLE = MODE >= 2, GPART = MODE == 0, DPART = MODE >= 1;
   constexpr int VEC = TL::VEC;
   constexpr int NV = KD / (64 * VEC);           // 16-byte loads per lane of one W_gu row
   constexpr int DPT = KD / SNT;                 // elements of x per thread
@@ -2498,10 +2501,10 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
       }
   }
   // The down rows go ahead of the sampler too when few loads are in flight
-  // per lane; with more (the 1.7B shape: 16 gate/up + 8 down per lane) the
-  // sampler itself ran slower behind them (code drawn after 10.7 us instead of
-  // 8.6), so there they follow the code with its table entries.
-  constexpr bool WD_EARLY = 2 * RWG * NV + RD <= 16;
+  // per lane (at most 16: with 16 gate/up + 8 down per lane the sampler itself
+  // ran slower behind them, code drawn after 10.7 us instead of 8.6), else
+  // they follow the code with its table entries.
+  constexpr bool WD_EARLY = (GPART ? 2 * RWG * NV : 0) + RD <= 16;
   const int row0 = blockIdx.x * RD;
   uint4 wd[DPART ? RD : 1];
   if constexpr (DPART && (!SAMPLE || WD_EARLY)) {
@@ -2648,6 +2651,7 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
   // act = SwiGLU(r (G_q + scale P[c])) at this lane's chunk; y = a + W_d act
   if constexpr (DPART) {
     float act[M][VEC];
+    float gnext[MODE == 2 ? M : 1][2][VEC];
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -2657,6 +2661,10 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
           gt = fmaf(g.scale, pr[0][i], gt);
           up = fmaf(g.scale, pr[1][i], up);
         }
+        if constexpr (MODE == 2) {   // G_{q+1} = G_q + scale P_{q-1}[c]
+          gnext[m][0][i] = gt;
+          gnext[m][1][i] = up;
+        }
         gt *= inv[m];
         up *= inv[m];
         // SwiGLU with the hardware exp2 and reciprocal (~1 ulp each): every
@@ -2664,6 +2672,18 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
         // is paid 256 times over.
         act[m][i] = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
       }
+    if constexpr (MODE == 2) {
+      if (lead) {   // every workgroup holds the same G_{q+1}; workgroup 0 stores it
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < VEC; i += 4)
+              *reinterpret_cast<float4*>(g.g_out + (size_t)m * 2 * KI + h * KI + kc + i) =
+                  make_float4(gnext[m][h][i], gnext[m][h][i + 1], gnext[m][h][i + 2], gnext[m][h][i + 3]);
+      }
+    }
     constexpr int ND = RD * M;                  // word i * M + m
     float dw[ND];
 #pragma unroll

@@ -174,6 +174,7 @@ struct sk_engine {
   // tables P_j[c] = W_gu (norm_in gain * table[j][c]) for j < Q-1, built when
   // the frame is captured, and the ping-pong G buffers [rows][2 * depth_inner].
   bool code_tables = false;
+  bool wide_tables = false;          // many rows: the samplers form the next depth step's SwiGLU output
   float* ptab = nullptr;
   float* gbuf[2] = {nullptr, nullptr};
 
@@ -647,10 +648,17 @@ hipError_t enqueue_depth_wide(sk_engine* e, int q) {
   const size_t tsz = (wt == SK_BF16) ? 2 : 4;
   hipError_t err;
   const bool xs = e->xs_abuf != nullptr;
-  SkinnyArgs k = skinny_args(e->d_gate, c.depth_inner, d, e->abuf, d, e->act, e->inner_max, M);
-  k.w2 = e->d_up;
-  if (xs) { k.xs = e->xs_abuf; k.xs_out = e->xs_act; }
-  if ((err = launch_skinny<EPI_SWIGLU>(e, k)) != hipSuccess) return err;
+  SkinnyArgs k;
+  // With code tables only codebook 0 runs the gate/up GEMM (its gate and up
+  // before the activation, r_0 G_0, kept for the samplers); codebook q's
+  // SwiGLU output comes from the sampler of q - 1.
+  if (!e->wide_tables || q == 0) {
+    k = skinny_args(e->d_gate, c.depth_inner, d, e->abuf, d, e->act, e->inner_max, M);
+    k.w2 = e->d_up;
+    if (xs) { k.xs = e->xs_abuf; k.xs_out = e->xs_act; }
+    if (e->wide_tables) { k.pre_out = e->gbuf[0]; k.ld_pre = 2 * c.depth_inner; }
+    if ((err = launch_skinny<EPI_SWIGLU>(e, k)) != hipSuccess) return err;
+  }
   k = skinny_args(e->d_down, d, c.depth_inner, e->act, e->inner_max, e->ybuf, d, M);
   k.res = e->abuf; k.ldr = d;
   if (xs) { k.xs = e->xs_act; k.xs_out = e->xs_y; k.xs_gain = e->d_norm_out; k.ss_out = e->ss_y; }
@@ -727,6 +735,13 @@ hipError_t enqueue_frame(sk_engine* e) {
   for (int q = 0; q < c.n_codebooks; ++q) {
     if (e->wide) {
       if ((err = enqueue_depth_wide(e, q)) != hipSuccess) return err;
+      if (e->wide_tables) {   // G_q in gbuf[q % 2] (after codebook 0: r_0 G_0), G_{q+1} into the other
+        s.ptab = e->ptab; s.ki = c.depth_inner;
+        s.g_in = e->gbuf[q % 2];
+        s.g_out = q + 2 < c.n_codebooks ? e->gbuf[(q + 1) % 2] : nullptr;
+        s.g_in_normed = q == 0;
+        s.act = e->act; s.ld_act = e->inner_max; s.xs_act = e->xs_act;
+      }
       err = (wt == SK_BF16) ? launch_sample_step<WBF16>(s, q, c.n_utts, e->stream)
                             : launch_sample_step<WF32>(s, q, c.n_utts, e->stream);
       if (err != hipSuccess) return err;
@@ -1457,7 +1472,8 @@ int sk_capture(sk_engine* e) {
   SK_HIP(hipStreamSynchronize(e->stream));
   e->code_tables = !e->wide && e->c.n_utts == 1 &&
                    code_tables_fit(e->c.d_model, e->rows, e->c.depth_inner, e->c.audio_vocab, e->c.weight_dtype);
-  if (e->code_tables && (rc = build_code_tables(e)) != SK_OK) return rc;
+  e->wide_tables = e->wide && e->c.depth_inner <= SNT * DEPTH_API && e->c.d_model <= SNT * DEPTH_DPT;
+  if ((e->code_tables || e->wide_tables) && (rc = build_code_tables(e)) != SK_OK) return rc;
   rc = capture(e, enqueue_frame, &e->graph, &e->exec);
   if (rc != SK_OK) return rc;
   const hipError_t fe = find_attn_nodes(e);

@@ -1959,19 +1959,29 @@ struct SampleArgs {
   // row, and its split form for the many-row GEMMs (xs_abuf, may be null).
   const float* hidden; const float* w_in; float eps_in;
   float* abuf; uint16_t* xs_abuf;
+  // Many rows with code tables (ptab set): the next depth step's SwiGLU
+  // output as well, act = SwiGLU(r G_{q+1}) with G_{q+1} = G_q + scale
+  // P_q[code] (G_q = W_gu (w_in * x_q)), so that step needs no gate/up GEMM.
+  const float* ptab; int ki;           // [Q-1][V][2 ki] code tables; depth inner size (<= 4 SNT)
+  const float* g_in; float* g_out;     // [rows][2 ki] G_q, G_{q+1} (gate | up); g_out null: not needed
+  int g_in_normed;                     // g_in holds r_0 G_0 (codebook 0's GEMM): scaled by rms(hidden)
+  float* act; int ld_act; uint16_t* xs_act;   // SwiGLU output [rows][ld_act] and its split form
 };
 
 // The depth input rows of one utterance after its code q (sample_step_kernel,
 // SNT threads): prefix += table[q][code] * scale, x = hidden + prefix,
-// abuf = w_in * (x * inv_rms(x)); the loads are issued together once the code
-// is known (all threads hold it).
+// abuf = w_in * (x * inv_rms(x)); with code tables also the next step's
+// SwiGLU output (SampleArgs.ptab).  The loads are issued together once the
+// code is known (all threads hold it).
 constexpr int DEPTH_DPT = 8;             // d <= SNT * DEPTH_DPT
+constexpr int DEPTH_API = 4;             // code-table inner indices per thread: ki <= SNT * DEPTH_API
 template <typename TL>
 __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, int q, int code) {
-  __shared__ float red[2][SWAVES];
+  __shared__ float red[2][2][SWAVES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nr = a.rows_per_utt;         // 1 or 2
   const size_t trow = ((size_t)q * a.V + code) * a.d;
+  const bool tables = a.ptab != nullptr;   // uniform
   // Every operand first, indices clamped in bounds (rows past nr re-read row
   // 0, dims past d re-read d-1): one round trip, no branch between the
   // loads, and no load behind the prefix stores that might alias it.
@@ -1988,11 +1998,27 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
       hv[rr][i] = a.hidden[ro + k];
     }
   }
+  // G_q of the rows and P_q[code] at this thread's inner indices (gate, up)
+  float gq[2][2][DEPTH_API], pq[2][DEPTH_API];
+  if (tables) {
+    const float* pr = a.ptab + ((size_t)q * a.V + code) * 2 * a.ki;
+#pragma unroll
+    for (int i = 0; i < DEPTH_API; ++i) {
+      const int k = min(tid + i * SNT, a.ki - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        pq[h][i] = pr[h * a.ki + k];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+          gq[rr][h][i] = a.g_in[(size_t)(r0 + (rr < nr ? rr : 0)) * 2 * a.ki + h * a.ki + k];
+      }
+    }
+  }
   float xv[2][DEPTH_DPT];
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
     const size_t ro = (size_t)(r0 + rr) * a.d;
-    float ss = 0.f;
+    float ss = 0.f, sh = 0.f;
 #pragma unroll
     for (int i = 0; i < DEPTH_DPT; ++i) {
       const int k = tid + i * SNT;
@@ -2002,16 +2028,21 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
       if (k < a.d) {
         if (rr < nr) a.prefix[ro + k] = p;
         ss = fmaf(x, x, ss);
+        sh = fmaf(hv[rr][i], hv[rr][i], sh);
       }
     }
     ss = wave_sum_dpp(ss);
-    if (lane == 0) red[rr][wave] = ss;
+    if (lane == 0) red[0][rr][wave] = ss;
+    if (tables) {
+      sh = wave_sum_dpp(sh);
+      if (lane == 0) red[1][rr][wave] = sh;
+    }
   }
   __syncthreads();
   for (int rr = 0; rr < nr; ++rr) {
     float t = 0.f;
 #pragma unroll
-    for (int w = 0; w < SWAVES; ++w) t += red[rr][w];
+    for (int w = 0; w < SWAVES; ++w) t += red[0][rr][w];
     const float inv = 1.0f / sqrtf(t / (float)a.d + a.eps_in);
     const size_t ro = (size_t)(r0 + rr) * a.d;
 #pragma unroll
@@ -2021,6 +2052,35 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
         const float y = gv[i] * (xv[rr][i] * inv);
         a.abuf[ro + k] = y;
         if (a.xs_abuf) xsplit_store(a.xs_abuf, r0 + rr, k, y);
+      }
+    }
+    if (tables) {
+      // G_{q+1} = G_q + scale P_q[code] (after codebook 0's GEMM, G_0 = its
+      // r_0 G_0 times rms(hidden)); act = SwiGLU(r_{q+1} G_{q+1}) as the GEMM
+      // epilogue forms it
+      float rms0 = 1.f;
+      if (a.g_in_normed) {
+        float th = 0.f;
+#pragma unroll
+        for (int w = 0; w < SWAVES; ++w) th += red[1][rr][w];
+        rms0 = sqrtf(th / (float)a.d + a.eps_in);
+      }
+      const size_t go = (size_t)(r0 + rr) * 2 * a.ki;
+#pragma unroll
+      for (int i = 0; i < DEPTH_API; ++i) {
+        const int k = tid + i * SNT;
+        if (k < a.ki) {
+          const float gt = fmaf(a.scale, pq[0][i], gq[rr][0][i] * rms0);
+          const float up = fmaf(a.scale, pq[1][i], gq[rr][1][i] * rms0);
+          if (a.g_out) {
+            a.g_out[go + k] = gt;
+            a.g_out[go + a.ki + k] = up;
+          }
+          const float xg = gt * inv, xu = up * inv;
+          const float y = xg / (1.0f + expf(-xg)) * xu;
+          a.act[(size_t)(r0 + rr) * a.ld_act + k] = y;
+          if (a.xs_act) xsplit_store(a.xs_act, r0 + rr, k, y);
+        }
       }
     }
   }

@@ -34,6 +34,8 @@ struct SkinnyArgs {
   uint16_t* xs_out;                    // out again in split form for the next GEMM; null: none
   const float* xs_gain;                // gain applied before that split (the next RMSNorm); null: 1
   float* ss_out;                       // [32][N/16] sums of out^2 per row and output tile; null: none
+  float* pre_out; int ld_pre;          // SwiGLU: gate and up before the activation, [R][ld_pre]
+                                       // (gate at o, up at N + o); null: none
 };
 
 // Floats per slice partial: two epilogue values per thread (SwiGLU) + 32 row
@@ -159,7 +161,13 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(SkinnyArgs a) {
     float y = c[0];
     if constexpr (EPI == EPI_BIAS) y = y + a.bias[oo];
     if constexpr (EPI == EPI_RESID) y = a.res[(size_t)r * a.ldr + oo] + y;
-    if constexpr (EPI == EPI_SWIGLU) y = y / (1.0f + expf(-y)) * c[NA - 1];
+    if constexpr (EPI == EPI_SWIGLU) {
+      if (a.pre_out) {
+        a.pre_out[(size_t)r * a.ld_pre + oo] = y;
+        a.pre_out[(size_t)r * a.ld_pre + a.N + oo] = c[NA - 1];
+      }
+      y = y / (1.0f + expf(-y)) * c[NA - 1];
+    }
     a.out[(size_t)r * a.ldo + oo] = y;
   }
 }
@@ -447,7 +455,13 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
     y = c[0];
     if constexpr (EPI == EPI_BIAS) y = y + epi_in;
     if constexpr (EPI == EPI_RESID) y = epi_in + y;
-    if constexpr (EPI == EPI_SWIGLU) y = y / (1.0f + expf(-y)) * c[NA - 1];
+    if constexpr (EPI == EPI_SWIGLU) {
+      if (a.pre_out) {
+        a.pre_out[(size_t)r * a.ld_pre + oo] = y;
+        a.pre_out[(size_t)r * a.ld_pre + a.N + oo] = c[NA - 1];
+      }
+      y = y / (1.0f + expf(-y)) * c[NA - 1];
+    }
     a.out[(size_t)r * a.ldo + oo] = y;
     if (a.xs_out) xsplit_store(a.xs_out, r, oo, a.xs_gain ? y * gain_in : y);
   }

@@ -724,6 +724,8 @@ hipError_t enqueue_frame(sk_engine* e) {
       a.norm_w = e->d_norm_out; a.eps = c.depth_eps; a.bias = e->d_bias + (size_t)q * V;
       if ((err = launch_gemv<PRO_NORM, EPI_BIAS>(wt, M, a, e->stream)) != hipSuccess) return err;
     }
+    // the prefix through codebook Q-2, written by the last depth step
+    s.prefix_last = (c.n_codebooks - 1) % 2 == 1 ? e->prefix2 : e->prefix;
     err = (wt == SK_BF16) ? launch_sample_step<WBF16>(s, c.n_codebooks - 1, 1, e->stream)
                           : launch_sample_step<WF32>(s, c.n_codebooks - 1, 1, e->stream);
     if (err != hipSuccess) return err;

@@ -1966,6 +1966,11 @@ struct SampleArgs {
   const float* g_in; float* g_out;     // [rows][2 ki] G_q, G_{q+1} (gate | up); g_out null: not needed
   int g_in_normed;                     // g_in holds r_0 G_0 (codebook 0's GEMM): scaled by rms(hidden)
   float* act; int ld_act; uint16_t* xs_act;   // SwiGLU output [rows][ld_act] and its split form
+  // The last codebook, one utterance with code tables: the prefix through
+  // codebook Q-2 as the depth steps left it (scale * table rows summed in
+  // codebook order), so the frame embedding is one more row (null: the rows
+  // are gathered and summed here).
+  const float* prefix_last;
 };
 
 // The depth input rows of one utterance after its code q (sample_step_kernel,
@@ -2127,8 +2132,15 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   // The last codebook's frame embedding: the table rows of codebooks
   // 0 .. Q-2 do not depend on the draw, so they are in flight during it
   // (issued once the logits are in, so the sampler does not wait for them).
+  // With prefix_last the depth steps have summed them already.
   constexpr int EI = 4, EQ = 16;        // d <= EI * SNT, 2 <= Q <= EQ
-  const bool early = last && a.d <= EI * SNT && a.Q >= 2 && a.Q <= EQ;
+  const bool from_prefix = last && a.prefix_last != nullptr && a.d <= EI * SNT;
+  const bool early = last && !from_prefix && a.d <= EI * SNT && a.Q >= 2 && a.Q <= EQ;
+  float pl[EI];
+  if (from_prefix) {
+#pragma unroll
+    for (int i = 0; i < EI; ++i) pl[i] = a.prefix_last[min((int)threadIdx.x + i * SNT, a.d - 1)];
+  }
   const size_t row_stride = (size_t)a.V * a.d;
   float te[EI][EQ - 1];
   if (early) {
@@ -2159,6 +2171,27 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   }
 
   __syncthreads();
+  if (from_prefix) {
+    // x = prefix_{Q-1} + scale * table[Q-1][code]: the prefix update's own
+    // order (model.py:600-605), the same sum as the frame embedding
+    // (model.py:105-114) up to FP32 rounding
+    const int cq = codes_l[q];
+    float tq[EI];
+#pragma unroll
+    for (int i = 0; i < EI; ++i)
+      tq[i] = TL::get(a.table, (size_t)q * row_stride + (size_t)cq * a.d + min((int)threadIdx.x + i * SNT, a.d - 1));
+#pragma unroll
+    for (int i = 0; i < EI; ++i) {
+      const int dd = threadIdx.x + i * SNT;
+      if (dd >= a.d) continue;
+      const float e = __fadd_rn(pl[i], __fmul_rn(tq[i], a.scale));
+      for (int rr = 0; rr < a.rows_per_utt; ++rr) {
+        a.xnext[(size_t)(r0 + rr) * a.d + dd] = e;
+        a.prefix[(size_t)(r0 + rr) * a.d + dd] = 0.f;
+      }
+    }
+    return;
+  }
   if (early) {
     const int cq = codes_l[q];
     float tq[EI];

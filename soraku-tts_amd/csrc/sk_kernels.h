@@ -282,6 +282,17 @@ template <int CTRL, int ROW_MASK, bool BOUND0>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, BOUND0));
 }
+// Workgroup barrier for LDS: waits for this wave's LDS (and scalar memory)
+// operations only.  A fenced __syncthreads also waits for every global load
+// the wave has in flight; the samplers and the depth steps share data
+// between waves through LDS alone, while their weight loads stay in flight.
+__device__ __forceinline__ void sk_sync() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += dpp<0xb1, 0xf, true>(v);    // quad_perm [1,0,3,2]
   v += dpp<0x4e, 0xf, true>(v);    // quad_perm [2,3,0,1]
@@ -1658,7 +1669,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
     }
     best = wave_max_u64(best);
     if (lane == 0) s.bk[wave] = best;
-    __syncthreads();
+    sk_sync();
     unsigned long long b = s.bk[0];
 #pragma unroll
     for (int w = 1; w < SWAVES; ++w) b = s.bk[w] > b ? s.bk[w] : b;
@@ -1678,7 +1689,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
   mx = wave_max_dpp(mx);
   sm = wave_sum_dpp(sm);
   if (lane == 0) s.bst[wave] = make_float4(mx, sm, __int_as_float(nf), 0.f);
-  __syncthreads();
+  sk_sync();
   float4 b0 = s.bst[0];
   float M = b0.x, S = b0.y;
   int nfin = __float_as_int(b0.z);
@@ -1717,7 +1728,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
   }
   const unsigned red = wave_reduce8(w8, lane);
   if ((lane & 7) == 0) s.lvc[wave][lane >> 3] = red;
-  __syncthreads();
+  sk_sync();
   // Lane j (of every row of 16 lanes) owns level j: its count over all waves
   // and over the waves before this one, then inclusive scans over the 16
   // levels.  L = the first level whose cumulative count reaches keff (15 if
@@ -1764,7 +1775,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
     const int n = cum;
     const int n2 = (n + 1) & ~1;
     if (tid == n && n < n2) ck[n] = 0ull;
-    __syncthreads();
+    sk_sync();
     if (n <= 64) {
       // Wave w counts, for each of the first 64 keys (one per lane), the keys
       // of its slice [8w, 8w + 8) that sort before it; wave 0 adds the slices.
@@ -1783,7 +1794,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
         }
       }
       s.prk[wave][lane] = part;
-      __syncthreads();
+      sk_sync();
       if (wave == 0) {
         int rank = 0;
 #pragma unroll
@@ -1798,7 +1809,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
       const unsigned long long K = ck[tid];
       sk[key_rank(ck, n2, K)] = K;
     }
-    __syncthreads();
+    sk_sync();
     if (wave == 0) return draw_sorted(sk, use_k ? topk_count(sk, n, top_k) : n, top_p, u, W);
     return 0;
   }
@@ -1816,11 +1827,11 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int i = tid * 4; i < SWAVES * 4 * 256; i += SNT * 4)
         *reinterpret_cast<int4*>(&H[i]) = make_int4(0, 0, 0, 0);
-      __syncthreads();
+      sk_sync();
 #pragma unroll
       for (int i = 0; i < VPT; ++i)
         if (tid + i * SNT < V && (key[i] & pmask) == prefix) atomicAdd(&Hw[(key[i] >> shift) & 255u], 1);
-      __syncthreads();
+      sk_sync();
       // bin 255 - tid (threads below 256) summed over the private copies,
       // then a scan over bins.
       int cnt = 0;
@@ -1830,16 +1841,16 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
       }
       int incl = wave_incl_scan(cnt);
       if (lane == 63) s.scan[wave] = incl;
-      __syncthreads();
+      sk_sync();
       for (int w = 0; w < wave; ++w) incl += s.scan[w];
       const int excl = incl - cnt;
       if (cnt > 0 && excl < kr && kr <= incl) { s.sel_digit = 255 - tid; s.sel_excl = excl; s.sel_cnt = cnt; }
-      __syncthreads();
+      sk_sync();
       prefix |= (uint32_t)s.sel_digit << shift;
       pmask |= 255u << shift;
       kr -= s.sel_excl;
       const bool done = (s.sel_cnt == kr);
-      __syncthreads();
+      sk_sync();
       if (done) break;
     }
     cut = prefix;
@@ -1855,7 +1866,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
   }
   const int wincl = wave_incl_scan(myc);
   if (lane == 63) s.wcount[wave] = wincl;
-  __syncthreads();
+  sk_sync();
   int base = 0, n = 0;
 #pragma unroll
   for (int w = 0; w < SWAVES; ++w) {
@@ -1868,9 +1879,9 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
     if (keep[i]) ck[base++] = skey(xr[i], tid + i * SNT);
   int P = 1;
   while (P < n) P <<= 1;
-  __syncthreads();
+  sk_sync();
   for (int i = n + tid; i < P; i += SNT) ck[i] = 0ull;
-  __syncthreads();
+  sk_sync();
   // Bitonic sort of the keys in LDS, largest first.
   for (int k = 2; k <= P; k <<= 1)
     for (int j = k >> 1; j > 0; j >>= 1) {
@@ -1882,7 +1893,7 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
           if (swap) { ck[i] = kl; ck[l] = ki; }
         }
       }
-      __syncthreads();
+      sk_sync();
     }
   if (wave == 0) return draw_sorted(ck, n, top_p, u, W);
   return 0;
@@ -2043,7 +2054,7 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
       if (lane == 0) red[1][rr][wave] = sh;
     }
   }
-  __syncthreads();
+  sk_sync();
   for (int rr = 0; rr < nr; ++rr) {
     float t = 0.f;
 #pragma unroll
@@ -2164,13 +2175,13 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   }
   if (!last) {
     if (a.abuf) {
-      __syncthreads();                   // codes_l[q] from thread 0
+      sk_sync();                   // codes_l[q] from thread 0
       depth_input_rows<TL>(a, r0, q, codes_l[q]);
     }
     return;
   }
 
-  __syncthreads();
+  sk_sync();
   if (from_prefix) {
     // x = prefix_{Q-1} + scale * table[Q-1][code]: the prefix update's own
     // order (model.py:600-605), the same sum as the frame embedding
@@ -2322,7 +2333,7 @@ __global__ __launch_bounds__(SNT) void depth_sample_gemv_kernel(SampleArgs a, Ge
       a.codes_cur[qs] = code;
     }
   }
-  __syncthreads();
+  sk_sync();
   code = code_sh;
 
   // prefix += table[q-1][code] * scale; x = hidden + prefix; a = w * (x / rms(x))
@@ -2344,7 +2355,7 @@ __global__ __launch_bounds__(SNT) void depth_sample_gemv_kernel(SampleArgs a, Ge
     ss = wave_sum_dpp(ss);
     if (lane == 0) red[m][wave] = ss;
   }
-  __syncthreads();
+  sk_sync();
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     float t = 0.f;
@@ -2358,7 +2369,7 @@ __global__ __launch_bounds__(SNT) void depth_sample_gemv_kernel(SampleArgs a, Ge
       if (lead) g.norm_out[(size_t)m * g.ldno + tid + i * SNT] = y;
     }
   }
-  __syncthreads();
+  sk_sync();
 
   float acc[RW][2][M];
 #pragma unroll
@@ -2637,7 +2648,7 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
         a.codes_cur[qs] = code;
       }
     }
-    __syncthreads();
+    sk_sync();
     code = code_sh;
     const size_t trow = ((size_t)qs * a.V + code) * KD;
 #pragma unroll
@@ -2677,7 +2688,7 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
     ss = wave_sum_dpp(ss);
     if (lane == 0) red[m][wave] = ss;
   }
-  __syncthreads();
+  sk_sync();
   float inv[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) {
@@ -2796,7 +2807,7 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
       const int word = lane / (64 / ND);
       dsum[wave][word / M][word % M] = dt;
     }
-    __syncthreads();
+    sk_sync();
     if (tid < RD * M) {
       const int i = tid / M, m = tid - i * M, row = row0 + i;
       float t = 0.f;

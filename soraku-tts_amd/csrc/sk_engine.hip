@@ -737,15 +737,27 @@ hipError_t enqueue_frame(sk_engine* e) {
   for (int q = 0; q < c.n_codebooks; ++q) {
     if (e->wide) {
       if ((err = enqueue_depth_wide(e, q)) != hipSuccess) return err;
+      int slices = 1;
       if (e->wide_tables) {   // G_q in gbuf[q % 2] (after codebook 0: r_0 G_0), G_{q+1} into the other
         s.ptab = e->ptab; s.ki = c.depth_inner;
         s.g_in = e->gbuf[q % 2];
         s.g_out = q + 2 < c.n_codebooks ? e->gbuf[(q + 1) % 2] : nullptr;
         s.g_in_normed = q == 0;
         s.act = e->act; s.ld_act = e->inner_max; s.xs_act = e->xs_act;
+        // Several workgroups per utterance (each draws the code, each writes
+        // a slice), reading the prefix from one buffer and writing the other;
+        // the last codebook's sampler clears `prefix`, where codebook 0 reads.
+        if (q + 1 < c.n_codebooks) {
+          slices = sample_slices(c.n_utts, d, c.depth_inner);
+          s.prefix = q % 2 == 0 ? e->prefix : e->prefix2;
+          s.prefix_out = q % 2 == 0 ? e->prefix2 : e->prefix;
+        } else {
+          s.prefix = e->prefix;
+          s.prefix_out = nullptr;
+        }
       }
-      err = (wt == SK_BF16) ? launch_sample_step<WBF16>(s, q, c.n_utts, e->stream)
-                            : launch_sample_step<WF32>(s, q, c.n_utts, e->stream);
+      err = (wt == SK_BF16) ? launch_sample_step<WBF16>(s, q, c.n_utts, e->stream, slices)
+                            : launch_sample_step<WF32>(s, q, c.n_utts, e->stream, slices);
       if (err != hipSuccess) return err;
       continue;
     }

@@ -1982,6 +1982,10 @@ struct SampleArgs {
   // codebook order), so the frame embedding is one more row (null: the rows
   // are gathered and summed here).
   const float* prefix_last;
+  // Where the advanced prefix goes (null: back into prefix).  Set when the
+  // sampler of an utterance runs in several workgroups (gridDim.y > 1), which
+  // all read the whole prefix while each writes its slice.
+  float* prefix_out;
 };
 
 // The depth input rows of one utterance after its code q (sample_step_kernel,
@@ -1991,19 +1995,25 @@ struct SampleArgs {
 // code is known (all threads hold it).
 constexpr int DEPTH_DPT = 8;             // d <= SNT * DEPTH_DPT
 constexpr int DEPTH_API = 4;             // code-table inner indices per thread: ki <= SNT * DEPTH_API
-template <typename TL>
-__device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, int q, int code) {
+// DPT: elements of d per thread (d <= SNT * DPT).  The outputs are split over
+// the ns workgroups of the utterance (slice sl): each forms the whole x for
+// the norm but writes d / ns of the prefix and abuf and ki / ns of G and act.
+template <typename TL, int DPT>
+__device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, int q, int code, int sl, int ns) {
   __shared__ float red[2][2][SWAVES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nr = a.rows_per_utt;         // 1 or 2
   const size_t trow = ((size_t)q * a.V + code) * a.d;
   const bool tables = a.ptab != nullptr;   // uniform
+  const int ds = a.d / ns, db = sl * ds;      // this slice's hidden indices
+  const int kis = a.ki / ns, kb = sl * kis;   // and inner indices
+  float* pout = a.prefix_out ? a.prefix_out : a.prefix;
   // Every operand first, indices clamped in bounds (rows past nr re-read row
   // 0, dims past d re-read d-1): one round trip, no branch between the
   // loads, and no load behind the prefix stores that might alias it.
-  float tv[DEPTH_DPT], gv[DEPTH_DPT], pv[2][DEPTH_DPT], hv[2][DEPTH_DPT];
+  float tv[DPT], gv[DPT], pv[2][DPT], hv[2][DPT];
 #pragma unroll
-  for (int i = 0; i < DEPTH_DPT; ++i) {
+  for (int i = 0; i < DPT; ++i) {
     const int k = min(tid + i * SNT, a.d - 1);
     tv[i] = TL::get(a.table, trow + k);
     gv[i] = a.w_in[k];
@@ -2020,7 +2030,8 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
     const float* pr = a.ptab + ((size_t)q * a.V + code) * 2 * a.ki;
 #pragma unroll
     for (int i = 0; i < DEPTH_API; ++i) {
-      const int k = min(tid + i * SNT, a.ki - 1);
+      if (i * SNT >= kis) break;         // uniform
+      const int k = kb + min(tid + i * SNT, kis - 1);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         pq[h][i] = pr[h * a.ki + k];
@@ -2030,19 +2041,19 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
       }
     }
   }
-  float xv[2][DEPTH_DPT];
+  float xv[2][DPT];
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
     const size_t ro = (size_t)(r0 + rr) * a.d;
     float ss = 0.f, sh = 0.f;
 #pragma unroll
-    for (int i = 0; i < DEPTH_DPT; ++i) {
+    for (int i = 0; i < DPT; ++i) {
       const int k = tid + i * SNT;
       const float p = __fadd_rn(pv[rr][i], __fmul_rn(tv[i], a.scale));
       const float x = __fadd_rn(hv[rr][i], p);
       xv[rr][i] = x;
       if (k < a.d) {
-        if (rr < nr) a.prefix[ro + k] = p;
+        if (rr < nr && k - db >= 0 && k - db < ds) pout[ro + k] = p;
         ss = fmaf(x, x, ss);
         sh = fmaf(hv[rr][i], hv[rr][i], sh);
       }
@@ -2062,9 +2073,9 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
     const float inv = 1.0f / sqrtf(t / (float)a.d + a.eps_in);
     const size_t ro = (size_t)(r0 + rr) * a.d;
 #pragma unroll
-    for (int i = 0; i < DEPTH_DPT; ++i) {
+    for (int i = 0; i < DPT; ++i) {
       const int k = tid + i * SNT;
-      if (k < a.d) {
+      if (k - db >= 0 && k - db < ds) {
         const float y = gv[i] * (xv[rr][i] * inv);
         a.abuf[ro + k] = y;
         if (a.xs_abuf) xsplit_store(a.xs_abuf, r0 + rr, k, y);
@@ -2084,8 +2095,9 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
       const size_t go = (size_t)(r0 + rr) * 2 * a.ki;
 #pragma unroll
       for (int i = 0; i < DEPTH_API; ++i) {
-        const int k = tid + i * SNT;
-        if (k < a.ki) {
+        if (i * SNT >= kis) break;       // uniform
+        const int j = tid + i * SNT, k = kb + j;
+        if (j < kis) {
           const float gt = fmaf(a.scale, pq[0][i], gq[rr][0][i] * rms0);
           const float up = fmaf(a.scale, pq[1][i], gq[rr][1][i] * rms0);
           if (a.g_out) {
@@ -2113,7 +2125,7 @@ __device__ __forceinline__ void depth_input_rows(const SampleArgs& a, int r0, in
 // is loaded in the first round trip (this frame's draws and flags sit at
 // fixed addresses, so nothing waits on the frame counter).  VPT = logits per
 // thread, ceil(V / SNT).
-template <typename TL, int VPT>
+template <typename TL, int VPT, int DPT>
 __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   extern __shared__ unsigned char raw[];
   double* W = reinterpret_cast<double*>(raw);
@@ -2123,6 +2135,10 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   __shared__ int codes_l[64];
 
   const int ut = blockIdx.x;
+  // Workgroups (ut, sl) for sl < gridDim.y all draw the utterance's code
+  // from the same inputs (so the same code); slice 0 records it, and each
+  // forms its slice of the next depth step's inputs.
+  const int sl = blockIdx.y, ns = gridDim.y;
   const int r0 = ut * a.rows_per_utt;
   const float* lc = a.logits + (size_t)r0 * a.ldl;
   const float* lu = (a.rows_per_utt == 2) ? lc + a.ldl : nullptr;
@@ -2139,7 +2155,7 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   const float topp = q0 ? P.top_p_q0 : P.top_p;
   float xr[VPT];
   merge_mask<VPT>(lc, lu, P.cfg_scale, a.V, a.bos, a.eos, a.pad, a.flag_cur, ut, q != 0, temp,
-                  P.record_logits ? a.dbg + ((size_t)ut * a.Q + q) * a.V : nullptr, xr);
+                  (P.record_logits && sl == 0) ? a.dbg + ((size_t)ut * a.Q + q) * a.V : nullptr, xr);
   // The last codebook's frame embedding: the table rows of codebooks
   // 0 .. Q-2 do not depend on the draw, so they are in flight during it
   // (issued once the logits are in, so the sampler does not wait for them).
@@ -2169,17 +2185,20 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   if (threadIdx.x == 0) {
     if (forced) code = (int)a.forced_ring[uoff];
     code = min(max(code, 0), a.V - 1);
-    a.codes_ring[uoff] = code;
-    a.codes_cur[(size_t)ut * a.Q + q] = code;
+    if (sl == 0) {
+      a.codes_ring[uoff] = code;
+      a.codes_cur[(size_t)ut * a.Q + q] = code;
+    }
     codes_l[q] = code;
   }
   if (!last) {
     if (a.abuf) {
       sk_sync();                   // codes_l[q] from thread 0
-      depth_input_rows<TL>(a, r0, q, codes_l[q]);
+      depth_input_rows<TL, DPT>(a, r0, q, codes_l[q], sl, ns);
     }
     return;
   }
+  if (sl != 0) return;               // the last codebook runs one workgroup per utterance
 
   sk_sync();
   if (from_prefix) {

@@ -167,12 +167,28 @@ static hipError_t with_vpt(int V, F&& f) {
 }
 
 template <typename TL>
-static hipError_t launch_sample_step(const SampleArgs& a, int q, int n_utts, hipStream_t st) {
+static hipError_t launch_sample_step(const SampleArgs& a, int q, int n_utts, hipStream_t st, int slices = 1) {
   return with_vpt(a.V, [&](auto vpt) {
-    hipLaunchKernelGGL((sample_step_kernel<TL, decltype(vpt)::value>), dim3(n_utts), dim3(SNT), SAMPLE_SMEM, st,
-                       a, q);
+    constexpr int VPT = decltype(vpt)::value;
+    const dim3 grid(n_utts, slices);
+    if (a.d <= SNT)
+      hipLaunchKernelGGL((sample_step_kernel<TL, VPT, 1>), grid, dim3(SNT), SAMPLE_SMEM, st, a, q);
+    else if (a.d <= 2 * SNT)
+      hipLaunchKernelGGL((sample_step_kernel<TL, VPT, 2>), grid, dim3(SNT), SAMPLE_SMEM, st, a, q);
+    else if (a.d <= 4 * SNT)
+      hipLaunchKernelGGL((sample_step_kernel<TL, VPT, 4>), grid, dim3(SNT), SAMPLE_SMEM, st, a, q);
+    else
+      hipLaunchKernelGGL((sample_step_kernel<TL, VPT, DEPTH_DPT>), grid, dim3(SNT), SAMPLE_SMEM, st, a, q);
     return hipGetLastError();
   });
+}
+// Workgroups per utterance for a many-row sampler that forms the next depth
+// step's inputs: the most (up to 16, within 256 in all) that divide d and the
+// inner size evenly.
+static inline int sample_slices(int n_utts, int d, int ki) {
+  int s = 16;
+  while (s > 1 && (n_utts * s > 256 || d % s != 0 || ki % s != 0)) s /= 2;
+  return s;
 }
 
 // Depth step with the previous codebook's sampler folded in
@@ -244,8 +260,14 @@ static inline hipError_t prepare_sampler() {
   for (int V : {SNT, 2 * SNT, 3 * SNT, 5 * SNT, 8 * SNT})
     with_vpt(V, [&](auto vpt) {
       constexpr int P = decltype(vpt)::value;
-      set(reinterpret_cast<const void*>(sample_step_kernel<WF32, P>));
-      set(reinterpret_cast<const void*>(sample_step_kernel<WBF16, P>));
+      set(reinterpret_cast<const void*>(sample_step_kernel<WF32, P, 1>));
+      set(reinterpret_cast<const void*>(sample_step_kernel<WF32, P, 2>));
+      set(reinterpret_cast<const void*>(sample_step_kernel<WF32, P, 4>));
+      set(reinterpret_cast<const void*>(sample_step_kernel<WF32, P, DEPTH_DPT>));
+      set(reinterpret_cast<const void*>(sample_step_kernel<WBF16, P, 1>));
+      set(reinterpret_cast<const void*>(sample_step_kernel<WBF16, P, 2>));
+      set(reinterpret_cast<const void*>(sample_step_kernel<WBF16, P, 4>));
+      set(reinterpret_cast<const void*>(sample_step_kernel<WBF16, P, DEPTH_DPT>));
       set(reinterpret_cast<const void*>(sample_op_kernel<P>));
       return e;
     });

@@ -133,6 +133,9 @@ struct sk_engine {
   float2* rope = nullptr;     // [rows][hd/2] (cos, sin) at each row's position
   float* sk_partial = nullptr;  // many-row path: split-K slice partials
   unsigned* sk_arrive = nullptr;
+  unsigned long long* sk_tpart = nullptr;   // split-K partials as tagged words
+  unsigned* sk_err = nullptr;              // bit 1: a split-K merge wait timed out
+  int sk_tags = 0;                         // GEMM launches enqueued so far in the frame
   // Many-row path with BF16 weights: GEMM inputs in split form (written by
   // their producers) and per-tile sums of squares for the RMSNorms.
   uint16_t *xs_x = nullptr, *xs_attn = nullptr, *xs_act = nullptr, *xs_abuf = nullptr, *xs_y = nullptr;
@@ -402,7 +405,12 @@ hipError_t launch_skinny_bf16(SkinnyArgs a, float* partial, unsigned* arrive, bo
   return hipGetLastError();
 }
 template <int EPI, bool NORM = false>
-hipError_t launch_skinny(sk_engine* e, const SkinnyArgs& a) {
+hipError_t launch_skinny(sk_engine* e, const SkinnyArgs& a0) {
+  SkinnyArgs a = a0;
+  if (e->sk_tags < 255) {   // a distinct tag per launch of the frame (tag_idx < 255)
+    a.tpart = e->sk_tpart; a.fc = e->fc; a.tag_idx = e->sk_tags++;
+    a.err = e->sk_err; a.spin = e->spin_ticks;
+  }
   return e->c.weight_dtype == SK_BF16 ? launch_skinny_bf16<EPI, NORM>(a, e->sk_partial, e->sk_arrive, e->split_k,
                                                                       e->stream)
                                       : launch_skinny_w<EPI, NORM, WF32>(a, e->stream);
@@ -675,6 +683,7 @@ hipError_t enqueue_tail(sk_engine* e);
 hipError_t enqueue_frame(sk_engine* e) {
   const sk_config& c = e->c;
   const int d = c.d_model, M = e->rows, V = c.audio_vocab;
+  e->sk_tags = 0;
   const int wt = c.weight_dtype;
   const size_t tsz = (wt == SK_BF16) ? 2 : 4;
   hipError_t err;
@@ -1094,6 +1103,8 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
                                   (size_t)c.audio_vocab, (size_t)c.d_model});
     ALLOC(e->sk_partial, (nmax / 16 + 1) * 4 * SK_PSZ);
     ALLOC(e->sk_arrive, nmax / 16 + 1);
+    ALLOC(e->sk_tpart, (nmax / 16 + 1) * SK_MAX_SPLIT * SK_PSZ);
+    ALLOC(e->sk_err, 1);
   }
   ALLOC(e->part, R * c.n_q_heads * e->max_chunks * part_stride(c.head_dim));
   const bool split_in = e->wide && c.weight_dtype == SK_BF16;
@@ -1127,6 +1138,11 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   if (he == hipSuccess) he = hipMemset(e->prefix, 0, R * d * sizeof(float));
   if (he == hipSuccess) he = hipMemset(e->prefix2, 0, R * d * sizeof(float));
   if (he == hipSuccess) he = hipMemset(e->kv_len, 0, R * sizeof(int));
+  if (he == hipSuccess) he = hipMemset(e->sk_err, 0, sizeof(unsigned));
+  if (he == hipSuccess)   // tag 0 is never a launch's
+    he = hipMemset(e->sk_tpart, 0,
+                   (std::max({(size_t)e->nqkv, (size_t)c.trunk_inter, (size_t)c.depth_inner, (size_t)c.audio_vocab,
+                              (size_t)c.d_model}) / 16 + 1) * SK_MAX_SPLIT * SK_PSZ * sizeof(unsigned long long));
   if (he == hipSuccess)
     he = hipMemset(e->sk_arrive, 0,
                    (std::max({(size_t)e->nqkv, (size_t)c.trunk_inter, (size_t)c.depth_inner, (size_t)c.audio_vocab,
@@ -1193,7 +1209,7 @@ int sk_destroy(sk_engine* e) {
   if (!e) return SK_OK;
   if (e->stream) hipStreamSynchronize(e->stream);
   drop_graphs(e);
-  void* bufs[] = {e->sk_partial, e->sk_arrive, e->xs_x, e->xs_attn, e->xs_act, e->xs_abuf, e->xs_y, e->ss_x, e->ss_y, e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
+  void* bufs[] = {e->sk_partial, e->sk_arrive, e->sk_tpart, e->sk_err, e->xs_x, e->xs_attn, e->xs_act, e->xs_abuf, e->xs_y, e->ss_x, e->ss_y, e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
                   e->kc, e->vc, e->inv_freq, e->rope, e->part, e->dbg, e->embeds, e->u_cur, e->flag_cur, e->codes_cur,
                   e->kv_len, e->pos, e->active, e->plen, e->fc, e->flag_ring, e->u_ring,
                   e->pf_mem, e->ptab, e->gbuf[0], e->gbuf[1],
@@ -1501,8 +1517,12 @@ int sk_capture(sk_engine* e) {
 
 // The XCD-resident layers' error word (read after the stream is drained).
 static int check_lx(sk_engine* e) {
-  if (!e->lx) return SK_OK;
   unsigned w = 0;
+  if (e->sk_err) {
+    SK_HIP(hipMemcpy(&w, e->sk_err, sizeof(w), hipMemcpyDeviceToHost));
+    SK_CHECK(w == 0u, SK_EHIP, "split-K merge wait timed out (error word 0x%x); the engine must be recreated", w);
+  }
+  if (!e->lx) return SK_OK;
   SK_HIP(hipMemcpy(&w, e->lx_err, sizeof(w), hipMemcpyDeviceToHost));
   SK_CHECK(w == 0u, SK_EHIP, "trunk layer barrier timed out (error word 0x%x); the engine must be recreated", w);
   return SK_OK;

@@ -36,6 +36,15 @@ struct SkinnyArgs {
   float* ss_out;                       // [32][N/16] sums of out^2 per row and output tile; null: none
   float* pre_out; int ld_pre;          // SwiGLU: gate and up before the activation, [R][ld_pre]
                                        // (gate at o, up at N + o); null: none
+  // Split-K merge by tagged words (null tpart: the arrival-count merge):
+  // slices 1.. store their partials as 8-byte words (value, tag) and leave;
+  // slice 0 reads them until every tag is this launch's, *fc * 256 + tag_idx
+  // + 1 (fc: the frame counter, constant over a frame; tag_idx: the launch's
+  // place among the frame's GEMM launches), so a word left by an earlier
+  // launch never carries it.  A wait past `spin` ticks sets err bit 1.
+  unsigned long long* tpart;           // [tiles][SK_MAX_SPLIT][SK_PSZ]
+  const int* fc; int tag_idx;
+  unsigned* err; unsigned long long spin;
 };
 
 // Floats per slice partial: two epilogue values per thread (SwiGLU) + 32 row
@@ -221,6 +230,8 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i16 = lane & 15, kq = lane >> 4;
   const int S = a.ksplit;
+  const bool tagged = S > 1 && a.tpart != nullptr;
+  const int fcv = tagged ? *a.fc : 0;
   int tile = blockIdx.x, slice = 0;
   if (S > 1) {
     const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
@@ -401,7 +412,60 @@ __global__ __launch_bounds__(W * 64) void skinny_bf16_kernel(SkinnyArgs a) {
       for (int k4 = 0; k4 < 4; ++k4) ss += ssq[w][t][k4 * 16 + (l & 15)];
   }
   if constexpr (XS && NORM) ss = ssr[r];
-  if (S > 1) {
+  if (tagged) {
+    const unsigned long long tag = (unsigned long long)((unsigned)fcv * 256u + (unsigned)a.tag_idx + 1u) << 32;
+    unsigned long long* tp = a.tpart + (size_t)tile * SK_MAX_SPLIT * SK_PSZ;
+    auto put = [&](unsigned long long* p, float x) {
+      __hip_atomic_store(p, tag | __float_as_uint(x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
+    if (slice != 0) {
+      if (et) {
+#pragma unroll
+        for (int n = 0; n < NA; ++n) put(tp + (size_t)slice * SK_PSZ + n * 512 + tid, c[n]);
+        if (XNORM && v == 0 && (l >> 4) == 0) put(tp + (size_t)slice * SK_PSZ + 2 * 512 + r, ss);
+      }
+      return;
+    }
+    if (et) {
+      // slices 1 .. S-1 (unrolled to SK_MAX_SPLIT, slice index clamped):
+      // word (q - 1) * NA + n, then the row sums of squares
+      constexpr int NW = (NA + (XNORM ? 1 : 0)) * (SK_MAX_SPLIT - 1);
+      auto addr = [&](int i) {
+        const int q = i < NA * (SK_MAX_SPLIT - 1) ? i / NA + 1 : i - NA * (SK_MAX_SPLIT - 1) + 1;
+        const size_t qo = (size_t)min(q, S - 1) * SK_PSZ;
+        return i < NA * (SK_MAX_SPLIT - 1) ? tp + qo + (i % NA) * 512 + tid : tp + qo + 2 * 512 + r;
+      };
+      unsigned long long w[NW];
+#pragma unroll
+      for (int i = 0; i < NW; ++i) w[i] = *addr(i);
+      const unsigned long long deadline = __builtin_amdgcn_s_memrealtime() + a.spin;
+      for (;;) {
+        bool miss = false;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) miss |= (w[i] & 0xffffffff00000000ull) != tag;
+        if (!miss) break;
+        if (__builtin_amdgcn_s_memrealtime() > deadline) {
+          __hip_atomic_fetch_or(a.err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+          break;
+        }
+#pragma unroll
+        for (int i = 0; i < NW; ++i)
+          if ((w[i] & 0xffffffff00000000ull) != tag)
+            w[i] = __hip_atomic_load(addr(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      // in slice order, as the arrival-count merge adds them
+#pragma unroll
+      for (int n = 0; n < NA; ++n)
+#pragma unroll
+        for (int q = 1; q < SK_MAX_SPLIT; ++q)
+          if (q < S) c[n] += __uint_as_float((unsigned)w[(q - 1) * NA + n]);
+      if constexpr (XNORM) {
+#pragma unroll
+        for (int q = 1; q < SK_MAX_SPLIT; ++q)
+          if (q < S) ss += __uint_as_float((unsigned)w[NA * (SK_MAX_SPLIT - 1) + q - 1]);
+      }
+    }
+  } else if (S > 1) {
     float* mine = a.partial + ((size_t)tile * S + slice) * SK_PSZ;
     if (et) {
 #pragma unroll

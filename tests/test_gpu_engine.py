@@ -614,6 +614,48 @@ def test_sixteen_utterances_q06b_bf16(hip_device):
     assert rel < LOGIT_TOL
 
 
+def test_split_k_wait_timeout_reports_error_and_fresh_engine_decodes(hip_device):
+    """The split-K GEMMs' bounded wait (slice 0 reading the other slices'
+    tagged partials), forced to give up from the host with
+    sk_debug_set_spin_ticks(e, 0): a merge that does not find every partial
+    at its first look ends at once and sets the error word, every kernel
+    exits, and sk_step_frame returns SK_EHIP with its message (within a few
+    frames: a merge that finds its partials ready does not wait).  A fresh
+    engine on the same weights then decodes three utterances x CFG (the
+    skinny-GEMM path with split-K, Qwen3-0.6B shape, BF16 weights) to the
+    oracle's logits."""
+    import dataclasses
+
+    from oracle.model import QWEN3_06B
+    from soraku_amd import GraphFrameEngine
+    from soraku_amd._lib import SK_EHIP, SkError, check, lib
+
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)
+    w = _device_weights(s, 23, hip_device)
+    rng = np.random.default_rng(23)
+    items = [(rng.integers(0, s.text_vocab, 12), np.array([7]), rng.integers(0, s.codebook_size, (2, s.n_codebooks)))
+             for _ in range(3)]
+    e = GraphFrameEngine(device=hip_device, max_cache_len=64, cfg_scale=1.5, batch=2, state_dict=w,
+                         shape=_shape(s), n_utts=3, bf16=True)
+    e.set_temperature(0.0)
+    e.prefill_utterances(items)
+    check(lib().sk_debug_set_spin_ticks(e._h, 0))
+    e.capture()
+    err = None
+    for fi in range(5):
+        try:
+            e.step_frame(mask_eos_q0=False, uniforms=np.zeros(3 * s.n_codebooks))
+        except SkError as ex:
+            err = ex
+            break
+    e.close()
+    print(f"forced split-K timeout: {err} (frame {fi})", flush=True)
+    assert err is not None and err.code == SK_EHIP and "split-K merge wait timed out" in str(err)
+    rel = _many_utterance_case(s, w, 3, 24, hip_device, bf16=True, frames=2)
+    print(f"fresh engine after the timeout: max row-relative logit error {rel:.3e}")
+    assert rel < LOGIT_TOL
+
+
 def test_sixteen_utterances_q06b_bf16_kv(hip_device):
     """The throughput batch's precision: 16 utterances x CFG at the
     Qwen3-0.6B shape with BF16 weights and a BF16 KV cache (the streaming

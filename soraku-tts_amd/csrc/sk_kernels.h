@@ -2623,14 +2623,13 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
         wgu[r][1][j] = TL::raw(g.w_up, off);
       }
   }
-  // The down rows go ahead of the sampler too when few loads are in flight
-  // per lane (at most 16: with 16 gate/up + 8 down per lane the sampler itself
-  // ran slower behind them, code drawn after 10.7 us instead of 8.6), else
-  // they follow the code with its table entries.
-  constexpr bool WD_EARLY = (GPART ? 2 * RWG * NV : 0) + RD <= 16;
+  // The down rows: at entry without a sampler; with one, once the logits
+  // are merged (issued at entry, they delayed the logits the sampler waits
+  // for: at the 1.7B shape its 16.8 MB held them back ~1.6 us), so they
+  // stream while the sampler runs.
   const int row0 = blockIdx.x * RD;
   uint4 wd[DPART ? RD : 1];
-  if constexpr (DPART && (!SAMPLE || WD_EARLY)) {
+  if constexpr (DPART && !SAMPLE) {
 #pragma unroll
     for (int i = 0; i < RD; ++i) wd[i] = TL::raw(g.w_down, (size_t)(row0 + i) * KI + kc);
   }
@@ -2647,6 +2646,10 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
     merge_mask_loaded<VPT>(cvv, uvv, M == 2, P.cfg_scale, a.V, a.bos, a.eos, a.pad, &mflag, 0, qs != 0,
                            q0 ? P.temperature_q0 : P.temperature,
                            (lead && P.record_logits) ? a.dbg + (size_t)qs * a.V : nullptr, xr);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < RD; ++i) wd[i] = TL::raw(g.w_down, (size_t)(row0 + i) * KI + kc);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // The code of codebook q-1 (every workgroup draws the same one), then its
@@ -2673,10 +2676,6 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
 #pragma unroll
     for (int i = 0; i < DPT; ++i) tv[i] = TL::get(a.table, trow + tid + i * SNT);
     load_gq();
-    if constexpr (!WD_EARLY) {
-#pragma unroll
-      for (int i = 0; i < RD; ++i) wd[i] = TL::raw(g.w_down, (size_t)(row0 + i) * KI + kc);
-    }
     const float* pp = g.ptab + ((size_t)qs * a.V + code) * 2 * KI + kc;
 #pragma unroll
     for (int h = 0; h < 2; ++h)

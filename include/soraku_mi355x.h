@@ -189,13 +189,15 @@ int32_t sk_frames_done(sk_engine* e);
  * kernels, -1 for a NULL engine.  For tests and profiling. */
 int32_t sk_xcd_layers(sk_engine* e);
 /* Test hook with no counterpart in the reference: the bound, in ticks of the
- * 100 MHz real-time counter, of every wait inside the XCD-resident layers
- * (barriers and tagged exchanges; default and maximum 5,000,000 = 50 ms).
- * Set before sk_capture (SK_ESTATE after).  A wait that passes it makes the
- * layer kernels leave the frame early and the next sk_step_frame /
- * sk_synchronize / sk_read_codes return SK_EHIP; 0 makes nearly every wait
- * give up at once, which is how a test forces that error path while every
- * kernel still exits normally.  The engine must then be recreated. */
+ * 100 MHz real-time counter, of every wait inside a frame's kernels (the
+ * XCD-resident layers' barriers and tagged exchanges, the many-row split-K
+ * GEMMs' merge of tagged partials; default and maximum 5,000,000 = 50 ms).
+ * Set before sk_capture (SK_ESTATE after).  A wait that passes it sets the
+ * engine's error word, the kernel goes on without the missing data, and the
+ * next sk_step_frame / sk_synchronize / sk_read_codes returns SK_EHIP; 0
+ * makes nearly every wait give up at once, which is how a test forces that
+ * error path while every kernel still exits normally.  The engine must then
+ * be recreated. */
 int sk_debug_set_spin_ticks(sk_engine* e, uint64_t ticks);
 
 /* ---- operator API (tilelang_kernels.py counterparts) ------------------

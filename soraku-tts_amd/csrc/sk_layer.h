@@ -97,6 +97,15 @@ struct LxArgs {
   unsigned long long spin_ticks;
 };
 
+// At d = 1024 the waves that issue the weight rows at entry first sleep 8
+// units of 64 clocks (~0.2 us), so the launch's input loads, issued at entry
+// by the other waves, reach the CU's memory queue ahead of the weight
+// requests.  A wave that issues more loads than the queue holds stalls at
+// issue until earlier ones return, and the input used to arrive behind the
+// weight rows.  Measured on the 0.6B frame: 818 -> 785 us (each half alone
+// -14 / -17 us; 6, 10 or 12 units 788-790 us); no change at d = 2048.
+constexpr int LX_WEIGHT_DELAY = 8;
+
 // The XCD this workgroup runs on (the XCC_ID hardware register).  The
 // dispatcher deals a launch's workgroups to the 8 XCDs round-robin, starting
 // at an XCD that can differ between launches (it did with two streams in
@@ -672,6 +681,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     const int w4 = wave;
     LxIn<D, FIX>::clear(a, wave, lane);
+    if constexpr (D == 1024) __builtin_amdgcn_s_sleep(LX_WEIGHT_DELAY);   // the input first
     // norm gains and RoPE entries (needed after the q/k/v exchange)
     const int t = tid, tr = t & 127, trow = t >> 7;
     const float qw_r = a.q_norm[tr], kw_r = a.k_norm[tr];
@@ -834,6 +844,7 @@ __global__ __launch_bounds__(LX_NT) void lx_mlp_kernel(LxArgs a) {
     // either is hoisted above the branch and made to wait for the other's loads)
     __builtin_amdgcn_sched_barrier(0);
     LxIn<D, FIX>::clear(a, wave, lane);
+    if constexpr (D == 1024) __builtin_amdgcn_s_sleep(LX_WEIGHT_DELAY);   // the input first
     float act;
     if (!gate_up(wave, act)) return;
     const unsigned tag = (unsigned)stsh[0] + 1;   // this launch's epoch

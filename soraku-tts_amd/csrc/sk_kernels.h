@@ -1170,6 +1170,14 @@ __device__ __forceinline__ float group_allsum(float v, int n) {
   if (n >= 16) v += dpp_keep<0x140, 0xf>(v);  // row_mirror: lane i <-> 15 - i
   return v;
 }
+// The same groups' maximum.
+__device__ __forceinline__ float group_allmax(float v, int n) {
+  if (n >= 2) v = fmaxf(v, dpp_keep<0xb1, 0xf>(v));
+  if (n >= 4) v = fmaxf(v, dpp_keep<0x4e, 0xf>(v));
+  if (n >= 8) v = fmaxf(v, dpp_keep<0x141, 0xf>(v));
+  if (n >= 16) v = fmaxf(v, dpp_keep<0x140, 0xf>(v));
+  return v;
+}
 
 // Two online-softmax states (max, sum, output) of one query head -> one.
 // An empty state has max -inf and contributes nothing.

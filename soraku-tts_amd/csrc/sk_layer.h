@@ -397,7 +397,7 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
   constexpr int M = LX_M, HD = LX_HD, G = LX_G, HQ = LX_HQ, HKV = LX_HKV;
   constexpr int VEC = WL::VEC, NVQ = D / (64 * VEC);
   constexpr int QRW = (G + 2) * HD / LX_PER / 4;        // q/k/v rows per exchange wave
-  constexpr int OROWS = D / LX_PER, ORW = OROWS / 4;     // W_o rows per workgroup / stream wave
+  constexpr int OROWS = D / LX_PER, ORW = OROWS / 4;     // W_o rows per workgroup / exchange wave
   constexpr int OCOL = G * HD;                           // W_o columns of one KV head
   constexpr int OE = lx_col_elems<WL>(OCOL);
   using NL = LxCols<WL, OE>;
@@ -448,10 +448,12 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
   // Chunk merge after the chunk barrier, by all 8 waves; each wave serves one
   // (row, head) pair (row tid >> 8, head (tid >> 7) & 1 of the pair, dim
   // tid & 127).  Every thread issues its output's first 16 chunk partials,
-  // lanes c = lane & 15 the pair's chunk maxima and sums; the wave turns them
-  // into weights exp(m_c - M) and 1 / sum_c l_c exp(m_c - M) with 16-lane
-  // shuffle trees and hands weight c to every lane by a shuffle, so no wave
-  // waits for another; then O = sum_c w_c o_c in chunk order.
+  // lanes c = lane & 15 (each 16-lane row alike) the pair's chunk maxima and
+  // sums; 16-lane DPP trees give every lane the maximum M and the weights'
+  // sum, each lane its chunk's weight exp(m_c - M), and readlane hands weight
+  // q to the whole wave as a scalar; then O = sum_c w_c o_c in chunk order.
+  // (LDS shuffles in place of the DPP steps and readlanes cost ~0.4 us more:
+  // some 24 dependent LDS round trips.)
   auto merge = [&]() {
     const int m = tid >> 8, gi = (tid >> 7) & 1, d = tid & (HD - 1);
     const int nch = m == 0 ? nch0 : nch1;   // uniform in the wave
@@ -465,14 +467,13 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     float mx = c < nch ? v0.x : -INFINITY;
     for (int c0 = CB; c0 < nch; c0 += CB)
       if (c0 + c < nch) mx = fmaxf(mx, lx_ld(pp + (size_t)(c0 + c) * PS + HD));
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = group_allmax(mx, 16);
     const float e0 = c < nch ? expf(v0.x - mx) : 0.f;
     float l = v0.y * e0;
     float O = 0.f;
 #pragma unroll
     for (int q = 0; q < CB; ++q) {
-      const float w = __shfl(e0, q, 64);
+      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e0), q));
       if (q < nch) O = fmaf(w, ov[q], O);
     }
     for (int c0 = CB; c0 < nch; c0 += CB) {
@@ -484,12 +485,11 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       }
 #pragma unroll
       for (int q = 0; q < CB; ++q) {
-        const float w = __shfl(e, q, 64);
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), q));
         if (c0 + q < nch) O = fmaf(w, lx_ld(pp + (size_t)(c0 + q) * PS + d), O);
       }
     }
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+    l = group_allsum(l, 16);
     ash[m][gi * HD + d] = O * (nch ? 1.0f / l : 0.f);
   };
 
@@ -498,19 +498,12 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     __builtin_amdgcn_sched_barrier(1);
     const int w4 = wave - 4, st = tid - 256;
     const int tok = st / LPT, sub = st % LPT;
-    // this wave's W_o rows; lanes with (lane & 3) == 0 own outputs
-    // (m, n) = (wd & 1, n0 + 8 h + (wd >> 1)), wd = lane >> 2, h < OH
-    const int n0 = j * OROWS + w4 * ORW, wd = lane >> 2;
-    constexpr int OH = ORW * M / 16;
     LxIn<D, FIX> in;
     unsigned ep, er;
-    long long xo[OH];
     {
       const int t0 = a.kv_len[0], t1 = a.kv_len[1], a0 = a.active[0], a1 = a.active[1];
       ep = fl[j]; er = *a.err;
       in.issue(a, st);
-#pragma unroll
-      for (int h = 0; h < OH; ++h) xo[h] = LxIn<D, FIX>::xo(a, wd & 1, n0 + 8 * h + (wd >> 1));
       rows_state(t0, t1, a0, a1);
       // every stream thread writes (thread 0 to row 0, the rest to row 1):
       // no branch for the compiler to sink these loads into
@@ -538,15 +531,6 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     load_kv(m0, c0s);
     lx_sync();                                                   // 4
     if (!lx_all_ok(okq)) return;
-    // this wave's W_o rows, head g's columns: needed only after the merge
-    // (issued before, they slow the q/k/v weight stream)
-    typename NL::raw_t wo[ORW][OU];
-#pragma unroll
-    for (int r = 0; r < ORW; ++r)
-#pragma unroll
-      for (int u = 0; u < OU; ++u)
-        wo[r][u] = NL::load(a.wo, (size_t)(n0 + r) * (HQ * HD) + g * OCOL + (size_t)(u * 64 + lane) * OE);
-    lx_sync();                                                   // 5
     if constexpr (KBF) lx_sync();                                // 6 (the rounded new token)
     // One slot: scores, chunk softmax, partial (o, max, sum) into pb.
     auto attend = [&](int it) {
@@ -634,46 +618,12 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       load_kv(live ? (s < nch0 ? 0 : 1) : 0, live ? (s < nch0 ? s : s - nch0) : 0);
       attend(it);
     }
-    // the partials are out once this wave's stores are (its K/V and W_o
-    // loads, issued before them, are in by now); stream wave 4 polls
+    // the partials are out once this wave's stores are (its K/V loads,
+    // issued before them, are in by now); stream wave 4 polls
     lx_wait_stores();
     if (!lx_xcd_barrier(fl, j, ep + 1, deadline, er, a.err, &okf, 4)) return;   // 7, 8
     merge();
-    lx_sync();                                                   // 9
-    float acc[ORW][M];
-#pragma unroll
-    for (int r = 0; r < ORW; ++r)
-#pragma unroll
-      for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
-#pragma unroll
-    for (int u = 0; u < OU; ++u) {
-      const int k0 = (u * 64 + lane) * OE;
-      float xv[M][OE];
-#pragma unroll
-      for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int i = 0; i < OE; ++i) xv[m][i] = ash[m][k0 + i];
-#pragma unroll
-      for (int r = 0; r < ORW; ++r) {
-        float wf[OE];
-        NL::widen(wo[r][u], wf);
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-#pragma unroll
-          for (int i = 0; i < OE; ++i) acc[r][m] = fmaf(wf[i], xv[m][i], acc[r][m]);
-      }
-    }
-    static_assert(ORW * M == 16 || ORW * M == 32, "O rows per stream wave");
-#pragma unroll
-    for (int h = 0; h < OH; ++h) {
-      float part[8][M];
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m) part[r][m] = acc[h * 8 + r][m];
-      const float v = lx_reduce<16, 8>(part, lane);   // word r * M + m in lanes [4 w, 4 w + 4)
-      if ((lane & 3) == 0) lx_accum(a.acc_out, (size_t)(wd & 1) * D + n0 + 8 * h + (wd >> 1), v, g == 0 ? xo[h] : 0ll);
-    }
+    lx_sync();                                                   // 9 (the exchange waves project)
   } else {
     // ===================== exchange waves =====================
     // (the two roles start with different scheduling barriers, so no code of
@@ -711,12 +661,18 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       const int wd = lane >> 3;
       if ((lane & 7) == 0) lx_put(a.qkv + (size_t)(wd & 1) * (HQ + 2 * HKV) * HD + ocol + (wd >> 1), v, tag);
     }
-    // raw q (both rows, this head pair), new k and v, as their tags arrive
+    // Wave w4 takes two whole vectors of 128 as their tags arrive -- q heads
+    // 0 and 1 of row 0 (wave 0) or of row 1 (wave 1), k of rows 0 and 1
+    // (wave 2), v of rows 0 and 1 (wave 3) -- lane l dims l and l + 64 of
+    // each, so the Qwen3 per-head RMSNorm (a wave sum) and the rotate-half
+    // RoPE (pairs l, l + 64) run on the settled registers and only their
+    // results go through LDS.
     {
       const int ldq = (HQ + 2 * HKV) * HD;
       auto src = [&](int i) -> const uint2* {
-        return i < 2 ? a.qkv + (size_t)i * ldq + g * G * HD + t
-                     : a.qkv + (size_t)trow * ldq + (i == 2 ? HQ * HD : (HQ + HKV) * HD) + g * HD + tr;
+        const int vv = i >> 1, dd = lane + (i & 1) * 64;
+        return w4 < 2 ? a.qkv + (size_t)w4 * ldq + g * G * HD + vv * HD + dd
+                      : a.qkv + (size_t)vv * ldq + (w4 == 2 ? HQ * HD : (HQ + HKV) * HD) + g * HD + dd;
       };
       unsigned long long v[4];
       // ~0.3 us before the first load: loaded right after the own store,
@@ -726,29 +682,45 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = lx_get(src(i));
       lx_report(lx_settle(v, src, tag, deadline), okq, w4, a.err);
-      qs[0][t] = lx_val(v[0]);
-      qs[1][t] = lx_val(v[1]);
-      kn[trow][tr] = lx_val(v[2]);
-      vn[trow][tr] = lx_val(v[3]);
+#pragma unroll
+      for (int vv = 0; vv < 2; ++vv) {
+        const float x1 = lx_val(v[2 * vv]), x2 = lx_val(v[2 * vv + 1]);
+        if (w4 == 3) {
+          vn[vv][lane] = x1;
+          vn[vv][lane + 64] = x2;
+        } else {
+          const int m = w4 < 2 ? w4 : vv;
+          const float ssum = wave_sum_dpp(fmaf(x1, x1, x2 * x2));
+          const float rinv = 1.0f / sqrtf(ssum / (float)HD + a.eps);
+          const float* wn = w4 < 2 ? qwn : kwn;
+          const float g1 = wn[lane], g2 = wn[lane + 64];
+          const float2 cs = csh[m][lane];
+          const float y1 = g1 * (x1 * rinv), y2 = g2 * (x2 * rinv);
+          float* o = w4 < 2 ? &qs[m][vv * HD] : kn[m];
+          o[lane] = y1 * cs.x - y2 * cs.y;
+          o[lane + 64] = y2 * cs.x + y1 * cs.y;
+        }
+      }
     }
     lx_sync();                                                   // 4
     if (!lx_all_ok(okq)) return;
-    // Qwen3 per-head RMSNorm, then rotate-half RoPE: vectors (row, q head 0,
-    // q head 1, k) = 6, waves 0-3 take 0-3 and 4-5.  Lane l holds dims l and l + 64.
-    for (int vi = w4; vi < 3 * M; vi += 4) {
-      const int m = vi / 3, kind = vi % 3;
-      float* v = kind < G ? &qs[m][kind * HD] : kn[m];
-      const float x1 = v[lane], x2 = v[lane + 64];
-      const float ssum = wave_sum_dpp(fmaf(x1, x1, x2 * x2));
-      const float rinv = 1.0f / sqrtf(ssum / (float)HD + a.eps);
-      const float* wn = kind < G ? qwn : kwn;
-      const float g1 = wn[lane], g2 = wn[lane + 64];
-      const float2 cs = csh[m][lane];
-      const float y1 = g1 * (x1 * rinv), y2 = g2 * (x2 * rinv);
-      v[lane] = y1 * cs.x - y2 * cs.y;
-      v[lane + 64] = y2 * cs.x + y1 * cs.y;
-    }
-    lx_sync();                                                   // 5
+    // This wave's W_o rows (head g's columns) and, on XCD 0, x at its
+    // outputs, needed after the merge.  Issued here, by waves that then only
+    // pass the attention's LDS barriers: a wave that issues them stalls at
+    // issue while the CU's memory queue is full, and in the stream waves that
+    // stall delayed the chunk scores.  Lanes with (lane & 3) == 0 own outputs
+    // (m, n) = (wd & 1, n0 + 8 h + (wd >> 1)), wd = lane >> 2, h < OH.
+    const int n0 = j * OROWS + w4 * ORW, wd = lane >> 2;
+    constexpr int OH = ORW * M / 16;
+    typename NL::raw_t wo[ORW][OU];
+#pragma unroll
+    for (int r = 0; r < ORW; ++r)
+#pragma unroll
+      for (int u = 0; u < OU; ++u)
+        wo[r][u] = NL::load(a.wo, (size_t)(n0 + r) * (HQ * HD) + g * OCOL + (size_t)(u * 64 + lane) * OE);
+    long long xo[OH];
+#pragma unroll
+    for (int h = 0; h < OH; ++h) xo[h] = g == 0 ? LxIn<D, FIX>::xo(a, wd & 1, n0 + 8 * h + (wd >> 1)) : 0ll;
     // append the new token (workgroup owning each row's last chunk); a BF16
     // cache stores it rounded and this step attends to the rounded values
     {
@@ -779,6 +751,40 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     if (!lx_xcd_barrier(fl, j, tag, deadline, err0, a.err, &okf, 4)) return;   // 7, 8 (stream wave 4 polls)
     merge();
     lx_sync();                                                   // 9
+    float oacc[ORW][M];
+#pragma unroll
+    for (int r = 0; r < ORW; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) oacc[r][m] = 0.f;
+#pragma unroll
+    for (int u = 0; u < OU; ++u) {
+      const int k0 = (u * 64 + lane) * OE;
+      float xv[M][OE];
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < OE; ++i) xv[m][i] = ash[m][k0 + i];
+#pragma unroll
+      for (int r = 0; r < ORW; ++r) {
+        float wf[OE];
+        NL::widen(wo[r][u], wf);
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int i = 0; i < OE; ++i) oacc[r][m] = fmaf(wf[i], xv[m][i], oacc[r][m]);
+      }
+    }
+    static_assert(ORW * M == 16 || ORW * M == 32, "O rows per exchange wave");
+#pragma unroll
+    for (int h = 0; h < OH; ++h) {
+      float part[8][M];
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) part[r][m] = oacc[h * 8 + r][m];
+      const float v = lx_reduce<16, 8>(part, lane);   // word r * M + m in lanes [4 w, 4 w + 4)
+      if ((lane & 3) == 0) lx_accum(a.acc_out, (size_t)(wd & 1) * D + n0 + 8 * h + (wd >> 1), v, xo[h]);
+    }
   }
 }
 

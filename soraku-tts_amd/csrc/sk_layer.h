@@ -59,6 +59,7 @@
 // behind it run through without waiting.
 #pragma once
 
+#include <type_traits>
 #include "sk_kernels.h"
 
 namespace sk {
@@ -354,8 +355,9 @@ __device__ __forceinline__ float lx_reduce(const float (&acc)[R][LX_M], int lane
 }
 
 // E consecutive elements of a weight row (the O and down projections' column
-// slices): FP32 E = 2 (8 bytes); BF16 E = 4 (8 bytes) or 2 (4 bytes) when the
-// slice is not a multiple of 256 columns.  Held raw from the load and widened
+// slices): FP32 E = 2 (8 bytes; 4, 16 bytes, for the O projection's 256
+// columns); BF16 E = 4 (8 bytes) or 2 (4 bytes) when the slice is not a
+// multiple of 256 columns.  Held raw from the load and widened
 // to FP32 where multiplied, so no conversion waits for a prefetch.
 template <typename WL, int E> struct LxCols;
 template <> struct LxCols<WF32, 2> {
@@ -364,6 +366,15 @@ template <> struct LxCols<WF32, 2> {
     return *reinterpret_cast<const uint2*>(static_cast<const float*>(base) + off);
   }
   __device__ __forceinline__ static void widen(raw_t t, float (&o)[2]) { o[0] = __uint_as_float(t.x); o[1] = __uint_as_float(t.y); }
+};
+template <> struct LxCols<WF32, 4> {
+  using raw_t = uint4;
+  __device__ __forceinline__ static raw_t load(const void* base, size_t off) {
+    return *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
+  }
+  __device__ __forceinline__ static void widen(raw_t t, float (&o)[4]) {
+    o[0] = __uint_as_float(t.x); o[1] = __uint_as_float(t.y); o[2] = __uint_as_float(t.z); o[3] = __uint_as_float(t.w);
+  }
 };
 template <> struct LxCols<WBF16, 4> {
   using raw_t = uint2;
@@ -399,7 +410,9 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
   constexpr int QRW = (G + 2) * HD / LX_PER / 4;        // q/k/v rows per exchange wave
   constexpr int OROWS = D / LX_PER, ORW = OROWS / 4;     // W_o rows per workgroup / exchange wave
   constexpr int OCOL = G * HD;                           // W_o columns of one KV head
-  constexpr int OE = lx_col_elems<WL>(OCOL);
+  // 16-byte FP32 slices: half the load instructions of 8-byte ones (the
+  // waves that issue them stall at issue while the CU's memory queue is full)
+  constexpr int OE = sizeof(typename WL::elem) == 4 ? 4 : lx_col_elems<WL>(OCOL);
   using NL = LxCols<WL, OE>;
   constexpr int OU = OCOL / (64 * OE);                   // column units per lane per W_o row
   constexpr int LPT = HD / ATT_DPL;                      // lanes per token
@@ -713,11 +726,20 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
     const int n0 = j * OROWS + w4 * ORW, wd = lane >> 2;
     constexpr int OH = ORW * M / 16;
     typename NL::raw_t wo[ORW][OU];
+    auto load_wo = [&](auto rb, auto re) {
 #pragma unroll
-    for (int r = 0; r < ORW; ++r)
+      for (int r = decltype(rb)::value; r < decltype(re)::value; ++r)
 #pragma unroll
-      for (int u = 0; u < OU; ++u)
-        wo[r][u] = NL::load(a.wo, (size_t)(n0 + r) * (HQ * HD) + g * OCOL + (size_t)(u * 64 + lane) * OE);
+        for (int u = 0; u < OU; ++u)
+          wo[r][u] = NL::load(a.wo, (size_t)(n0 + r) * (HQ * HD) + g * OCOL + (size_t)(u * 64 + lane) * OE);
+    };
+    // more than 8 loads per lane (the 1.7B shape's 16) go out in two halves,
+    // the second after the first slot's scores: 1,140 -> 1,136 us per 1.7B
+    // frame; at 8 loads the split cost 3 us per 0.6B frame
+    using H0 = std::integral_constant<int, 0>;
+    using H1 = std::integral_constant<int, (ORW * OU > 8 ? ORW / 2 : ORW)>;
+    using H2 = std::integral_constant<int, ORW>;
+    load_wo(H0{}, H1{});
     long long xo[OH];
 #pragma unroll
     for (int h = 0; h < OH; ++h) xo[h] = g == 0 ? LxIn<D, FIX>::xo(a, wd & 1, n0 + 8 * h + (wd >> 1)) : 0ll;
@@ -743,10 +765,19 @@ __global__ __launch_bounds__(LX_NT) void lx_attn_kernel(LxArgs a) {
       }
     }
     if constexpr (KBF) lx_sync();                                // 6 (the rounded new token)
-    for (int it = 0; it < nit; ++it) {
+    // the second half of the W_o rows (if split) once the first slot's scores are in
+    if (nit > 0) {
       lx_sync();                                                 // A: scores, V in LDS
+      load_wo(H1{}, H2{});
       lx_sync();                                                 // B: softmax
       lx_sync();                                                 // C: partials stored
+    } else {
+      load_wo(H1{}, H2{});
+    }
+    for (int it = 1; it < nit; ++it) {
+      lx_sync();                                                 // A
+      lx_sync();                                                 // B
+      lx_sync();                                                 // C
     }
     if (!lx_xcd_barrier(fl, j, tag, deadline, err0, a.err, &okf, 4)) return;   // 7, 8 (stream wave 4 polls)
     merge();

@@ -41,11 +41,14 @@
 // issued before it, and a load's data is usable only once every earlier load
 // of the wave has arrived.  Each workgroup therefore splits its 8 waves:
 //   * exchange waves (0-3) issue the first phase's weights and do the q/k/v
-//     or SwiGLU exchange and the chunk partials' barrier; they hold no
-//     prefetch across an exchange;
+//     or SwiGLU exchange; they hold no prefetch across an exchange (in the
+//     attention half they issue the O projection's rows once the q/k/v
+//     exchange is done, then only pass the attention's LDS barriers, and
+//     project after the chunk merge);
 //   * stream waves (4-7) load the input into LDS, then issue the later
-//     phases' K/V and weights ahead of use and take their inputs from LDS,
-//     so nothing they wait for is behind an exchange.
+//     phases' K/V and weights ahead of use, take their inputs from LDS and
+//     poll the chunk partials' barrier, so nothing they wait for is behind
+//     an exchange.
 // Each role is straight-line code and both execute the same sequence of LDS
 // barriers (lx_sync); none of them waits for global loads.
 //

@@ -680,6 +680,25 @@ hipError_t enqueue_depth_wide(sk_engine* e, int q) {
 
 hipError_t enqueue_tail(sk_engine* e);
 
+// Depth-step arguments of the code-table path (the per-step buffers are set
+// by the caller).
+DepthArgs depth_args(sk_engine* e) {
+  const sk_config& c = e->c;
+  DepthArgs g{};
+  g.w_gate = e->d_gate; g.w_up = e->d_up; g.w_down = e->d_down; g.hidden = e->hidden;
+  g.norm_w = e->d_norm_in; g.eps = c.depth_eps; g.ptab = e->ptab; g.y = e->ybuf; g.scale = c.frame_scale;
+  return g;
+}
+// G_1 = W_gu (w_in * hidden) of the code-table path into gbuf[0], where
+// codebook 0's step reads it: after a prefill and at capture (a frame
+// computes it for the next one at its end).
+hipError_t launch_g1(sk_engine* e) {
+  DepthArgs g = depth_args(e);
+  g.g_out = e->gbuf[0];
+  SampleArgs s{};
+  return launch_depth_step<0>(e->c.weight_dtype, e->c.d_model, s, g, 0, e->stream);
+}
+
 hipError_t enqueue_frame(sk_engine* e) {
   const sk_config& c = e->c;
   const int d = c.d_model, M = e->rows, V = c.audio_vocab;
@@ -710,13 +729,9 @@ hipError_t enqueue_frame(sk_engine* e) {
   // (codebook q-1's sampler, the prefix, SwiGLU, down projection and the next
   // step's G) and the classifier; codebook 0 takes G_1, then SwiGLU + down.
   if (e->code_tables) {
-    DepthArgs g{};
-    g.w_gate = e->d_gate; g.w_up = e->d_up; g.w_down = e->d_down; g.hidden = e->hidden;
-    g.norm_w = e->d_norm_in; g.eps = c.depth_eps; g.ptab = e->ptab; g.y = e->ybuf; g.scale = c.frame_scale;
+    DepthArgs g = depth_args(e);
     for (int q = 0; q < c.n_codebooks; ++q) {
-      if (q == 0) {
-        g.g_out = e->gbuf[0];
-        if ((err = launch_depth_step<0>(wt, d, s, g, 0, e->stream)) != hipSuccess) return err;
+      if (q == 0) {   // G_1 is in gbuf[0]: from the previous frame's end, the prefill or the capture
         g.g_in = e->gbuf[0];
         if ((err = launch_depth_step<1>(wt, d, s, g, 0, e->stream)) != hipSuccess) return err;
       } else {
@@ -816,6 +831,22 @@ hipError_t enqueue_tail(sk_engine* e) {
   const int d = c.d_model, M = e->rows;
   hipError_t err;
   if ((err = enqueue_trunk(e)) != hipSuccess) return err;
+  if (e->code_tables) {   // final norm, bookkeeping and the next frame's G_1 in one launch
+    DepthArgs g = depth_args(e);
+    g.g_out = e->gbuf[0];
+    g.xfix = e->lx ? reinterpret_cast<const long long*>(lx_acc(e, 2 * c.n_layers)) : nullptr;
+    g.xf32 = e->x;
+    g.fix_clear = e->lx ? lx_acc(e, 1) : nullptr;
+    g.fnorm_w = e->final_norm; g.fnorm_eps = c.trunk_eps; g.hidden_out = e->hidden;
+    g.kv_len = e->kv_len; g.pos = e->pos; g.active = e->active; g.counter = e->fc;
+    g.u_ring = e->u_ring; g.flag_ring = e->flag_ring; g.u_cur = e->u_cur; g.flag_cur = e->flag_cur;
+    g.nq = c.n_utts * c.n_codebooks; g.max_frames = c.max_frames;
+    g.inv_freq = e->inv_freq; g.half = c.head_dim / 2; g.rope = e->rope;
+    g.rope_tab = (const float2*)e->p_rope; g.tab_n = c.max_ctx + 1;
+    SampleArgs s{};
+    return e->lx ? launch_depth_step<4>(c.weight_dtype, d, s, g, 0, e->stream)    // fixed-point trunk output
+                 : launch_depth_step<5>(c.weight_dtype, d, s, g, 0, e->stream);   // FP32 trunk output
+  }
   hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(NT), 0, e->stream, e->x,
                      e->lx ? reinterpret_cast<const long long*>(lx_acc(e, 2 * c.n_layers)) : nullptr,
                      e->lx ? lx_acc(e, 1) : nullptr, e->final_norm,
@@ -968,7 +999,9 @@ hipError_t enqueue_batched_prefill(sk_engine* e, int M, int max_len, const Prefi
   hipLaunchKernelGGL(pf_finish_kernel, dim3(e->rows), dim3(NT), 0, st, b.X, e->p_row_start, e->plen,
                      e->final_norm, c.trunk_eps, d, e->hidden, e->kv_len, e->pos, e->active, e->inv_freq, hd / 2,
                      e->rope, e->d_norm_in, c.depth_eps, e->abuf, e->xs_abuf);
-  return hipGetLastError();
+  const hipError_t fe = hipGetLastError();
+  if (fe != hipSuccess || !e->code_tables) return fe;
+  return launch_g1(e);
 }
 
 int capture(sk_engine* e, hipError_t (*body)(sk_engine*), hipGraph_t* g, hipGraphExec_t* x) {
@@ -1504,6 +1537,7 @@ int sk_capture(sk_engine* e) {
                    code_tables_fit(e->c.d_model, e->rows, e->c.depth_inner, e->c.audio_vocab, e->c.weight_dtype);
   e->wide_tables = e->wide && e->c.depth_inner <= SNT * DEPTH_API && e->c.d_model <= SNT * DEPTH_DPT;
   if ((e->code_tables || e->wide_tables) && (rc = build_code_tables(e)) != SK_OK) return rc;
+  if (e->code_tables && e->prefilled) SK_HIP(launch_g1(e));   // a prefill before the capture did not compute G_1
   rc = capture(e, enqueue_frame, &e->graph, &e->exec);
   if (rc != SK_OK) return rc;
   const hipError_t fe = find_attn_nodes(e);

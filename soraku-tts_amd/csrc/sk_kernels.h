@@ -2497,6 +2497,13 @@ __device__ __forceinline__ float wave_reduce_words(float (&w)[N], int lane) {
   return x;
 }
 
+// RoPE (cos, sin) of position p for frequency fq: angle = fp32(p * fq), cos
+// and sin evaluated in double and rounded once (modeling_qwen3.py:116-122).
+__device__ __forceinline__ float2 rope_cs(int p, float fq) {
+  const float ang = (float)p * fq;
+  return make_float2((float)cos((double)ang), (float)sin((double)ang));
+}
+
 // ------------------------------------------------------------ depth step (code tables)
 // One utterance's depth step with the SwiGLU input taken apart by linearity.
 // The gate/up input of codebook q is a_q = w_in * x_q * r_q, with x_q = hidden +
@@ -2527,6 +2534,14 @@ __device__ __forceinline__ float wave_reduce_words(float (&w)[N], int lane) {
 //   MODE 2: codebooks 1 .. Q-2: sampler of q-1, prefix, act_q, y_q, and
 //           G_{q+1} = G_q + scale P_{q-1}[c] (workgroup 0 stores it).
 //   MODE 3: codebook Q-1: as MODE 2 without G_{q+1}.
+//   MODE 4, 5: the frame's end: the trunk's final RMSNorm of each active row
+//           (hidden, written by workgroup 0) from its fixed-point (4) or FP32
+//           (5) output, then MODE 0 on it -- G_1 of the next frame -- and the
+//           rows' step bookkeeping (lengths, positions, RoPE entries, frame
+//           counter, the next frame's draws and flags), so the next frame
+//           starts at codebook 0's SwiGLU.  (A final-norm launch of its own and
+//           MODE 0 at the next frame's start were two launches; G_1 needs the
+//           whole normed row in every workgroup anyway.)
 struct DepthArgs {
   const void* w_gate; const void* w_up;    // [KI][KD]
   const void* w_down;                      // [KD][KI]
@@ -2538,6 +2553,15 @@ struct DepthArgs {
   const float* ptab;                       // [Q-1][V][2 KI] code tables, MODE 2 and 3
   float* y;                                // [M][KD] depth MLP output, MODE 1-3
   float scale;                             // frame scale 1/sqrt(Q)
+  // MODE 4, 5: the trunk's last output, fixed point (xfix, 2^-32 units, MODE
+  // 4) or FP32 (xf32, MODE 5); the accumulator whose active rows are zeroed (fix_clear); the
+  // final norm; hidden (written for active rows; inactive rows keep theirs);
+  // the bookkeeping buffers, as final_norm_kernel's.
+  const long long* xfix; const float* xf32; unsigned long long* fix_clear;
+  const float* fnorm_w; float fnorm_eps; float* hidden_out;
+  int* kv_len; int* pos; const int* active; int* counter;
+  const double* u_ring; const int* flag_ring; double* u_cur; int* flag_cur; int nq; int max_frames;
+  const float* inv_freq; int half; float2* rope; const float2* rope_tab; int tab_n;
 };
 constexpr int DEPTH_WGS = 256;
 
@@ -2547,7 +2571,8 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
   double* W = reinterpret_cast<double*>(raw);
   unsigned long long* ck = reinterpret_cast<unsigned long long*>(W + a.V);
   unsigned long long* sk = ck + pow2_ceil(a.V);
-  constexpr bool SAMPLE = MODE >= 2, GPART = MODE == 0, DPART = MODE >= 1;
+  constexpr bool SAMPLE = MODE == 2 || MODE == 3, GPART = MODE == 0 || MODE >= 4;
+  constexpr bool DPART = MODE >= 1 && MODE <= 3, TAIL = MODE >= 4, TFIX = MODE == 4;
   constexpr int VEC = TL::VEC;
   constexpr int NV = KD / (64 * VEC);           // 16-byte loads per lane of one W_gu row
   constexpr int DPT = KD / SNT;                 // elements of x per thread
@@ -2588,14 +2613,43 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
     P = *a.params;
   }
   float hv[M][DPT], pv[M][DPT], gv[DPT];
+  // MODE 4, 5: the trunk's output rows (hv: fixed point in MODE 4, FP32 in
+  // MODE 5), the final norm's gain (fw) and the rows' current hidden (kept by
+  // inactive rows, in pv) -- loaded without branches, so they go out as one
+  // batch ahead of the weight stream.
+  float fw[TAIL ? DPT : 1];
+  int act[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) act[m] = TAIL ? g.active[m] : 1;
+  // ... and the step bookkeeping's independent inputs (every workgroup loads
+  // them at clamped indices, only workgroup 0 uses them): thread t < M the
+  // row's length and position, t < M * half the position of its RoPE row,
+  // the frame counter.  The loads that depend on them (the RoPE table entry,
+  // the next frame's draws and flags) follow the weight stream.
+  int bk_kv = 0, bk_pos = 0, bk_cnt = 0, rp_row = 0, rp_t = 0, rp_pos = 0, rp_act = 0;
+  if constexpr (TAIL) {
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    bk_cnt = g.counter[zero];
+    const int rb = min(tid, M - 1);
+    bk_kv = g.kv_len[rb];
+    bk_pos = g.pos[rb];
+    rp_row = min(tid / g.half, M - 1);
+    rp_t = min(tid - rp_row * g.half, g.half - 1);
+    rp_pos = g.pos[rp_row] + 1;
+    rp_act = g.active[rp_row];
+  }
 #pragma unroll
   for (int i = 0; i < DPT; ++i) {
     const int k = tid + i * SNT;
     gv[i] = g.norm_w[k];
+    if constexpr (TAIL) fw[i] = g.fnorm_w[k];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      hv[m][i] = g.hidden[(size_t)m * KD + k];
-      pv[m][i] = SAMPLE ? g.prefix_in[(size_t)m * KD + k] : 0.f;
+      if constexpr (TFIX) hv[m][i] = (float)g.xfix[(size_t)m * KD + k] * 0x1p-32f;
+      else if constexpr (TAIL) hv[m][i] = g.xf32[(size_t)m * KD + k];
+      else hv[m][i] = g.hidden[(size_t)m * KD + k];
+      pv[m][i] = TAIL ? g.hidden[(size_t)m * KD + k] : SAMPLE ? g.prefix_in[(size_t)m * KD + k] : 0.f;
     }
   }
   // G_q at this lane's inner indices of its wave's chunk (gate and up): at
@@ -2642,6 +2696,17 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
     for (int i = 0; i < RD; ++i) wd[i] = TL::raw(g.w_down, (size_t)(row0 + i) * KI + kc);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // MODE 4, 5: the bookkeeping loads that depend on a position or the frame
+  // counter, behind the weights (their inputs were loaded ahead of them)
+  double bk_u = 0.0;
+  int bk_flag = 0;
+  float2 bk_rp = make_float2(0.f, 0.f);
+  if constexpr (TAIL) {
+    bk_rp = g.rope_tab[(size_t)min(rp_pos, g.tab_n - 1) * g.half + rp_t];
+    const int nx = min(bk_cnt + 1, g.max_frames - 1);
+    bk_u = g.u_ring[(size_t)nx * g.nq + min(tid, g.nq - 1)];
+    bk_flag = g.flag_ring[2 * nx + min(tid, 1)];
+  }
   // The ring slot and the forced code as scalar loads behind the weights: a
   // vector load here would be waited for behind the whole weight stream, and
   // ahead of the weights its address chain held them back.
@@ -2692,6 +2757,45 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
         const float4 t = *reinterpret_cast<const float4*>(pp + h * KI + i);
         pr[h][i] = t.x; pr[h][i + 1] = t.y; pr[h][i + 2] = t.z; pr[h][i + 3] = t.w;
       }
+  }
+
+  // MODE 4, 5: hidden = final_norm(trunk output) for active rows (the same
+  // form as final_norm_kernel, w * (x * (1 / sqrt(mean(x^2) + eps)))); the
+  // inactive rows keep their hidden.  Workgroup 0 stores it; every
+  // workgroup zeroes its share of the accumulator the next frame's first
+  // trunk launch adds into (a different buffer from xfix).
+  if constexpr (TAIL) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) ss = fmaf(hv[m][i], hv[m][i], ss);
+      ss = wave_sum_dpp(ss);
+      if (lane == 0) red[m][wave] = ss;
+    }
+    sk_sync();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < SWAVES; ++w) t += red[m][w];
+      const float invf = 1.0f / sqrtf(t / (float)KD + g.fnorm_eps);
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) {
+        const float h = fw[i] * (hv[m][i] * invf);
+        hv[m][i] = act[m] ? h : pv[m][i];
+        pv[m][i] = 0.f;
+        if (lead && act[m]) g.hidden_out[(size_t)m * KD + tid + i * SNT] = h;
+      }
+    }
+    if (g.fix_clear) {
+      constexpr int CPW = M * KD / DEPTH_WGS;   // accumulator entries per workgroup
+      if (tid < CPW) {
+        const int e = blockIdx.x * CPW + tid, m = e / KD;
+        if (act[m]) g.fix_clear[e] = 0ull;
+      }
+    }
+    sk_sync();   // red is reused below
   }
 
   // x = hidden + (prefix + table row * scale), in the oracle's order; r = 1/rms(x)
@@ -2775,6 +2879,22 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
     if (lane % (64 / NG) == 0) {
       const int word = lane / (64 / NG), m = word % M, h = (word / M) % 2, r = word / (2 * M);
       g.g_out[(size_t)m * 2 * KI + h * KI + n0 + r] = tot;
+    }
+  }
+  // MODE 4, 5, workgroup 0: the step bookkeeping from the values loaded
+  // above (every read of them came before these writes: the barriers above
+  // separate them).
+  if constexpr (TAIL) {
+    if (lead) {
+      if (tid < M && act[tid]) { g.kv_len[tid] = bk_kv + 1; g.pos[tid] = bk_pos + 1; }
+      if (tid < M * g.half && rp_act)
+        g.rope[(size_t)rp_row * g.half + rp_t] = rp_pos < g.tab_n ? bk_rp : rope_cs(rp_pos, g.inv_freq[rp_t]);
+      const int next = bk_cnt + 1;
+      if (tid == 0) *g.counter = next;
+      if (next < g.max_frames) {
+        if (tid < g.nq) g.u_cur[tid] = bk_u;
+        if (tid < 2) g.flag_cur[tid] = bk_flag;
+      }
     }
   }
 
@@ -2880,12 +3000,6 @@ __global__ __launch_bounds__(SNT) void sample_op_kernel(const float* logits, int
 constexpr size_t SAMPLE_SMEM = (size_t)MAX_V * sizeof(double) + (size_t)(MAX_V + FILTER_MAX) * 8;
 
 // ------------------------------------------------------------ small kernels
-// RoPE (cos, sin) of position p for frequency fq: angle = fp32(p * fq), cos
-// and sin evaluated in double and rounded once (modeling_qwen3.py:116-122).
-__device__ __forceinline__ float2 rope_cs(int p, float fq) {
-  const float ang = (float)p * fq;
-  return make_float2((float)cos((double)ang), (float)sin((double)ang));
-}
 
 // (cos, sin) table of rows row0 + blockIdx.x at their current positions.
 __global__ __launch_bounds__(NT) void rope_rows_kernel(const int* pos, const float* inv_freq, int half, int row0,

@@ -3,7 +3,7 @@
     python -m soraku_amd.prof_summary trace OUT/tr_results.db
         per-kernel table of the decode frames in a ``--kernel-trace`` run
         (dispatches after the last prefill kernel, frames delimited by the
-        trunk's ``final_norm_kernel``)
+        trunk's ``final_norm_kernel`` or the depth step that fuses it)
 
     python -m soraku_amd.prof_summary prefill OUT/tr_results.db
         per-kernel table of the first batched prefill in the same run
@@ -49,11 +49,17 @@ def short_name(name: str) -> str:
 PREFILL_MARKERS = ("prefill", "pf_", "gemm_nt_kernel")
 
 
+def _is_frame_end(n):
+    """The frame's last kernel: the trunk's final norm, or on the code-table
+    path the depth step that fuses it (``depth_step_kernel<..., 4>``)."""
+    return "final_norm_kernel" in n or (n.startswith("depth_step_kernel<") and n.replace(" ", "").endswith(",4>"))
+
+
 def _frames(names):
-    """Index ranges (a, b] of whole frames: between consecutive final norms
+    """Index ranges (a, b] of whole frames: between consecutive frame ends
     after the last prefill kernel."""
     last_pf = max((i for i, n in enumerate(names) if any(m in n for m in PREFILL_MARKERS)), default=-1)
-    marks = [i for i, n in enumerate(names) if i > last_pf and "final_norm_kernel" in n]
+    marks = [i for i, n in enumerate(names) if i > last_pf and _is_frame_end(n)]
     return list(zip(marks[:-1], marks[1:]))
 
 

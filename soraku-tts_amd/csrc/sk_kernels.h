@@ -1912,15 +1912,18 @@ __device__ __forceinline__ int sample_core(const float (&xr)[VPT], int V, float 
 // (the utterance) of *mask_flag is set.  The merged row is optionally recorded, then kept in
 // registers divided by the temperature when sampling (model.py:696).  Loads
 // are clamped into the row and entries past V become -inf afterwards, so no
-// load sits behind a branch.
+// load sits behind a branch (without an uncond row the cond row is loaded
+// twice and the copy ignored: a load under `lu ?` made each one wait for the
+// one before).
 template <int VPT>
 __device__ __forceinline__ void load_logits(const float* lc, const float* lu, int V, float (&cvv)[VPT],
                                             float (&uvv)[VPT]) {
+  const float* lu2 = lu ? lu : lc;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int v = min((int)threadIdx.x + i * SNT, V - 1);
     cvv[i] = lc[v];
-    uvv[i] = lu ? lu[v] : 0.f;
+    uvv[i] = lu2[v];
   }
 }
 template <int VPT>
@@ -2155,7 +2158,13 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   const int slot = *a.fc;
   const SkParams P = *a.params;
   const bool last = (q + 1 == a.Q);
-  if (last && threadIdx.x < a.Q && threadIdx.x != q)
+  // The last codebook's frame embedding: from the prefix the depth steps
+  // accumulated (prefix_last), else from the table rows of every code.
+  constexpr int EI = 4, EQ = 16;        // d <= EI * SNT, 2 <= Q <= EQ
+  const bool from_prefix = last && a.prefix_last != nullptr && a.d <= EI * SNT;
+  // The codes drawn so far, for the table rows: with prefix_last they are not
+  // needed, and the load (whose test makes the logits wait for it) is skipped.
+  if (last && !from_prefix && threadIdx.x < a.Q && threadIdx.x != q)
     codes_l[threadIdx.x] = a.codes_cur[(size_t)ut * a.Q + threadIdx.x];
   const bool q0 = (q == 0) && P.has_q0;
   const float temp = q0 ? P.temperature_q0 : P.temperature;
@@ -2168,8 +2177,6 @@ __global__ __launch_bounds__(SNT) void sample_step_kernel(SampleArgs a, int q) {
   // 0 .. Q-2 do not depend on the draw, so they are in flight during it
   // (issued once the logits are in, so the sampler does not wait for them).
   // With prefix_last the depth steps have summed them already.
-  constexpr int EI = 4, EQ = 16;        // d <= EI * SNT, 2 <= Q <= EQ
-  const bool from_prefix = last && a.prefix_last != nullptr && a.d <= EI * SNT;
   const bool early = last && !from_prefix && a.d <= EI * SNT && a.Q >= 2 && a.Q <= EQ;
   float pl[EI];
   if (from_prefix) {

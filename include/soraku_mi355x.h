@@ -173,7 +173,11 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
  * (uniforms [n][n_utts][Q], mask_eos_q0 [n] utterance bit masks as in
  * sk_step_frame), then replay `n` frames back to
  * back with no host synchronisation.  sk_read_codes copies codes of the
- * `n` most recent frames ([n][n_utts][Q]). */
+ * `n` most recent frames ([n][n_utts][Q]).
+ * Frames of different engines on one device run one after another: when the
+ * device's frames pass from one engine to another (sk_step_frame or
+ * sk_replay), the new engine's stream first waits for the work queued on the
+ * previous engine's stream.  An engine stepping alone pays nothing. */
 int sk_queue_frames(sk_engine* e, int32_t n, const double* uniforms, const int32_t* mask_eos_q0);
 int sk_replay(sk_engine* e, int32_t n);
 int sk_read_codes(sk_engine* e, int32_t n, int64_t* codes_out);

@@ -113,6 +113,7 @@ struct sk_engine {
   bool split_k = false;       // many-row BF16 GEMMs may split K (workgroups i, i + 8, ... share an XCD)
   int device = 0;
   hipStream_t stream = nullptr;
+  hipEvent_t order_ev = nullptr;   // recorded on `stream` when another engine's frames follow this one's
 
   // weights (borrowed)
   std::vector<LayerW> L;
@@ -1074,6 +1075,44 @@ extern "C" {
 
 const char* sk_last_error(void) { return last_error().c_str(); }
 
+// ---- frame order between engines on one device ------------------------------
+// Frames of different engines on one device run one after another.  The
+// XCD-resident layers and the tagged split-K merge wait inside a launch for
+// other workgroups of the same launch, so all of its workgroups must be
+// resident at once; another engine's frame running beside it would hold CUs
+// those workgroups need, and both would wait until their spin limits end the
+// frames with an error.  When a device's frames pass from one engine to
+// another, the new engine's stream first waits for everything the previous
+// engine had queued (an event recorded on that engine's stream at the
+// switch), so an engine that steps alone pays nothing.  The lock is held
+// while the frames are enqueued and while a graph is captured, so no event
+// is ever recorded on a stream that is capturing.
+namespace {
+struct FrameOrder {
+  std::mutex mu;
+  sk_engine* last = nullptr;   // the engine whose frames were enqueued last on this device
+};
+FrameOrder g_frame_order[MAX_DEVICES];
+}  // namespace
+
+// With g_frame_order[e->device].mu held, before e enqueues frames.
+static hipError_t order_after_previous(sk_engine* e) {
+  FrameOrder& fo = g_frame_order[e->device];
+  sk_engine* p = fo.last;
+  fo.last = e;
+  if (!p || p == e) return hipSuccess;
+  hipError_t err = hipEventRecord(p->order_ev, p->stream);
+  if (err == hipSuccess) err = hipStreamWaitEvent(e->stream, p->order_ev, 0);
+  return err;
+}
+
+static void leave_frame_order(sk_engine* e) {
+  if (!e->stream) return;   // never got as far as launching anything
+  FrameOrder& fo = g_frame_order[e->device];
+  std::lock_guard<std::mutex> lk(fo.mu);
+  if (fo.last == e) fo.last = nullptr;
+}
+
 int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   SK_CHECK(out != nullptr, SK_EINVAL, "out is NULL");
   *out = nullptr;
@@ -1120,6 +1159,10 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   }
   if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess) {
     fail(SK_EHIP, "hipStreamCreateWithFlags failed");
+    return bail(SK_EHIP);
+  }
+  if (hipEventCreateWithFlags(&e->order_ev, hipEventDisableTiming) != hipSuccess) {
+    fail(SK_EHIP, "hipEventCreateWithFlags failed");
     return bail(SK_EHIP);
   }
   const size_t R = e->rows, d = c.d_model, Q = c.n_codebooks, V = c.audio_vocab;
@@ -1240,6 +1283,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
 
 int sk_destroy(sk_engine* e) {
   if (!e) return SK_OK;
+  leave_frame_order(e);
   if (e->stream) hipStreamSynchronize(e->stream);
   drop_graphs(e);
   void* bufs[] = {e->sk_partial, e->sk_arrive, e->sk_tpart, e->sk_err, e->xs_x, e->xs_attn, e->xs_act, e->xs_abuf, e->xs_y, e->ss_x, e->ss_y, e->x, e->hidden, e->prefix, e->prefix2, e->abuf, e->ybuf, e->qkv, e->attn, e->act, e->logits,
@@ -1252,6 +1296,7 @@ int sk_destroy(sk_engine* e) {
                   e->forced_ring, e->codes_ring, e->stage_ids, e->stage_codes, e->params};
   for (void* p : bufs)
     if (p) hipFree(p);
+  if (e->order_ev) hipEventDestroy(e->order_ev);
   if (e->stream) hipStreamDestroy(e->stream);
   delete e;
   return SK_OK;
@@ -1538,7 +1583,10 @@ int sk_capture(sk_engine* e) {
   e->wide_tables = e->wide && e->c.depth_inner <= SNT * DEPTH_API && e->c.d_model <= SNT * DEPTH_DPT;
   if ((e->code_tables || e->wide_tables) && (rc = build_code_tables(e)) != SK_OK) return rc;
   if (e->code_tables && e->prefilled) SK_HIP(launch_g1(e));   // a prefill before the capture did not compute G_1
-  rc = capture(e, enqueue_frame, &e->graph, &e->exec);
+  {
+    std::lock_guard<std::mutex> lk(g_frame_order[e->device].mu);
+    rc = capture(e, enqueue_frame, &e->graph, &e->exec);
+  }
   if (rc != SK_OK) return rc;
   const hipError_t fe = find_attn_nodes(e);
   if (fe != hipSuccess) {
@@ -1599,8 +1647,12 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
   if (forced_codes)
     SK_HIP(hipMemcpyAsync(e->forced_ring + slot * nq, forced_codes, nq * sizeof(int64_t), hipMemcpyHostToDevice,
                           e->stream));
-  SK_HIP(set_frame_chunks(e, 0));
-  SK_HIP(hipGraphLaunch(e->exec, e->stream));
+  {
+    std::lock_guard<std::mutex> lk(g_frame_order[e->device].mu);
+    SK_HIP(order_after_previous(e));
+    SK_HIP(set_frame_chunks(e, 0));
+    SK_HIP(hipGraphLaunch(e->exec, e->stream));
+  }
   SK_HIP(hipMemcpyAsync(codes_out, e->codes_ring + slot * nq, nq * sizeof(int64_t), hipMemcpyDeviceToHost, e->stream));
   if (logits_dbg)
     SK_HIP(hipMemcpyAsync(logits_dbg, e->dbg, nq * c.audio_vocab * sizeof(float), hipMemcpyDeviceToHost, e->stream));
@@ -1635,9 +1687,13 @@ int sk_queue_frames(sk_engine* e, int32_t n, const double* uniforms, const int32
 int sk_replay(sk_engine* e, int32_t n) {
   int rc = check_step(e, n);
   if (rc != SK_OK) return rc;
-  for (int i = 0; i < n; ++i) {
-    SK_HIP(set_frame_chunks(e, i));
-    SK_HIP(hipGraphLaunch(e->exec, e->stream));
+  {
+    std::lock_guard<std::mutex> lk(g_frame_order[e->device].mu);
+    SK_HIP(order_after_previous(e));
+    for (int i = 0; i < n; ++i) {
+      SK_HIP(set_frame_chunks(e, i));
+      SK_HIP(hipGraphLaunch(e->exec, e->stream));
+    }
   }
   e->fc_host += n;
   for (int r = 0; r < e->rows; ++r) e->kv_host[r] += n * e->active_host[r];

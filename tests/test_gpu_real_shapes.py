@@ -412,6 +412,48 @@ def test_barrier_timeout_reports_error_and_fresh_engine_decodes(hip_device):
     assert rel < LOGIT_TOL
 
 
+def test_two_engines_take_turns_on_one_gpu(hip_device):
+    """Two engines with XCD-resident layers on one GPU, each on its own
+    stream, replaying queued frames in turns with no host sync between them.
+    Each launch's barriers need all of its workgroups resident; the device's
+    frame order makes each engine's frames wait for the other's, so no
+    barrier times out, and each engine's codes equal those it decodes alone
+    (replays are bitwise deterministic)."""
+    f, s, gen = load_golden("q06b_sampled")
+    w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                          bias_std=float(f["bias_std"]))
+    text, uncond, prompt = _c3_inputs(f)
+    g = {k: gen[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
+    n = 8
+    u = [np.random.default_rng(11 + i).random((n, s.n_codebooks)) for i in range(2)]
+    mask = np.ones(n, np.int32)
+    prompts = [prompt, prompt[:100]]   # 241 / 197 cond positions
+
+    def make(i):
+        e = _engine(s, w, hip_device, text, uncond, prompts[i], 260, **g)
+        assert e.xcd_layers
+        e.queue_frames(u[i], mask)
+        return e
+
+    alone = []
+    for i in range(2):
+        e = make(i)
+        e.replay(n)
+        alone.append(e.read_codes(n))
+        e.close()
+    engines = [make(0), make(1)]
+    for _ in range(0, n, 2):
+        for e in engines:
+            e.replay(2)
+    got = [e.read_codes(n) for e in engines]
+    for e in engines:
+        e.close()
+    print("codes alone:", [a[:2, 0, :4].tolist() for a in alone], flush=True)
+    for i in range(2):
+        np.testing.assert_array_equal(got[i], alone[i])
+    assert not np.array_equal(alone[0], alone[1])
+
+
 def test_untied_head_through_model_binding(hip_device):
     """GraphFrameEngine(model) with a SorakuTTSv2-like module whose config has
     tie_audio_head=False binds depth_head.out_proj as the classifier

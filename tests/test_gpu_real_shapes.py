@@ -13,6 +13,8 @@ reference's vectors and the oracle.
 * The XCD-resident trunk layers (the path these two-row engines take)
   against the per-op layer kernels, at both shapes, and with more chunk slots
   than an XCD has workgroups.
+* Two engines with XCD-resident layers taking turns on one GPU (queued
+  replays on two streams, no host sync): codes equal each engine's alone.
 * An untied classifier head bound through ``GraphFrameEngine(model=...)``.
 
 Tolerance: logits within 1e-3 of the reference / oracle, relative to the

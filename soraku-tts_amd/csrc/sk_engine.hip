@@ -135,6 +135,7 @@ struct sk_engine {
   float* sk_partial = nullptr;  // many-row path: split-K slice partials
   unsigned* sk_arrive = nullptr;
   unsigned long long* sk_tpart = nullptr;   // split-K partials as tagged words
+  size_t sk_tpart_bytes = 0;
   unsigned* sk_err = nullptr;              // bit 1: a split-K merge wait timed out
   int sk_tags = 0;                         // GEMM launches enqueued so far in the frame
   // Many-row path with BF16 weights: GEMM inputs in split form (written by
@@ -1180,6 +1181,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
     ALLOC(e->sk_partial, (nmax / 16 + 1) * 4 * SK_PSZ);
     ALLOC(e->sk_arrive, nmax / 16 + 1);
     ALLOC(e->sk_tpart, (nmax / 16 + 1) * SK_MAX_SPLIT * SK_PSZ);
+    e->sk_tpart_bytes = (nmax / 16 + 1) * SK_MAX_SPLIT * SK_PSZ * sizeof(unsigned long long);
     ALLOC(e->sk_err, 1);
   }
   ALLOC(e->part, R * c.n_q_heads * e->max_chunks * part_stride(c.head_dim));
@@ -1215,10 +1217,7 @@ int sk_create(const sk_config* cfg, void* hip_stream, sk_engine** out) {
   if (he == hipSuccess) he = hipMemset(e->prefix2, 0, R * d * sizeof(float));
   if (he == hipSuccess) he = hipMemset(e->kv_len, 0, R * sizeof(int));
   if (he == hipSuccess) he = hipMemset(e->sk_err, 0, sizeof(unsigned));
-  if (he == hipSuccess)   // tag 0 is never a launch's
-    he = hipMemset(e->sk_tpart, 0,
-                   (std::max({(size_t)e->nqkv, (size_t)c.trunk_inter, (size_t)c.depth_inner, (size_t)c.audio_vocab,
-                              (size_t)c.d_model}) / 16 + 1) * SK_MAX_SPLIT * SK_PSZ * sizeof(unsigned long long));
+  if (he == hipSuccess) he = hipMemset(e->sk_tpart, 0, e->sk_tpart_bytes);   // tag 0 is never a launch's
   if (he == hipSuccess)
     he = hipMemset(e->sk_arrive, 0,
                    (std::max({(size_t)e->nqkv, (size_t)c.trunk_inter, (size_t)c.depth_inner, (size_t)c.audio_vocab,
@@ -1408,6 +1407,15 @@ int sk_prefill_row(sk_engine* e, int32_t row, const int64_t* text_ids, int32_t n
 // rows are touched -- the other rows' caches, lengths and hidden states and
 // the frame counter stay as they are (unstaged rows get length 0 here, which
 // every prefill kernel skips).
+// The split-K merge's tagged words carry frame counter * 256 + launch + 1.
+// Where the frame counter restarts at 0, a word an earlier run's frame left
+// could carry the tag a launch of the new run waits for (slice 0 would then
+// take a stale partial): the words are cleared there, since tag 0 is never a
+// launch's.
+static hipError_t clear_split_tags(sk_engine* e) {
+  return e->wide ? hipMemsetAsync(e->sk_tpart, 0, e->sk_tpart_bytes, e->stream) : hipSuccess;
+}
+
 static int prefill_staged(sk_engine* e, bool all, bool noalloc) {
   const int R = e->rows;
   int n_staged = 0;
@@ -1448,6 +1456,7 @@ static int prefill_staged(sk_engine* e, bool all, bool noalloc) {
   SK_HIP(hipMemcpyAsync(bufs.tok_pos, tok_pos.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
   if (all) {
     SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
+    SK_HIP(clear_split_tags(e));
     SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
     SK_HIP(hipMemsetAsync(e->prefix2, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
   }
@@ -1494,6 +1503,7 @@ int sk_retire_row(sk_engine* e, int32_t row) {
 int sk_reset_frames(sk_engine* e) {
   SK_CHECK(e != nullptr, SK_EINVAL, "engine is NULL");
   SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
+  SK_HIP(clear_split_tags(e));
   SK_HIP(hipStreamSynchronize(e->stream));
   e->fc_host = 0;
   return SK_OK;

@@ -41,7 +41,8 @@ struct SkinnyArgs {
   // slice 0 reads them until every tag is this launch's, *fc * 256 + tag_idx
   // + 1 (fc: the frame counter, constant over a frame; tag_idx: the launch's
   // place among the frame's GEMM launches), so a word left by an earlier
-  // launch never carries it.  A wait past `spin` ticks sets err bit 1.
+  // launch never carries it (the host clears the words wherever the frame
+  // counter restarts at 0).  A wait past `spin` ticks sets err bit 1.
   unsigned long long* tpart;           // [tiles][SK_MAX_SPLIT][SK_PSZ]
   const int* fc; int tag_idx;
   unsigned* err; unsigned long long spin;

@@ -656,6 +656,54 @@ def test_split_k_wait_timeout_reports_error_and_fresh_engine_decodes(hip_device)
     assert rel < LOGIT_TOL
 
 
+def test_split_k_tags_after_frame_counter_restart(hip_device):
+    """The split-K merge's tags repeat once the frame counter restarts at 0 (a
+    new prefill).  An engine (three utterances x CFG, Qwen3-0.6B shape, BF16
+    weights: the skinny GEMMs with split-K) decodes one frame, so the tagged
+    words hold frame 0's tags, then prefills other utterances and decodes
+    three frames: its codes and logits equal, bit for bit, those of a fresh
+    engine that decodes the second set alone."""
+    import dataclasses
+
+    from oracle.model import QWEN3_06B
+    from soraku_amd import GraphFrameEngine
+
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)
+    w = _device_weights(s, 29, hip_device)
+    rng = np.random.default_rng(29)
+
+    def items():
+        return [(rng.integers(0, s.text_vocab, 10 + 3 * i), np.array([7]),
+                 rng.integers(0, s.codebook_size, (2 + i, s.n_codebooks))) for i in range(3)]
+
+    first, second = items(), items()
+    u = np.zeros(3 * s.n_codebooks)
+
+    def make(its):
+        e = GraphFrameEngine(device=hip_device, max_cache_len=64, cfg_scale=1.5, batch=2, state_dict=w,
+                             shape=_shape(s), n_utts=3, bf16=True)
+        e.set_temperature(0.0)
+        e.set_debug(True)
+        e.prefill_utterances(its)
+        e.capture()
+        return e
+
+    def decode(e, n):
+        out = [e.step_frame(mask_eos_q0=True, uniforms=u, return_logits=True) for _ in range(n)]
+        return np.stack([c.numpy() for c, _ in out]), np.stack([lg for _, lg in out])
+
+    e = make(first)
+    decode(e, 1)
+    e.prefill_utterances(second)
+    got = decode(e, 3)
+    e.close()
+    e = make(second)
+    want = decode(e, 3)
+    e.close()
+    np.testing.assert_array_equal(got[0], want[0])
+    np.testing.assert_array_equal(got[1], want[1])
+
+
 def test_sixteen_utterances_q06b_bf16_kv(hip_device):
     """The throughput batch's precision: 16 utterances x CFG at the
     Qwen3-0.6B shape with BF16 weights and a BF16 KV cache (the streaming

@@ -505,8 +505,12 @@ hipError_t launch_attn_stream(sk_engine* e, const AttnArgs& at) {
 bool lx_fits(const sk_engine* e) {
   const sk_config& c = e->c;
   const bool shape = (c.d_model == 1024 && c.trunk_inter == 3072) || (c.d_model == 2048 && c.trunk_inter == 6144);
+  // n_layers % 3 == 2 would leave the trunk's output in accumulator 1, the
+  // next frame's first-layer target, which the frame's last launch must zero
+  // after every workgroup has read the whole output: one kernel cannot order
+  // that, so such trunks keep the five-kernel layers.
   return e->rows == LX_M && !e->wide && e->attn_splits == 0 && c.n_kv_heads == LX_HKV && c.n_q_heads == LX_HQ &&
-         c.head_dim == LX_HD && shape && e->max_chunks <= LX_MAXCH;
+         c.head_dim == LX_HD && shape && e->max_chunks <= LX_MAXCH && c.n_layers % 3 != 2;
 }
 
 template <typename WL, typename KT>

@@ -2561,7 +2561,7 @@ struct DepthArgs {
   float* y;                                // [M][KD] depth MLP output, MODE 1-3
   float scale;                             // frame scale 1/sqrt(Q)
   // MODE 4, 5: the trunk's last output, fixed point (xfix, 2^-32 units, MODE
-  // 4) or FP32 (xf32, MODE 5); the accumulator whose active rows are zeroed (fix_clear); the
+  // 4) or FP32 (xf32, MODE 5); the accumulator that is zeroed, every row (fix_clear); the
   // final norm; hidden (written for active rows; inactive rows keep theirs);
   // the bookkeeping buffers, as final_norm_kernel's.
   const long long* xfix; const float* xf32; unsigned long long* fix_clear;
@@ -2798,8 +2798,7 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
     if (g.fix_clear) {
       constexpr int CPW = M * KD / DEPTH_WGS;   // accumulator entries per workgroup
       if (tid < CPW) {
-        const int e = blockIdx.x * CPW + tid, m = e / KD;
-        if (act[m]) g.fix_clear[e] = 0ull;
+        g.fix_clear[blockIdx.x * CPW + tid] = 0ull;   // every row: a refill may make a retired row active again
       }
     }
     sk_sync();   // red is reused below
@@ -3024,7 +3023,9 @@ __global__ __launch_bounds__(NT) void rope_rows_kernel(const int* pos, const flo
 // zero when a frame starts), and its split form when xs_abuf is set.  With
 // xfix set the input row is the XCD-resident layers' fixed-point residual
 // stream [rows][D] (2^-32 units) instead of x, and fix_clear (set with it) is
-// the accumulator whose row this workgroup zeroes once the input is read.
+// the accumulator whose row this workgroup zeroes (an active row once the
+// input is read, a retired row at once: the next frame's first layer adds
+// into it for every row, and a refill may make the row active again).
 __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const long long* xfix,
                                                         unsigned long long* fix_clear, const float* w, float eps,
                                                         int D, float* hidden, int* kv_len, int* pos,
@@ -3067,6 +3068,8 @@ __global__ __launch_bounds__(NT) void final_norm_kernel(const float* x, const lo
     f0 = flag_ring[2 * nx + min(tx, 1)];
   };
   if (!act) book();
+  if (!act && fix_clear)   // a retired row's entries too: a refill may make it active again
+    for (int i = tx; i < D; i += NT) fix_clear[(size_t)b * D + i] = 0ull;
   if (act) {
     const float* xr = x + (size_t)b * D;
     const size_t ro = (size_t)b * D;

@@ -456,6 +456,43 @@ def test_two_engines_take_turns_on_one_gpu(hip_device):
     assert not np.array_equal(alone[0], alone[1])
 
 
+def test_xcd_layers_frame_with_retired_rows_then_prefill(hip_device):
+    """The XCD-resident layers' residual accumulators across a retired
+    utterance: an engine decodes one frame, retires its utterance, runs one
+    frame with both rows retired (the next frame's first-layer accumulator
+    must still be cleared for them), then prefills the C3 prefix again; its
+    teacher-forced frames then equal a fresh engine's (same codes, logits
+    within 1e-6 of the fresh engine's and within 1e-3 of the reference)."""
+    f, s, gen = load_golden("q06b_sampled")
+    w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                          bias_std=float(f["bias_std"]))
+    text, uncond, prompt = _c3_inputs(f)
+    g = {k: gen[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
+    z = np.zeros(s.n_codebooks)
+
+    def frames(e, n):
+        out = [e.step_frame(mask_eos_q0=True, uniforms=z, forced_codes=f["codes"][i], return_logits=True)
+               for i in range(n)]
+        return np.stack([c.numpy() for c, _ in out]), np.stack([lg[0] for _, lg in out])
+
+    e = _engine(s, w, hip_device, text, uncond, prompt[:100], 270, **g)
+    assert e.xcd_layers
+    frames(e, 1)
+    e.retire(0)
+    e.step_frame(mask_eos_q0=True, uniforms=z)
+    e.prefill(text, uncond, prompt)
+    got = frames(e, 2)
+    e.close()
+    e = _engine(s, w, hip_device, text, uncond, prompt, 270, **g)
+    want = frames(e, 2)
+    e.close()
+    np.testing.assert_array_equal(got[0], want[0])
+    rel = _rowwise_rel(got[1].reshape(-1, got[1].shape[-1]), want[1].reshape(-1, want[1].shape[-1]))
+    ref = _rowwise_rel(got[1].reshape(-1, got[1].shape[-1]), f["sample_logits"][: 2 * s.n_codebooks])
+    print(f"after a frame with retired rows and a new prefill: vs fresh engine {rel:.3e}, vs reference {ref:.3e}")
+    assert rel < 1e-6 and ref < LOGIT_TOL
+
+
 def test_untied_head_through_model_binding(hip_device):
     """GraphFrameEngine(model) with a SorakuTTSv2-like module whose config has
     tie_audio_head=False binds depth_head.out_proj as the classifier

@@ -2538,9 +2538,9 @@ __device__ __forceinline__ float2 rope_cs(int p, float fq) {
 // sampler runs.
 //   MODE 0: G_1 = W_gu (w_in * hidden) only (x_0 = hidden; no sampler).
 //   MODE 1: codebook 0's SwiGLU + down: act_0 = SwiGLU(r_0 G_1), y_0.
-//   MODE 2: codebooks 1 .. Q-2: sampler of q-1, prefix, act_q, y_q, and
-//           G_{q+1} = G_q + scale P_{q-1}[c] (workgroup 0 stores it).
-//   MODE 3: codebook Q-1: as MODE 2 without G_{q+1}.
+//   MODE 2: codebooks 1 .. Q-1: sampler of q-1, prefix, act_q, y_q, and
+//           G_{q+1} = G_q + scale P_{q-1}[c] (workgroup 0 stores it; for
+//           codebook Q-1 into a buffer nothing reads before it is rewritten).
 //   MODE 4, 5: the frame's end: the trunk's final RMSNorm of each active row
 //           (hidden, written by workgroup 0) from its fixed-point (4) or FP32
 //           (5) output, then MODE 0 on it -- G_1 of the next frame -- and the
@@ -2553,12 +2553,12 @@ struct DepthArgs {
   const void* w_gate; const void* w_up;    // [KI][KD]
   const void* w_down;                      // [KD][KI]
   const float* hidden;                     // [M][KD]
-  const float* prefix_in; float* prefix_out;   // [M][KD] before / after code q-1 (MODE 2, 3)
+  const float* prefix_in; float* prefix_out;   // [M][KD] before / after code q-1 (MODE 2)
   const float* norm_w; float eps;          // norm_in gain [KD], FLT_EPSILON
-  const float* g_in;                       // [M][2 KI] G_q (gate | up), MODE 1-3
+  const float* g_in;                       // [M][2 KI] G_q (gate | up), MODE 1, 2
   float* g_out;                            // [M][2 KI] G_1 (MODE 0) or G_{q+1} (MODE 2)
-  const float* ptab;                       // [Q-1][V][2 KI] code tables, MODE 2 and 3
-  float* y;                                // [M][KD] depth MLP output, MODE 1-3
+  const float* ptab;                       // [Q-1][V][2 KI] code tables, MODE 2
+  float* y;                                // [M][KD] depth MLP output, MODE 1, 2
   float scale;                             // frame scale 1/sqrt(Q)
   // MODE 4, 5: the trunk's last output, fixed point (xfix, 2^-32 units, MODE
   // 4) or FP32 (xf32, MODE 5); the accumulator that is zeroed, every row (fix_clear); the
@@ -2578,8 +2578,8 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
   double* W = reinterpret_cast<double*>(raw);
   unsigned long long* ck = reinterpret_cast<unsigned long long*>(W + a.V);
   unsigned long long* sk = ck + pow2_ceil(a.V);
-  constexpr bool SAMPLE = MODE == 2 || MODE == 3, GPART = MODE == 0 || MODE >= 4;
-  constexpr bool DPART = MODE >= 1 && MODE <= 3, TAIL = MODE >= 4, TFIX = MODE == 4;
+  constexpr bool SAMPLE = MODE == 2, GPART = MODE == 0 || MODE >= 4;
+  constexpr bool DPART = MODE == 1 || MODE == 2, TAIL = MODE >= 4, TFIX = MODE == 4;
   constexpr int VEC = TL::VEC;
   constexpr int NV = KD / (64 * VEC);           // 16-byte loads per lane of one W_gu row
   constexpr int DPT = KD / SNT;                 // elements of x per thread
@@ -2594,7 +2594,7 @@ __global__ __launch_bounds__(SNT) void depth_step_kernel(SampleArgs a, DepthArgs
   __shared__ float dsum[SWAVES][RD][M];
   __shared__ int code_sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int qs = q - 1;                         // the codebook sampled here (MODE 2, 3)
+  const int qs = q - 1;                         // the codebook sampled here (MODE 2)
   const bool lead = blockIdx.x == 0;
 
   // Loads that do not depend on the code, before the weight stream: the

@@ -230,7 +230,7 @@ static inline bool code_tables_fit(int d, int rows, int depth_inner, int V, int 
 }
 template <typename TL, int KD, int KI, int MODE>
 static hipError_t launch_depth_step_t(const SampleArgs& s, const DepthArgs& g, int q, hipStream_t st) {
-  if constexpr (MODE == 2 || MODE == 3) {   // with a sampler
+  if constexpr (MODE == 2) {   // with a sampler
     return with_vpt(s.V, [&](auto vpt) {
       hipLaunchKernelGGL((depth_step_kernel<TL, decltype(vpt)::value, 2, KD, KI, MODE>), dim3(DEPTH_WGS), dim3(SNT),
                          depth_sample_smem(s.V), st, s, g, q);

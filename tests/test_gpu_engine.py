@@ -704,6 +704,46 @@ def test_split_k_tags_after_frame_counter_restart(hip_device):
     np.testing.assert_array_equal(got[1], want[1])
 
 
+def test_split_k_frames_after_ring_reset(hip_device):
+    """sk_reset_frames on the split-K path: the frame counter restarts at 0 while
+    the caches keep growing, so the frames after the reset reuse frame 0's
+    tags.  Three utterances x CFG (Qwen3-0.6B shape, BF16 weights): one frame,
+    a ring reset, two frames equal, bit for bit, frames 1 and 2 of an
+    uninterrupted run."""
+    import dataclasses
+
+    from oracle.model import QWEN3_06B
+    from soraku_amd import GraphFrameEngine
+
+    s = dataclasses.replace(QWEN3_06B, text_vocab=4096)
+    w = _device_weights(s, 31, hip_device)
+    rng = np.random.default_rng(31)
+    its = [(rng.integers(0, s.text_vocab, 9 + 4 * i), np.array([7]),
+            rng.integers(0, s.codebook_size, (1 + i, s.n_codebooks))) for i in range(3)]
+    u = np.zeros(3 * s.n_codebooks)
+
+    def run(reset):
+        e = GraphFrameEngine(device=hip_device, max_cache_len=64, cfg_scale=1.5, batch=2, state_dict=w,
+                             shape=_shape(s), n_utts=3, bf16=True)
+        e.set_temperature(0.0)
+        e.set_debug(True)
+        e.prefill_utterances(its)
+        e.capture()
+        out = []
+        for i in range(3):
+            if reset and i == 1:
+                e.reset_frames()
+            c, lg = e.step_frame(mask_eos_q0=True, uniforms=u, return_logits=True)
+            out.append((c.numpy(), lg))
+        e.close()
+        return out
+
+    plain, reset = run(False), run(True)
+    for i in (1, 2):
+        np.testing.assert_array_equal(reset[i][0], plain[i][0])
+        np.testing.assert_array_equal(reset[i][1], plain[i][1])
+
+
 def test_sixteen_utterances_q06b_bf16_kv(hip_device):
     """The throughput batch's precision: 16 utterances x CFG at the
     Qwen3-0.6B shape with BF16 weights and a BF16 KV cache (the streaming

@@ -15,6 +15,8 @@ reference's vectors and the oracle.
   than an XCD has workgroups.
 * Two engines with XCD-resident layers taking turns on one GPU (queued
   replays on two streams, no host sync): codes equal each engine's alone.
+* The XCD-resident layers after a frame with the utterance retired, then a
+  new prefill or a continuous-batching refill: equal to a fresh engine.
 * An untied classifier head bound through ``GraphFrameEngine(model=...)``.
 
 Tolerance: logits within 1e-3 of the reference / oracle, relative to the
@@ -490,6 +492,45 @@ def test_xcd_layers_frame_with_retired_rows_then_prefill(hip_device):
     rel = _rowwise_rel(got[1].reshape(-1, got[1].shape[-1]), want[1].reshape(-1, want[1].shape[-1]))
     ref = _rowwise_rel(got[1].reshape(-1, got[1].shape[-1]), f["sample_logits"][: 2 * s.n_codebooks])
     print(f"after a frame with retired rows and a new prefill: vs fresh engine {rel:.3e}, vs reference {ref:.3e}")
+    assert rel < 1e-6 and ref < LOGIT_TOL
+
+
+def test_xcd_layers_refill_after_retired_frame(hip_device):
+    """Continuous batching on the XCD-resident layers (one utterance slot):
+    decode one frame, retire the utterance, run one frame with the slot
+    retired, then refill the slot with the C3 prefix (the frame counter keeps
+    running).  Its teacher-forced frames equal a fresh engine's (same codes,
+    logits within 1e-6 of the fresh engine's and within 1e-3 of the
+    reference)."""
+    f, s, gen = load_golden("q06b_sampled")
+    w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                          bias_std=float(f["bias_std"]))
+    text, uncond, prompt = _c3_inputs(f)
+    g = {k: gen[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
+    z = np.zeros(s.n_codebooks)
+
+    def frames(e, n):
+        out = [e.step_frame(mask_eos_q0=True, uniforms=z, forced_codes=f["codes"][i], return_logits=True)
+               for i in range(n)]
+        return np.stack([c.numpy() for c, _ in out]), np.stack([lg[0] for _, lg in out])
+
+    e = _engine(s, w, hip_device, text, uncond, prompt[:60], 270, **g)
+    assert e.xcd_layers
+    frames(e, 1)
+    e.retire(0)
+    e.step_frame(mask_eos_q0=True, uniforms=z)
+    e.refill({0: (text, uncond, prompt)})
+    got = frames(e, 2)
+    assert e.frames_done == 4
+    e.close()
+    e = _engine(s, w, hip_device, text, uncond, prompt, 270, **g)
+    want = frames(e, 2)
+    e.close()
+    np.testing.assert_array_equal(got[0], want[0])
+    V = got[1].shape[-1]
+    rel = _rowwise_rel(got[1].reshape(-1, V), want[1].reshape(-1, V))
+    ref = _rowwise_rel(got[1].reshape(-1, V), f["sample_logits"][: 2 * s.n_codebooks])
+    print(f"refill after a retired frame: vs fresh engine {rel:.3e}, vs reference {ref:.3e}")
     assert rel < 1e-6 and ref < LOGIT_TOL
 
 

@@ -110,8 +110,10 @@ int sk_prefill_run(sk_engine* e);
  * of the engine's lazily grown buffers; a packed prefix that needs more
  * (about 600 tokens at the Qwen3-0.6B shape, 450 at 1.7B) is rejected with
  * SK_EINVAL -- sk_prefill_run takes any size.  Every call on one GPU shares
- * that scratch: calls that overlap on one GPU (two engines on two streams)
- * race.  Results are those of sk_prefill_run, bit for bit. */
+ * that scratch, so calls that overlapped on one GPU would race; the device
+ * order of engines (below, at sk_replay) makes the prefills of different
+ * engines take turns, and one engine's calls share its stream.  Results are
+ * those of sk_prefill_run, bit for bit. */
 #define SK_NOALLOC_SCRATCH_BYTES (32u << 20)
 int sk_prefill_run_noalloc(sk_engine* e);
 /* Continuous batching (no counterpart in the reference, which decodes one
@@ -174,10 +176,11 @@ int sk_step_frame(sk_engine* e, int32_t mask_eos_q0, const double* uniforms,
  * sk_step_frame), then replay `n` frames back to
  * back with no host synchronisation.  sk_read_codes copies codes of the
  * `n` most recent frames ([n][n_utts][Q]).
- * Frames of different engines on one device run one after another: when the
- * device's frames pass from one engine to another (sk_step_frame or
- * sk_replay), the new engine's stream first waits for the work queued on the
- * previous engine's stream.  An engine stepping alone pays nothing. */
+ * Frames and prefills of different engines on one device run one after
+ * another: when the device's work passes from one engine to another
+ * (sk_step_frame, sk_replay, the prefills), the new engine's stream first
+ * waits for the work queued on the previous engine's stream.  An engine
+ * working alone pays nothing. */
 int sk_queue_frames(sk_engine* e, int32_t n, const double* uniforms, const int32_t* mask_eos_q0);
 int sk_replay(sk_engine* e, int32_t n);
 int sk_read_codes(sk_engine* e, int32_t n, int64_t* codes_out);

@@ -1083,7 +1083,8 @@ extern "C" {
 const char* sk_last_error(void) { return last_error().c_str(); }
 
 // ---- frame order between engines on one device ------------------------------
-// Frames of different engines on one device run one after another.  The
+// Frames (and prefills) of different engines on one device run one after
+// another.  The
 // XCD-resident layers and the tagged split-K merge wait inside a launch for
 // other workgroups of the same launch, so all of its workgroups must be
 // resident at once; another engine's frame running beside it would hold CUs
@@ -1092,8 +1093,8 @@ const char* sk_last_error(void) { return last_error().c_str(); }
 // another, the new engine's stream first waits for everything the previous
 // engine had queued (an event recorded on that engine's stream at the
 // switch), so an engine that steps alone pays nothing.  The lock is held
-// while the frames are enqueued and while a graph is captured, so no event
-// is ever recorded on a stream that is capturing.
+// while frames or a prefill are enqueued and while a graph is captured, so
+// no event is ever recorded on a stream that is capturing.
 namespace {
 struct FrameOrder {
   std::mutex mu;
@@ -1456,17 +1457,24 @@ static int prefill_staged(sk_engine* e, bool all, bool noalloc) {
     SK_CHECK(ae == hipSuccess, SK_EHIP, "prefill buffers for %d tokens: %s", M, hipGetErrorString(ae));
     bufs = e->pf;
   }
-  SK_HIP(hipMemcpyAsync(e->plen, row_len.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  SK_HIP(hipMemcpyAsync(e->p_row_start, row_start.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  SK_HIP(hipMemcpyAsync(bufs.tok_row, tok_row.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  SK_HIP(hipMemcpyAsync(bufs.tok_pos, tok_pos.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
-  if (all) {
-    SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
-    SK_HIP(clear_split_tags(e));
-    SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
-    SK_HIP(hipMemsetAsync(e->prefix2, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
+  {
+    // in the device's order of engines, like frames: no other engine's frame
+    // runs beside the prefill, and prefills of different engines (which share
+    // the no-alloc scratch) take turns
+    std::lock_guard<std::mutex> lk(g_frame_order[e->device].mu);
+    SK_HIP(order_after_previous(e));
+    SK_HIP(hipMemcpyAsync(e->plen, row_len.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+    SK_HIP(hipMemcpyAsync(e->p_row_start, row_start.data(), R * sizeof(int), hipMemcpyHostToDevice, e->stream));
+    SK_HIP(hipMemcpyAsync(bufs.tok_row, tok_row.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
+    SK_HIP(hipMemcpyAsync(bufs.tok_pos, tok_pos.data(), M * sizeof(int), hipMemcpyHostToDevice, e->stream));
+    if (all) {
+      SK_HIP(hipMemsetAsync(e->fc, 0, sizeof(int), e->stream));
+      SK_HIP(clear_split_tags(e));
+      SK_HIP(hipMemsetAsync(e->prefix, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
+      SK_HIP(hipMemsetAsync(e->prefix2, 0, (size_t)R * e->c.d_model * sizeof(float), e->stream));
+    }
+    SK_HIP(enqueue_batched_prefill(e, M, max_len, bufs));
   }
-  SK_HIP(enqueue_batched_prefill(e, M, max_len, bufs));
   SK_HIP(hipStreamSynchronize(e->stream));
   for (int r = 0; r < R; ++r)
     if (e->staged[r]) { e->kv_host[r] = e->len_host[r]; e->active_host[r] = 1; e->staged[r] = 0; }

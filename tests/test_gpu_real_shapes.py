@@ -458,6 +458,46 @@ def test_two_engines_take_turns_on_one_gpu(hip_device):
     assert not np.array_equal(alone[0], alone[1])
 
 
+def test_prefill_beside_another_engines_queued_frames(hip_device):
+    """One engine's queued frames (no host sync) and a second engine's prefill,
+    capture and frames enqueued meanwhile: in the device order of engines the
+    prefill waits for the queued frames, and both engines' codes equal those
+    they decode alone."""
+    f, s, gen = load_golden("q06b_sampled")
+    w = synthetic_weights(s, int(f["seed"]), norm_gain_std=float(f["norm_gain_std"]),
+                          bias_std=float(f["bias_std"]))
+    text, uncond, prompt = _c3_inputs(f)
+    g = {k: gen[k] for k in ("cfg_scale", "temperature", "top_k", "top_p")}
+    n = 8
+    u = np.random.default_rng(13).random((n, s.n_codebooks))
+    mask = np.ones(n, np.int32)
+
+    def first():
+        e = _engine(s, w, hip_device, text, uncond, prompt, 260, **g)
+        e.queue_frames(u, mask)
+        return e
+
+    def second_codes(e):
+        return np.stack([e.step_frame(mask_eos_q0=True, uniforms=u[i]).numpy() for i in range(3)])
+
+    e = first()
+    e.replay(n)
+    alone_a = e.read_codes(n)
+    e.close()
+    e = _engine(s, w, hip_device, text, uncond, prompt[:100], 260, **g)
+    alone_b = second_codes(e)
+    e.close()
+    a = first()
+    a.replay(n)                                   # queued, not waited for
+    b = _engine(s, w, hip_device, text, uncond, prompt[:100], 260, **g)
+    got_b = second_codes(b)
+    got_a = a.read_codes(n)
+    a.close()
+    b.close()
+    np.testing.assert_array_equal(got_a, alone_a)
+    np.testing.assert_array_equal(got_b, alone_b)
+
+
 def test_xcd_layers_frame_with_retired_rows_then_prefill(hip_device):
     """The XCD-resident layers' residual accumulators across a retired
     utterance: an engine decodes one frame, retires its utterance, runs one

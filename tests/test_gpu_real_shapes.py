@@ -14,7 +14,8 @@ reference's vectors and the oracle.
   against the per-op layer kernels, at both shapes, and with more chunk slots
   than an XCD has workgroups.
 * Two engines with XCD-resident layers taking turns on one GPU (queued
-  replays on two streams, no host sync): codes equal each engine's alone.
+  replays on two streams, no host sync; one engine's prefill beside the
+  other's queued frames): codes equal each engine's alone.
 * The XCD-resident layers after a frame with the utterance retired, then a
   new prefill or a continuous-batching refill: equal to a fresh engine.
 * An untied classifier head bound through ``GraphFrameEngine(model=...)``.
